@@ -1,0 +1,303 @@
+"""Benchmark of the quantized-weight hot path on one MI355X.
+
+Step (the timed unit): one pass of BASELINE config 2 -- every Llama-3-8B
+projection of a decoder layer (q, k, v, o, gate, up, down) as a quantized
+matmul at M in {1, 4, 16, 32} activation rows, for Q4 and Q8 (group 64).
+Four distinct layer copies are cycled (Q4 + Q8 weights ~1.4 GB, far above
+the 256 MB MALL), so every call streams its weights from HBM.  `value` is
+the step's algorithmic bytes (packed codes + scales + biases + x + y) over
+its wall time: HBM GB/s of the whole job.
+
+Extra fields (same JSON line):
+  roofline      dominant kernel of the step, HIP-event timed per launch
+  kernels       per (bits, M) decode GEMV GB/s and % of 8 TB/s
+  prefill       config 3: qmm at M=2048, Q4, 4096->14336 and 14336->4096, TFLOP/s
+  gguf          config 4: block dequant of a 14336x4096 tensor, GB/s per type
+  cpu_baseline  the CPU restatement (oracle, OpenMP) on a bounded sample
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "mlx-llm_amd"))
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, published
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, published
+METRIC = "Q4/Q8 qmatmul GB/s & TFLOP/s (% roofline), Llama-3-8B proj shapes, 1 GPU"
+
+# (name, K, N): y[M, N] = x[M, K] . W[N, K]^T
+PROJ = [("q", 4096, 4096), ("k", 4096, 1024), ("v", 4096, 1024), ("o", 4096, 4096),
+        ("gate", 4096, 14336), ("up", 4096, 14336), ("down", 14336, 4096)]
+MS = (1, 4, 16, 32)
+BITS = (4, 8)
+GS = 64
+LAYERS = 4
+
+
+def qbytes(m, n, k, bits, gs=GS):
+    """Algorithmic bytes of one quantized matmul call."""
+    return n * k * bits // 8 + 2 * (n * k // gs) * 2 + m * k * 2 + m * n * 2
+
+
+def make_layers(torch, mlxq, bits, layers, seed):
+    g = torch.Generator(device="cuda")
+    out = []
+    for li in range(layers):
+        layer = {}
+        for pi, (name, k, n) in enumerate(PROJ):
+            g.manual_seed(seed + 1000 * li + pi)
+            w = (torch.randn((n, k), generator=g, device="cuda", dtype=torch.float32) * 0.02).to(torch.bfloat16)
+            layer[name] = mlxq.quantize(w, GS, bits)
+            del w
+        out.append(layer)
+    return out
+
+
+def bind_step(mlxq, weights, xs, ys):
+    """The step's launches as pre-bound calls, in order."""
+    calls = []
+    for bits in BITS:
+        for m in MS:
+            for layer in weights[bits]:
+                for name, k, n in PROJ:
+                    wq, s, b = layer[name]
+                    calls.append(mlxq.bind_qmatmul(xs[(m, k)], wq, s, b, GS, bits, out=ys[(m, n)]))
+    return calls
+
+
+def run_step(calls):
+    for c in calls:
+        c()
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--quick", action="store_true", help="skip prefill / gguf / cpu legs")
+    a = ap.parse_args(argv)
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only (no collectives, no sharding); "
+              "run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import torch
+
+    import mlxq
+
+    torch.manual_seed(0)
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    dev = torch.device("cuda:0")
+    weights = {bits: make_layers(torch, mlxq, bits, LAYERS, 0x5EED0000 + 100 * bits) for bits in BITS}
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0x5EED1000)
+    xs = {(m, k): torch.randn((m, k), generator=g, device=dev).to(torch.bfloat16)
+          for m in MS for k in {p[1] for p in PROJ}}
+    ys = {(m, n): torch.empty((m, n), device=dev, dtype=torch.bfloat16) for m in MS for n in {p[2] for p in PROJ}}
+    # workspace sized for the largest shape up front (no allocation in the timed region)
+    mlxq.workspace(max(mlxq.workspace_size(m, n, k, GS, bits) for m in MS for _, k, n in PROJ for bits in BITS), dev)
+    step_bytes = sum(LAYERS * qbytes(m, n, k, bits) for bits in BITS for m in MS for _, k, n in PROJ)
+    calls = bind_step(mlxq, weights, xs, ys)
+
+    # eager launches (host-bound for the small shapes) ...
+    for _ in range(a.warmup):
+        run_step(calls)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(a.steps):
+        run_step(calls)
+    torch.cuda.synchronize()
+    eager_ms = (time.perf_counter() - t0) * 1e3 / a.steps
+
+    # ... and the same step captured once as a HIP graph and replayed
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        run_step(calls)
+    for _ in range(a.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(a.steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    ms_per_step = dt * 1e3 / a.steps
+    value = step_bytes * a.steps / dt / 1e9
+
+    # ---- per-launch HIP-event timing: per (bits, M) and per kernel shape ----
+    reps = 5
+    per = {}
+    for bits in BITS:
+        for m in MS:
+            for name, k, n in PROJ:
+                evs = []
+                fns = [mlxq.bind_qmatmul(xs[(m, k)], *layer[name], GS, bits, out=ys[(m, n)])
+                       for layer in weights[bits]]
+                for r in range(reps):
+                    for fn in fns:
+                        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                        e0.record()
+                        fn()
+                        e1.record()
+                        evs.append((e0, e1))
+                torch.cuda.synchronize()
+                us = sum(e0.elapsed_time(e1) for e0, e1 in evs) * 1e3 / len(evs)
+                per[(bits, m, name)] = (us, qbytes(m, n, k, bits))
+    kernels = {}
+    for bits in BITS:
+        for m in MS:
+            tot_us = sum(per[(bits, m, nm)][0] for nm, _, _ in PROJ)
+            tot_b = sum(per[(bits, m, nm)][1] for nm, _, _ in PROJ)
+            gbs = tot_b / (tot_us * 1e-6) / 1e9
+            kernels[f"q{bits}_m{m}"] = {
+                "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 3),
+                "us_per_layer": round(tot_us, 2),
+                "by_proj_us": {nm: round(per[(bits, m, nm)][0], 2) for nm, _, _ in PROJ},
+            }
+    # dominant kernel class of the step: the (bits, M) decode GEMV with the most time
+    dom = max(kernels, key=lambda kk: kernels[kk]["us_per_layer"])
+    dom_bits, dom_m = int(dom[1]), int(dom.split("_m")[1])
+    launches = len(PROJ)
+    avg_us = kernels[dom]["us_per_layer"] / launches
+    avg_bytes = sum(per[(dom_bits, dom_m, nm)][1] for nm, _, _ in PROJ) / launches
+    achieved = avg_bytes / (avg_us * 1e-6) / 1e9
+    roofline = {"kernel": f"qmv_kernel<bits={dom_bits}, M={dom_m}> over the 7 projection shapes",
+                "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "avg_launch_us": round(avg_us, 3), "algorithmic_bytes_per_launch": int(avg_bytes)}
+    q4m1 = kernels["q4_m1"]
+
+    out = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16 activations, u4/u8 codes, f32 accumulate",
+        "data": "synthetic: seeded N(0,0.02) bf16 weights quantized on device, N(0,1) bf16 activations",
+        "eager_ms_per_step": round(eager_ms, 4),
+        "timing": "value = step bytes / wall time of HIP-graph replays of the step (barrier + synchronize "
+                  "around the timed replays); eager_ms_per_step = the same launches issued one by one",
+        "config": {"workload": "config 2 sweep: q,k,v,o,gate,up,down (Llama-3-8B) x M in {1,4,16,32} x {Q4,Q8} g64, "
+                               f"{LAYERS} distinct layer copies cycled",
+                   "group_size": GS, "bytes_per_step": step_bytes},
+        "roofline": roofline,
+        "headline_q4_m1": {"GB/s": q4m1["GB/s"], "frac_hbm": q4m1["frac_hbm"]},
+        "kernels": kernels,
+    }
+
+    if not a.quick:
+        out["prefill"] = bench_prefill(torch, mlxq)
+        out["gguf"] = bench_gguf(torch, mlxq)
+    if not a.quick and not a.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(torch, weights, xs, a.cpu_seconds)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def bench_prefill(torch, mlxq, iters=10):
+    """Config 3: M=2048 bf16 x Q4 g64 weights, gate/up (4096->14336) and down (14336->4096)."""
+    res = {}
+    g = torch.Generator(device="cuda")
+    for name, k, n in (("gate_up", 4096, 14336), ("down", 14336, 4096)):
+        g.manual_seed(0x5EED0300 + k)
+        w = (torch.randn((n, k), generator=g, device="cuda") * 0.02)
+        cols = torch.randperm(k, generator=torch.Generator().manual_seed(k))[: (k + 999) // 1000]
+        w[:, cols] *= 20  # 0.1% outlier input channels
+        wq, s, b = mlxq.quantize(w.to(torch.bfloat16), 64, 4)
+        x = torch.randn((2048, k), generator=g, device="cuda").to(torch.bfloat16)
+        y = torch.empty((2048, n), device="cuda", dtype=torch.bfloat16)
+        for _ in range(3):
+            mlxq.qmatmul(x, wq, s, b, 64, 4, out=y)
+        torch.cuda.synchronize()
+        evs = []
+        for _ in range(iters):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            mlxq.qmatmul(x, wq, s, b, 64, 4, out=y)
+            e1.record()
+            evs.append((e0, e1))
+        torch.cuda.synchronize()
+        us = sum(e0.elapsed_time(e1) for e0, e1 in evs) * 1e3 / iters
+        tf = 2.0 * 2048 * n * k / (us * 1e-6) / 1e12
+        res[name] = {"us": round(us, 1), "TFLOP/s": round(tf, 1), "frac_mfma_bf16": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)}
+        del w, wq, s, b, x, y
+    return res
+
+
+def bench_gguf(torch, mlxq, iters=10):
+    """Config 4: 14336x4096 tensor per type; synthetic blocks (random codes, finite f16 scales)."""
+    res = {}
+    n = 14336 * 4096
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0x5EED0400)
+    d_off = {"Q4_0": [0], "Q8_0": [0], "Q4_K": [0, 2], "Q6_K": [208], "IQ4_NL": [0], "IQ4_XS": [0]}
+    out32 = torch.empty(n, device="cuda", dtype=torch.float32)
+    out16 = torch.empty(n, device="cuda", dtype=torch.bfloat16)
+    for tname, offs in d_off.items():
+        tag = mlxq.GGUF_TAGS[tname]
+        be, bb = mlxq.gguf_block(tag)
+        nblk = n // be
+        raw = torch.randint(0, 256, (nblk, bb), generator=g, device="cuda", dtype=torch.uint8)
+        for o in offs:  # f16 scale ~ 2^-7 .. 2^-5, positive
+            raw[:, o] = torch.randint(0, 256, (nblk,), generator=g, device="cuda", dtype=torch.uint8)
+            raw[:, o + 1] = 0x20 + torch.randint(0, 8, (nblk,), generator=g, device="cuda", dtype=torch.uint8)
+        raw = raw.reshape(-1).contiguous()
+        entry = {}
+        for oname, o, ob in (("f32", out32, 4), ("bf16", out16, 2)):
+            mlxq.gguf_dequantize(tag, raw, n, out=o)
+            torch.cuda.synchronize()
+            evs = []
+            for _ in range(iters):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                mlxq.gguf_dequantize(tag, raw, n, out=o)
+                e1.record()
+                evs.append((e0, e1))
+            torch.cuda.synchronize()
+            us = sum(e0.elapsed_time(e1) for e0, e1 in evs) * 1e3 / iters
+            gbs = (raw.numel() + n * ob) / (us * 1e-6) / 1e9
+            entry[oname] = {"us": round(us, 1), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 3)}
+        res[tname] = entry
+        del raw
+    return res
+
+
+def cpu_baseline(torch, weights, xs, seconds):
+    """The oracle's OpenMP dequant-on-the-fly GEMV (a port of the reference's
+    CPU path) on the Q4 M=1 projections of one layer, repeated for ~`seconds`."""
+    import numpy as np
+
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle as orc
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
+    layer = weights[4][0]
+    host = {}
+    for name, k, n in PROJ:
+        wq, s, b = layer[name]
+        host[name] = (wq.cpu().numpy().view(np.uint32), s.cpu().view(torch.int16).numpy().view(np.uint16),
+                      b.cpu().view(torch.int16).numpy().view(np.uint16))
+    xh = {k: xs[(1, k)].cpu().view(torch.int16).numpy().view(np.uint16) for k in {p[1] for p in PROJ}}
+    nbytes, reps = 0, 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds or reps == 0:
+        for name, k, n in PROJ:
+            wq, s, b = host[name]
+            orc.qmatmul_f32(xh[k], wq, s, b, 64, 4, threads=threads)
+            nbytes += qbytes(1, n, k, 4)
+        reps += 1
+    dt = time.perf_counter() - t0
+    return {"value": round(nbytes / dt / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"Q4 g64 M=1, the 7 projections of one layer, {reps} passes in {dt:.1f} s "
+                      f"(oracle/baseline.c orc_qmatmul_f32, {threads} OpenMP threads)"}
+
+
+if __name__ == "__main__":
+    sys.exit(main())

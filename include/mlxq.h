@@ -1,0 +1,143 @@
+/*
+ * mlxq -- MI355X (gfx950) quantized-weight hot path, C ABI.
+ *
+ * Drop-in boundary for the device arithmetic that SceneWorks/mlx-llm reaches
+ * through MLX (group-wise affine quantize / dequantize / quantized_matmul) and
+ * for its pure-Rust GGUF block dequantizer.  Each entry point names the
+ * reference call it replaces (paths relative to the reference crate root).
+ *
+ * Conventions
+ *   - All tensor pointers are DEVICE pointers owned by the caller; the library
+ *     allocates nothing on these paths.  Work is enqueued asynchronously on
+ *     `stream` (a hipStream_t; NULL = the default stream); the caller
+ *     synchronizes before reading results.
+ *   - Row-major layouts.  Weights use the Hugging Face `[out, in]` layout:
+ *     W is [N, K]; x is [M, K]; y is [M, N] (quantized_matmul transpose=true).
+ *   - Packed codes: wq is uint32 [N, K*bits/32]; element k of a row sits in
+ *     word k/(32/bits) at bits [(k%(32/bits))*bits, +bits) (LSB first).
+ *     scales/biases are [N, K/group_size] in the weight dtype.
+ *   - bf16 / f16 values are passed as their 16-bit patterns.
+ *   - Every function returns an mlxq_status.  On failure, mlxq_last_error()
+ *     returns a message for the calling thread.
+ *   - Calls are reentrant per stream.  The qmatmul workspace (below) must not
+ *     be shared by calls that can run concurrently.
+ */
+#ifndef MLXQ_H
+#define MLXQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes.  The reference maps errors to crate::error::Error
+ * (src/error.rs:11-42): MLXQ_ERR_UNSUPPORTED -> Error::Unsupported,
+ * MLXQ_ERR_DEVICE -> Error::Mlx, everything else -> Error::Msg. */
+typedef enum {
+  MLXQ_OK = 0,
+  MLXQ_ERR_INVALID = 1,      /* null pointer, negative size, bad enum value */
+  MLXQ_ERR_SHAPE = 2,        /* K % group_size != 0, n % block_elems != 0  */
+  MLXQ_ERR_UNSUPPORTED = 3,  /* bits / group_size / GGUF tag / dtype       */
+  MLXQ_ERR_SHORT_BUFFER = 4, /* GGUF data shorter than the blocks need     */
+  MLXQ_ERR_WORKSPACE = 5,    /* qmatmul workspace missing or too small     */
+  MLXQ_ERR_DEVICE = 6        /* HIP runtime / launch failure               */
+} mlxq_status;
+
+/* Element types for the `dtype` arguments. */
+typedef enum {
+  MLXQ_F32 = 0,
+  MLXQ_F16 = 1,
+  MLXQ_BF16 = 2
+} mlxq_dtype;
+
+/* Kernel choice for mlxq_qmatmul_algo. */
+typedef enum {
+  MLXQ_ALGO_AUTO = 0, /* qmv for M <= 32, qmm above (what mlxq_qmatmul does) */
+  MLXQ_ALGO_QMV = 1,  /* decode GEMV, any M <= 32                             */
+  MLXQ_ALGO_QMM = 2   /* LDS-dequant bf16 MFMA GEMM, any M                    */
+} mlxq_algo;
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* mlxq_last_error(void);
+/* Library version string. */
+const char* mlxq_version(void);
+
+/* ------------------------------------------------------------------ */
+/* Affine group-wise quantization                                      */
+/* ------------------------------------------------------------------ */
+
+/* Replaces mlx_rs::ops::quantize(w, group_size, bits) reached from
+ * QuantizedLinear::quantize (src/primitives/quant.rs:38-53, call at :44),
+ * itself called by Projection::load_with_bias (src/primitives/projection.rs:57-71),
+ * quantize-on-load (src/models/llama.rs:97) and the snapshot requant
+ * (src/snapshot.rs:100-107).
+ * w: [rows, cols] in `dtype` (MLXQ_F32 or MLXQ_BF16); scales/biases are
+ * written in the same dtype.  bits in {4, 8}; group_size in {32, 64, 128}. */
+int mlxq_quantize(const void* w, int dtype, int64_t rows, int64_t cols,
+                  int group_size, int bits, uint32_t* wq, void* scales,
+                  void* biases, void* stream);
+
+/* Replaces mlx_rs::ops::dequantize reached from
+ * QuantizedLinear::dequantize_weight (src/primitives/quant.rs:73-81).
+ * out[r, c] = scale * q + bias, computed in f32 and stored in `dtype`. */
+int mlxq_dequantize(const uint32_t* wq, const void* scales, const void* biases,
+                    int dtype, int64_t rows, int64_t cols, int group_size,
+                    int bits, void* out, void* stream);
+
+/* ------------------------------------------------------------------ */
+/* Quantized matmul                                                    */
+/* ------------------------------------------------------------------ */
+
+/* Bytes of device workspace mlxq_qmatmul needs for this shape (0 possible).
+ * The workspace must be zero-filled once before its first use; every call
+ * leaves it zero-filled again on completion. */
+int mlxq_qmatmul_workspace_size(int64_t M, int64_t N, int64_t K,
+                                int group_size, int bits, size_t* bytes);
+
+/* Replaces mlx_rs::ops::quantized_matmul(x, w, scales, Some(biases),
+ * transpose=true, group_size, bits) plus the optional dense bias add, i.e.
+ * QuantizedLinear::forward (src/primitives/quant.rs:56-70), reached from
+ * Projection::forward (src/primitives/projection.rs:93-98).
+ * y[m, n] = sum_k x[m, k] * (scale*q + bias)[n, k]  (+ bias_vec[n])
+ * x, scales, biases, bias_vec (nullable, [N]) and y are bf16; accumulation is
+ * f32.  M >= 1 rows of activations (decode: M = batch; prefill: M = tokens). */
+int mlxq_qmatmul(const void* x, int64_t M, const uint32_t* wq,
+                 const void* scales, const void* biases, const void* bias_vec,
+                 int64_t N, int64_t K, int group_size, int bits, void* y,
+                 void* workspace, size_t workspace_bytes, void* stream);
+
+/* mlxq_qmatmul with an explicit kernel choice (mlxq_algo).  MLX makes the
+ * same qmv/qmm choice internally from M. */
+int mlxq_qmatmul_algo(const void* x, int64_t M, const uint32_t* wq,
+                      const void* scales, const void* biases,
+                      const void* bias_vec, int64_t N, int64_t K,
+                      int group_size, int bits, void* y, void* workspace,
+                      size_t workspace_bytes, int algo, void* stream);
+
+/* ------------------------------------------------------------------ */
+/* GGUF block dequantization                                           */
+/* ------------------------------------------------------------------ */
+
+/* GgmlType::from_tag + GgmlType::block (src/gguf/dequant.rs:85-141):
+ * (elements per block, bytes per block) for a GGUF type tag.  Host only. */
+int mlxq_gguf_block(uint32_t tag, int64_t* elems, int64_t* bytes);
+
+/* tensor_byte_len (src/gguf/dequant.rs:144-153).  Host only. */
+int mlxq_gguf_tensor_byte_len(uint32_t tag, int64_t n, int64_t* bytes);
+
+/* Replaces gguf::dequant::dequantize(tag, data, n) (src/gguf/dequant.rs:156-211),
+ * called by gguf::convert (src/gguf/convert.rs:132).  data: device bytes of
+ * n/elems blocks (data_len >= the blocks' bytes); out: n values in out_dtype
+ * (MLXQ_F32: bit-exact with the reference; MLXQ_BF16: that f32 value rounded
+ * to nearest-even, as convert.rs:156 does).  Device tags: F32, F16, BF16,
+ * Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS.
+ * IQ1/IQ2/IQ3 grid types return MLXQ_ERR_UNSUPPORTED. */
+int mlxq_gguf_dequantize(uint32_t tag, const void* data, int64_t data_len,
+                         int64_t n, int out_dtype, void* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MLXQ_H */

@@ -1,0 +1,91 @@
+"""Build libmlxq.so (gfx950 HIP kernels + C ABI + C++ host API) in-tree.
+
+Usage: python mlx-llm_amd/build.py [--jobs N] [--verbose]
+
+Every HIP source is compiled with hipcc for gfx950 only.  Packed FP32 VALU
+ops are disabled (`-Xclang -target-feature -Xclang -packed-fp32-ops`).
+Sources whose results must be bit-identical with the CPU restatement
+(GGUF dequant, affine quantize) are compiled with -ffp-contract=off.
+"""
+from __future__ import annotations
+
+import argparse
+import concurrent.futures as cf
+import os
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+HOST = PKG / "host"
+OBJ = PKG / "_build"
+LIB = PKG / "libmlxq.so"
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+
+COMMON = [
+    "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", "-Wno-unused-result", "-Wno-unused-command-line-argument",
+    f"-I{ROOT / 'include'}", f"-I{CSRC}",
+]
+NO_CONTRACT = {"gguf.hip", "affine.hip"}
+
+
+def sources() -> list[Path]:
+    srcs = sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
+    if HOST.is_dir():
+        srcs += sorted(HOST.glob("*.cpp"))
+    return srcs
+
+
+def compile_one(src: Path, verbose: bool) -> Path:
+    obj = OBJ / (src.parent.name + "_" + src.name + ".o")
+    cmd = [HIPCC, *COMMON]
+    if src.name in NO_CONTRACT:
+        cmd.append("-ffp-contract=off")
+    if src.suffix == ".cpp":
+        cmd += ["-x", "hip"]  # host files include hip_runtime for stream types
+    cmd += ["-c", str(src), "-o", str(obj)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {src.name}:\n{r.stdout}\n{r.stderr}")
+    # hipcc's host pass warns that it does not know packed-fp32-ops: harmless.
+    errs = [ln for ln in r.stderr.splitlines() if "warning" in ln and "packed-fp32-ops" not in ln]
+    if errs and verbose:
+        print("\n".join(errs))
+    return obj
+
+
+def build(jobs: int = 8, verbose: bool = False) -> Path:
+    OBJ.mkdir(exist_ok=True)
+    srcs = sources()
+    with cf.ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
+        objs = list(ex.map(lambda s: compile_one(s, verbose), srcs))
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", str(tmp), *map(str, objs)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, LIB)
+    return LIB
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--jobs", type=int, default=min(8, os.cpu_count() or 1))
+    ap.add_argument("--verbose", action="store_true")
+    a = ap.parse_args(argv)
+    lib = build(a.jobs, a.verbose)
+    print(f"built {lib}")
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,78 @@
+// Host-side C ABI pieces that launch nothing: error strings, version, GGUF
+// block geometry.
+#include <stdint.h>
+
+#include <string>
+
+#include "common.hpp"
+
+namespace mlxq {
+
+static thread_local std::string g_last_error;
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+void clear_error() { g_last_error.clear(); }
+int fail(int status, const std::string& msg) {
+  g_last_error = msg;
+  return status;
+}
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    return fail(MLXQ_ERR_DEVICE, std::string(what) + ": " + hipGetErrorString(e));
+  return MLXQ_OK;
+}
+
+}  // namespace mlxq
+
+using namespace mlxq;
+
+extern "C" const char* mlxq_last_error(void) { return g_last_error.c_str(); }
+
+extern "C" const char* mlxq_version(void) { return "mlxq 0.1.0 (gfx950)"; }
+
+// GgmlType::from_tag + block() (src/gguf/dequant.rs:85-141).  The table is
+// the GGUF/ggml on-disk format, so it is necessarily identical.
+extern "C" int mlxq_gguf_block(uint32_t tag, int64_t* elems, int64_t* bytes) {
+  int64_t e, b;
+  switch (tag) {
+    case 0: e = 1; b = 4; break;            // F32
+    case 1: case 30: e = 1; b = 2; break;   // F16, BF16
+    case 2: e = 32; b = 18; break;          // Q4_0
+    case 3: e = 32; b = 20; break;          // Q4_1
+    case 6: e = 32; b = 22; break;          // Q5_0
+    case 7: e = 32; b = 24; break;          // Q5_1
+    case 8: e = 32; b = 34; break;          // Q8_0
+    case 10: e = 256; b = 84; break;        // Q2_K
+    case 11: e = 256; b = 110; break;       // Q3_K
+    case 12: e = 256; b = 144; break;       // Q4_K
+    case 13: e = 256; b = 176; break;       // Q5_K
+    case 14: e = 256; b = 210; break;       // Q6_K
+    case 16: e = 256; b = 66; break;        // IQ2_XXS
+    case 17: e = 256; b = 74; break;        // IQ2_XS
+    case 18: e = 256; b = 98; break;        // IQ3_XXS
+    case 19: e = 256; b = 50; break;        // IQ1_S
+    case 20: e = 32; b = 18; break;         // IQ4_NL
+    case 21: e = 256; b = 110; break;       // IQ3_S
+    case 22: e = 256; b = 82; break;        // IQ2_S
+    case 23: e = 256; b = 136; break;       // IQ4_XS
+    case 29: e = 256; b = 56; break;        // IQ1_M
+    default:
+      return fail(MLXQ_ERR_UNSUPPORTED, "unsupported: GGUF type tag " + std::to_string(tag));
+  }
+  if (elems) *elems = e;
+  if (bytes) *bytes = b;
+  return MLXQ_OK;
+}
+
+extern "C" int mlxq_gguf_tensor_byte_len(uint32_t tag, int64_t n, int64_t* bytes) {
+  int64_t be = 0, bb = 0;
+  int rc = mlxq_gguf_block(tag, &be, &bb);
+  if (rc) return rc;
+  if (!bytes) return fail(MLXQ_ERR_INVALID, "gguf: null output pointer");
+  if (n < 0 || n % be)
+    return fail(MLXQ_ERR_SHAPE, "gguf: " + std::to_string(n) + " elements not a multiple of " +
+                                    std::to_string(be) + " for tag " + std::to_string(tag));
+  *bytes = (n / be) * bb;
+  return MLXQ_OK;
+}

@@ -1,0 +1,52 @@
+// Shared host/device helpers for the mlxq gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/mlxq.h"
+
+namespace mlxq {
+
+// ---- error reporting (thread-local message behind mlxq_last_error) ----
+void set_error(const std::string& msg);
+void clear_error();
+int fail(int status, const std::string& msg);
+// Check the launch that was just enqueued.
+int check_launch(const char* what);
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ---- device scalar conversions (bit-level, independent of FP modes) ----
+__device__ __forceinline__ float bits_to_f32(uint32_t u) { return __uint_as_float(u); }
+
+// Exact binary16 -> binary32, NaNs quieted with payload kept (the conversion
+// `half::f16::to_f32` performs, used by src/gguf/dequant.rs:222-225).
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+  uint32_t sign = (h & 0x8000u) << 16;
+  uint32_t exp = (h >> 10) & 0x1Fu;
+  uint32_t man = h & 0x3FFu;
+  if (exp == 0x1Fu) return bits_to_f32(sign | 0x7F800000u | (man ? (0x400000u | (man << 13)) : 0u));
+  if (exp == 0u) {
+    // subnormal (or zero): man * 2^-24 is exact in f32
+    float v = static_cast<float>(man) * 5.9604644775390625e-08f;
+    return sign ? -v : v;
+  }
+  return bits_to_f32(sign | ((exp + 112u) << 23) | (man << 13));
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return bits_to_f32(b << 16); }
+
+// f32 -> bf16 round-to-nearest-even; NaN stays NaN (quiet bit set).
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (u >> 16) | 0x40u;
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+__host__ __device__ __forceinline__ int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace mlxq

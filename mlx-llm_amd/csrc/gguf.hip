@@ -1,0 +1,361 @@
+// GGUF block dequantization for gfx950.
+//
+// Reference: src/gguf/dequant.rs:156-211 (dispatcher) and the per-type block
+// decoders it calls (:228-497).  The reference walks blocks one at a time on
+// one host thread; here a workgroup stages a chunk of whole blocks into LDS
+// with wide coalesced loads, then every thread decodes VEC consecutive output
+// elements straight from LDS and writes them with one 16-byte store.
+//
+// Bit-exactness: each output element is computed with exactly the IEEE f32
+// operations, operand order and roundings the reference uses for it (the
+// per-element formulas below are the reference's block loops solved for one
+// element).  This file is compiled with -ffp-contract=off so no mul+add/sub is
+// fused, and f16 scales are decoded with integer bit operations.
+#include <hip/hip_runtime.h>
+
+#include <string>
+
+#include "common.hpp"
+
+namespace mlxq {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kVec = 8;                          // outputs per thread per pass
+constexpr int kChunkElems = kThreads * kVec;     // 2048 elements per chunk
+
+__constant__ int8_t kIq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
+                                  1,    13,   25,  38,  53,  69,  89,  113};
+
+__device__ __forceinline__ float rd_f16(const uint8_t* b, int i) {
+  return f16_bits_to_f32(static_cast<uint32_t>(b[i]) | (static_cast<uint32_t>(b[i + 1]) << 8));
+}
+__device__ __forceinline__ uint32_t rd_u32(const uint8_t* b) {
+  return static_cast<uint32_t>(b[0]) | (static_cast<uint32_t>(b[1]) << 8) |
+         (static_cast<uint32_t>(b[2]) << 16) | (static_cast<uint32_t>(b[3]) << 24);
+}
+
+// get_scale_min_k4 (dequant.rs:375-383)
+__device__ __forceinline__ void scale_min_k4(int j, const uint8_t* q, uint32_t& d, uint32_t& m) {
+  if (j < 4) {
+    d = q[j] & 63u;
+    m = q[j + 4] & 63u;
+  } else {
+    d = (q[j + 4] & 0x0Fu) | ((q[j - 4] >> 6) << 4);
+    m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+  }
+}
+
+// One element j of a block at b (LDS).  Tag is a template constant.
+template <int TAG>
+__device__ __forceinline__ float decode(const uint8_t* b, int j);
+
+// Q4_0 (dequant.rs:228-237): y[j]=(lo-8)*d, y[j+16]=(hi-8)*d
+template <>
+__device__ __forceinline__ float decode<2>(const uint8_t* b, int j) {
+  float d = rd_f16(b, 0);
+  uint32_t byte = b[2 + (j & 15)];
+  int q = static_cast<int>(j < 16 ? (byte & 0xFu) : (byte >> 4)) - 8;
+  return static_cast<float>(q) * d;
+}
+// Q4_1 (dequant.rs:239-247): q*d + m
+template <>
+__device__ __forceinline__ float decode<3>(const uint8_t* b, int j) {
+  float d = rd_f16(b, 0), m = rd_f16(b, 2);
+  uint32_t byte = b[4 + (j & 15)];
+  uint32_t q = j < 16 ? (byte & 0xFu) : (byte >> 4);
+  return static_cast<float>(q) * d + m;
+}
+// Q5_0 (dequant.rs:249-261)
+template <>
+__device__ __forceinline__ float decode<6>(const uint8_t* b, int j) {
+  float d = rd_f16(b, 0);
+  uint32_t qh = rd_u32(b + 2);
+  int jj = j & 15;
+  uint32_t byte = b[6 + jj];
+  uint32_t x;
+  if (j < 16) x = (byte & 0xFu) | (((qh >> jj) << 4) & 0x10u);
+  else x = (byte >> 4) | ((qh >> (jj + 12)) & 0x10u);
+  return static_cast<float>(static_cast<int>(x) - 16) * d;
+}
+// Q5_1 (dequant.rs:263-276)
+template <>
+__device__ __forceinline__ float decode<7>(const uint8_t* b, int j) {
+  float d = rd_f16(b, 0), m = rd_f16(b, 2);
+  uint32_t qh = rd_u32(b + 4);
+  int jj = j & 15;
+  uint32_t byte = b[8 + jj];
+  uint32_t x;
+  if (j < 16) x = (byte & 0xFu) | (((qh >> jj) << 4) & 0x10u);
+  else x = (byte >> 4) | ((qh >> (jj + 12)) & 0x10u);
+  return static_cast<float>(x) * d + m;
+}
+// Q8_0 (dequant.rs:278-284)
+template <>
+__device__ __forceinline__ float decode<8>(const uint8_t* b, int j) {
+  float d = rd_f16(b, 0);
+  return static_cast<float>(static_cast<int8_t>(b[2 + j])) * d;
+}
+// Q2_K (dequant.rs:288-318): element j -> half h (128), shift round r (32),
+// 16-lane half l2/16 selecting scales[8h + 2r + l2/16].
+template <>
+__device__ __forceinline__ float decode<10>(const uint8_t* b, int j) {
+  int h = j >> 7, r = (j >> 5) & 3, l2 = j & 31;
+  uint32_t sc = b[8 * h + 2 * r + (l2 >> 4)];
+  float d = rd_f16(b, 80), dmin = rd_f16(b, 82);
+  float dl = d * static_cast<float>(sc & 0xFu);
+  float ml = dmin * static_cast<float>(sc >> 4);
+  uint32_t qb = b[16 + 32 * h + l2];
+  return dl * static_cast<float>((qb >> (2 * r)) & 3u) - ml;
+}
+// Q3_K (dequant.rs:320-371)
+template <>
+__device__ __forceinline__ float decode<11>(const uint8_t* b, int j) {
+  const uint32_t K1 = 0x03030303u, K2 = 0x0f0f0f0fu;
+  int h = j >> 7, r = (j >> 5) & 3, l2 = j & 31;
+  int is = 8 * h + 2 * r + (l2 >> 4);
+  uint32_t a0 = rd_u32(b + 96), a1 = rd_u32(b + 100), tmp = rd_u32(b + 104);
+  uint32_t aux;
+  switch (is >> 2) {
+    case 0: aux = (a0 & K2) | ((tmp & K1) << 4); break;
+    case 1: aux = (a1 & K2) | (((tmp >> 2) & K1) << 4); break;
+    case 2: aux = ((a0 >> 4) & K2) | (((tmp >> 4) & K1) << 4); break;
+    default: aux = ((a1 >> 4) & K2) | (((tmp >> 6) & K1) << 4); break;
+  }
+  int sc = static_cast<int8_t>((aux >> (8 * (is & 3))) & 0xFFu);
+  float d_all = rd_f16(b, 108);
+  float dl = d_all * static_cast<float>(sc - 32);
+  uint32_t m = 1u << (4 * h + r);
+  int hbit = (b[l2] & m) ? 0 : 4;
+  uint32_t qb = b[32 + 32 * h + l2];
+  return dl * static_cast<float>(static_cast<int>((qb >> (2 * r)) & 3u) - hbit);
+}
+// Q4_K (dequant.rs:385-410)
+template <>
+__device__ __forceinline__ float decode<12>(const uint8_t* b, int j) {
+  int c = j >> 6, hi = (j >> 5) & 1, l = j & 31;
+  uint32_t sc, m;
+  scale_min_k4(2 * c + hi, b + 4, sc, m);
+  float d = rd_f16(b, 0), dmin = rd_f16(b, 2);
+  float d1 = d * static_cast<float>(sc);
+  float m1 = dmin * static_cast<float>(m);
+  uint32_t qb = b[16 + 32 * c + l];
+  uint32_t q = hi ? (qb >> 4) : (qb & 0xFu);
+  return d1 * static_cast<float>(q) - m1;
+}
+// Q5_K (dequant.rs:412-444)
+template <>
+__device__ __forceinline__ float decode<13>(const uint8_t* b, int j) {
+  int c = j >> 6, hi = (j >> 5) & 1, l = j & 31;
+  uint32_t sc, m;
+  scale_min_k4(2 * c + hi, b + 4, sc, m);
+  float d = rd_f16(b, 0), dmin = rd_f16(b, 2);
+  float d1 = d * static_cast<float>(sc);
+  float m1 = dmin * static_cast<float>(m);
+  uint32_t u = (hi ? 2u : 1u) << (2 * c);
+  int hib = (b[16 + l] & u) ? 16 : 0;
+  uint32_t qb = b[48 + 32 * c + l];
+  int q = static_cast<int>(hi ? (qb >> 4) : (qb & 0xFu)) + hib;
+  return d1 * static_cast<float>(q) - m1;
+}
+// Q6_K (dequant.rs:446-468): (d * scale) * q, left to right
+template <>
+__device__ __forceinline__ float decode<14>(const uint8_t* b, int j) {
+  int idx = j >> 7, t = (j >> 5) & 3, l = j & 31;
+  const uint8_t* qlp = b + 64 * idx;
+  const uint8_t* qhp = b + 128 + 32 * idx;
+  uint32_t lo = (t & 1) ? qlp[l + 32] : qlp[l];
+  lo = (t & 2) ? (lo >> 4) : (lo & 0xFu);
+  uint32_t hb = (qhp[l] >> (2 * t)) & 3u;
+  int q = static_cast<int>(static_cast<int8_t>(lo | (hb << 4))) - 32;
+  int sc = static_cast<int8_t>(b[192 + 8 * idx + (l >> 4) + 2 * t]);
+  float d = rd_f16(b, 208);
+  return d * static_cast<float>(sc) * static_cast<float>(q);
+}
+// IQ4_NL (dequant.rs:472-479)
+template <>
+__device__ __forceinline__ float decode<20>(const uint8_t* b, int j) {
+  float d = rd_f16(b, 0);
+  uint32_t byte = b[2 + (j & 15)];
+  uint32_t q = j < 16 ? (byte & 0xFu) : (byte >> 4);
+  return d * static_cast<float>(kIq4nl[q]);
+}
+// IQ4_XS (dequant.rs:481-497)
+template <>
+__device__ __forceinline__ float decode<23>(const uint8_t* b, int j) {
+  int ib = j >> 5, jj = j & 31;
+  float d = rd_f16(b, 0);
+  uint32_t sh = static_cast<uint32_t>(b[2]) | (static_cast<uint32_t>(b[3]) << 8);
+  int ls = static_cast<int>((b[4 + (ib >> 1)] >> (4 * (ib & 1))) & 0xFu) |
+           static_cast<int>(((sh >> (2 * ib)) & 3u) << 4);
+  float dl = d * static_cast<float>(ls - 32);
+  uint32_t byte = b[8 + 16 * ib + (jj & 15)];
+  uint32_t q = jj < 16 ? (byte & 0xFu) : (byte >> 4);
+  return dl * static_cast<float>(kIq4nl[q]);
+}
+
+template <int TAG> struct Geo;
+template <> struct Geo<2> { static constexpr int E = 32, B = 18; };
+template <> struct Geo<3> { static constexpr int E = 32, B = 20; };
+template <> struct Geo<6> { static constexpr int E = 32, B = 22; };
+template <> struct Geo<7> { static constexpr int E = 32, B = 24; };
+template <> struct Geo<8> { static constexpr int E = 32, B = 34; };
+template <> struct Geo<10> { static constexpr int E = 256, B = 84; };
+template <> struct Geo<11> { static constexpr int E = 256, B = 110; };
+template <> struct Geo<12> { static constexpr int E = 256, B = 144; };
+template <> struct Geo<13> { static constexpr int E = 256, B = 176; };
+template <> struct Geo<14> { static constexpr int E = 256, B = 210; };
+template <> struct Geo<20> { static constexpr int E = 32, B = 18; };
+template <> struct Geo<23> { static constexpr int E = 256, B = 136; };
+
+template <bool BF16OUT>
+__device__ __forceinline__ void store_vec(void* out, int64_t e, const float (&v)[kVec]) {
+  if constexpr (BF16OUT) {
+    uint4 p;
+    p.x = f32_to_bf16_bits(v[0]) | (f32_to_bf16_bits(v[1]) << 16);
+    p.y = f32_to_bf16_bits(v[2]) | (f32_to_bf16_bits(v[3]) << 16);
+    p.z = f32_to_bf16_bits(v[4]) | (f32_to_bf16_bits(v[5]) << 16);
+    p.w = f32_to_bf16_bits(v[6]) | (f32_to_bf16_bits(v[7]) << 16);
+    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(out) + e) = p;
+  } else {
+    float4* o = reinterpret_cast<float4*>(static_cast<float*>(out) + e);
+    o[0] = make_float4(v[0], v[1], v[2], v[3]);
+    o[1] = make_float4(v[4], v[5], v[6], v[7]);
+  }
+}
+
+// One workgroup per chunk of kChunkElems elements (a whole number of blocks).
+// Chunk bytes are a multiple of 16 for every tag, so with a 16-byte aligned
+// base every chunk start is 16-byte aligned and staged with uint4 loads.
+template <int TAG, bool BF16OUT, bool ALIGNED16>
+__global__ __launch_bounds__(kThreads) void gguf_dequant_kernel(const uint8_t* __restrict__ data,
+                                                                 int64_t nblocks, void* __restrict__ out) {
+  constexpr int E = Geo<TAG>::E, B = Geo<TAG>::B;
+  constexpr int BPC = kChunkElems / E;         // blocks per chunk
+  constexpr int CB = BPC * B;                  // chunk bytes
+  static_assert(CB % 16 == 0, "chunk bytes must be a multiple of 16");
+  __shared__ __align__(16) uint8_t lds[CB];
+
+  const int64_t chunk = blockIdx.x;
+  const int64_t blk0 = chunk * BPC;
+  const int nb = static_cast<int>(min<int64_t>(BPC, nblocks - blk0));
+  const int bytes = nb * B;
+  const uint8_t* src = data + blk0 * B;
+  const int tid = threadIdx.x;
+
+  if constexpr (ALIGNED16) {
+    const int n16 = bytes >> 4;  // whole uint4s (bytes is a multiple of 2 at least)
+    for (int i = tid; i < n16; i += kThreads)
+      reinterpret_cast<uint4*>(lds)[i] = reinterpret_cast<const uint4*>(src)[i];
+    for (int i = (n16 << 4) + tid; i < bytes; i += kThreads) lds[i] = src[i];
+  } else {
+    for (int i = tid; i < bytes; i += kThreads) lds[i] = src[i];
+  }
+  __syncthreads();
+
+  const int e0 = tid * kVec;  // element within the chunk
+  if (e0 >= nb * E) return;
+  float v[kVec];
+#pragma unroll
+  for (int i = 0; i < kVec; i++) {
+    int e = e0 + i;
+    v[i] = decode<TAG>(lds + (e / E) * B, e % E);
+  }
+  store_vec<BF16OUT>(out, chunk * kChunkElems + e0, v);
+}
+
+// F32 / F16 / BF16 pass-through (dequant.rs:174-188): one element per thread.
+template <int TAG, bool BF16OUT>
+__global__ __launch_bounds__(kThreads) void gguf_float_kernel(const uint8_t* __restrict__ data, int64_t n,
+                                                               void* __restrict__ out) {
+  int64_t e = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (e >= n) return;
+  float v;
+  if (TAG == 0) {
+    v = bits_to_f32(rd_u32(data + 4 * e));
+  } else {
+    uint32_t h = static_cast<uint32_t>(data[2 * e]) | (static_cast<uint32_t>(data[2 * e + 1]) << 8);
+    v = TAG == 1 ? f16_bits_to_f32(h) : bf16_bits_to_f32(h);
+  }
+  if constexpr (BF16OUT) static_cast<uint16_t*>(out)[e] = static_cast<uint16_t>(f32_to_bf16_bits(v));
+  else static_cast<float*>(out)[e] = v;
+}
+
+template <int TAG, bool BF16OUT>
+void launch_blocks(const uint8_t* data, int64_t nblocks, void* out, hipStream_t st) {
+  constexpr int E = Geo<TAG>::E;
+  int64_t chunks = ceil_div(nblocks * E, kChunkElems);
+  if (chunks == 0) return;
+  bool aligned = (reinterpret_cast<uintptr_t>(data) & 15u) == 0;
+  if (aligned)
+    hipLaunchKernelGGL((gguf_dequant_kernel<TAG, BF16OUT, true>), dim3(chunks), dim3(kThreads), 0, st, data,
+                       nblocks, out);
+  else
+    hipLaunchKernelGGL((gguf_dequant_kernel<TAG, BF16OUT, false>), dim3(chunks), dim3(kThreads), 0, st, data,
+                       nblocks, out);
+}
+
+template <int TAG, bool BF16OUT>
+void launch_float(const uint8_t* data, int64_t n, void* out, hipStream_t st) {
+  int64_t grid = ceil_div(n, static_cast<int64_t>(kThreads));
+  if (grid == 0) return;
+  hipLaunchKernelGGL((gguf_float_kernel<TAG, BF16OUT>), dim3(grid), dim3(kThreads), 0, st, data, n, out);
+}
+
+template <bool BF16OUT>
+int dispatch(uint32_t tag, const uint8_t* d, int64_t nblocks, int64_t n, void* out, hipStream_t st) {
+  switch (tag) {
+    case 0: launch_float<0, BF16OUT>(d, n, out, st); break;
+    case 1: launch_float<1, BF16OUT>(d, n, out, st); break;
+    case 30: launch_float<30, BF16OUT>(d, n, out, st); break;
+    case 2: launch_blocks<2, BF16OUT>(d, nblocks, out, st); break;
+    case 3: launch_blocks<3, BF16OUT>(d, nblocks, out, st); break;
+    case 6: launch_blocks<6, BF16OUT>(d, nblocks, out, st); break;
+    case 7: launch_blocks<7, BF16OUT>(d, nblocks, out, st); break;
+    case 8: launch_blocks<8, BF16OUT>(d, nblocks, out, st); break;
+    case 10: launch_blocks<10, BF16OUT>(d, nblocks, out, st); break;
+    case 11: launch_blocks<11, BF16OUT>(d, nblocks, out, st); break;
+    case 12: launch_blocks<12, BF16OUT>(d, nblocks, out, st); break;
+    case 13: launch_blocks<13, BF16OUT>(d, nblocks, out, st); break;
+    case 14: launch_blocks<14, BF16OUT>(d, nblocks, out, st); break;
+    case 20: launch_blocks<20, BF16OUT>(d, nblocks, out, st); break;
+    case 23: launch_blocks<23, BF16OUT>(d, nblocks, out, st); break;
+    default:
+      return fail(MLXQ_ERR_UNSUPPORTED,
+                  "unsupported: GGUF type tag " + std::to_string(tag) + " has no device dequantizer");
+  }
+  return check_launch("gguf_dequantize");
+}
+
+}  // namespace
+}  // namespace mlxq
+
+using namespace mlxq;
+
+extern "C" int mlxq_gguf_dequantize(uint32_t tag, const void* data, int64_t data_len, int64_t n,
+                                    int out_dtype, void* out, void* stream) {
+  clear_error();
+  int64_t be = 0, bb = 0;
+  int rc = mlxq_gguf_block(tag, &be, &bb);
+  if (rc) return rc;
+  if (n < 0 || data_len < 0) return fail(MLXQ_ERR_INVALID, "gguf: negative size");
+  if (n % be)  // dequant.rs:159-163
+    return fail(MLXQ_ERR_SHAPE, "gguf: " + std::to_string(n) + " elements not a multiple of " +
+                                    std::to_string(be) + " for tag " + std::to_string(tag));
+  int64_t nblocks = n / be, need = nblocks * bb;
+  if (data_len < need)  // dequant.rs:166-171
+    return fail(MLXQ_ERR_SHORT_BUFFER, "gguf: tag " + std::to_string(tag) + " needs " + std::to_string(need) +
+                                           " bytes for " + std::to_string(n) + " elements, got " +
+                                           std::to_string(data_len));
+  if (out_dtype != MLXQ_F32 && out_dtype != MLXQ_BF16)
+    return fail(MLXQ_ERR_UNSUPPORTED, "gguf: output dtype must be f32 or bf16");
+  if (n == 0) return MLXQ_OK;
+  if (!data || !out) return fail(MLXQ_ERR_INVALID, "gguf: null pointer");
+  // Block types write kVec outputs per 16-byte store (n is a multiple of 32).
+  if (be > 1 && (reinterpret_cast<uintptr_t>(out) & 15u))
+    return fail(MLXQ_ERR_INVALID, "gguf: output pointer must be 16-byte aligned");
+  const uint8_t* d = static_cast<const uint8_t*>(data);
+  hipStream_t st = as_stream(stream);
+  return out_dtype == MLXQ_BF16 ? dispatch<true>(tag, d, nblocks, n, out, st)
+                                : dispatch<false>(tag, d, nblocks, n, out, st);
+}

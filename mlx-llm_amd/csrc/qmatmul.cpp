@@ -1,0 +1,92 @@
+// C ABI of the quantized matmul: argument checks, workspace sizing and the
+// qmv / qmm choice (MLX makes the same choice from M inside quantized_matmul).
+#include <hip/hip_runtime.h>
+
+#include <string>
+
+#include "common.hpp"
+#include "qmatmul.hpp"
+
+using namespace mlxq;
+
+namespace {
+
+int check_shape(int64_t M, int64_t N, int64_t K, int group_size, int bits) {
+  if (bits != 4 && bits != 8)
+    return fail(MLXQ_ERR_UNSUPPORTED, "unsupported: bits=" + std::to_string(bits) + " (4 or 8)");
+  if (group_size != 32 && group_size != 64 && group_size != 128)
+    return fail(MLXQ_ERR_UNSUPPORTED, "unsupported: group_size=" + std::to_string(group_size) + " (32, 64, 128)");
+  if (M < 0 || N <= 0 || K <= 0) return fail(MLXQ_ERR_INVALID, "qmatmul: bad shape");
+  if (K % group_size)
+    return fail(MLXQ_ERR_SHAPE, "qmatmul: K=" + std::to_string(K) + " is not divisible by group_size " +
+                                    std::to_string(group_size));
+  if (N > INT32_MAX / 2 || K > INT32_MAX / 2 || M > INT32_MAX / 2)
+    return fail(MLXQ_ERR_INVALID, "qmatmul: dimension too large");
+  return MLXQ_OK;
+}
+
+QmvPlan qmv_plan_for(int64_t M, int64_t N, int64_t K, int group_size, int bits) {
+  return plan_qmv(std::min<int64_t>(std::max<int64_t>(M, 1), kQmvMaxM), N, K, group_size, bits);
+}
+
+}  // namespace
+
+extern "C" int mlxq_qmatmul_workspace_size(int64_t M, int64_t N, int64_t K, int group_size, int bits,
+                                           size_t* bytes) {
+  clear_error();
+  int rc = check_shape(M, N, K, group_size, bits);
+  if (rc) return rc;
+  if (!bytes) return fail(MLXQ_ERR_INVALID, "qmatmul: null output pointer");
+  *bytes = qmv_plan_for(M, N, K, group_size, bits).workspace_bytes();
+  return MLXQ_OK;
+}
+
+extern "C" int mlxq_qmatmul_algo(const void* x, int64_t M, const uint32_t* wq, const void* scales,
+                                 const void* biases, const void* bias_vec, int64_t N, int64_t K, int group_size,
+                                 int bits, void* y, void* workspace, size_t workspace_bytes, int algo,
+                                 void* stream) {
+  clear_error();
+  int rc = check_shape(M, N, K, group_size, bits);
+  if (rc) return rc;
+  if (algo < MLXQ_ALGO_AUTO || algo > MLXQ_ALGO_QMM)
+    return fail(MLXQ_ERR_INVALID, "qmatmul: unknown algo " + std::to_string(algo));
+  if (M == 0) return MLXQ_OK;
+  if (!x || !wq || !scales || !biases || !y) return fail(MLXQ_ERR_INVALID, "qmatmul: null pointer");
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(wq)) & 15u)
+    return fail(MLXQ_ERR_INVALID, "qmatmul: x and wq must be 16-byte aligned");
+  if (algo == MLXQ_ALGO_AUTO) algo = M <= kQmvMaxM ? MLXQ_ALGO_QMV : MLXQ_ALGO_QMM;
+  if (algo == MLXQ_ALGO_QMM && K % 64) algo = MLXQ_ALGO_QMV;  // qmm steps K by 64
+
+  const uint16_t* xp = static_cast<const uint16_t*>(x);
+  const uint16_t* sp = static_cast<const uint16_t*>(scales);
+  const uint16_t* bp = static_cast<const uint16_t*>(biases);
+  const uint16_t* bias = static_cast<const uint16_t*>(bias_vec);
+  uint16_t* yp = static_cast<uint16_t*>(y);
+  hipStream_t st = as_stream(stream);
+
+  if (algo == MLXQ_ALGO_QMM) return launch_qmm(xp, M, wq, sp, bp, bias, N, K, group_size, bits, yp, st);
+
+  // qmv in chunks of at most 32 activation rows (one launch for decode shapes)
+  const QmvPlan full = qmv_plan_for(M, N, K, group_size, bits);
+  if (full.workspace_bytes() > 0) {
+    if (!workspace || workspace_bytes < full.workspace_bytes())
+      return fail(MLXQ_ERR_WORKSPACE, "qmatmul: workspace of " + std::to_string(full.workspace_bytes()) +
+                                          " bytes required, got " + std::to_string(workspace_bytes));
+    if (reinterpret_cast<uintptr_t>(workspace) & 255u)
+      return fail(MLXQ_ERR_WORKSPACE, "qmatmul: workspace must be 256-byte aligned");
+  }
+  for (int64_t m0 = 0; m0 < M; m0 += kQmvMaxM) {
+    const int64_t mc = std::min<int64_t>(kQmvMaxM, M - m0);
+    const QmvPlan p = plan_qmv(mc, N, K, group_size, bits);
+    rc = launch_qmv(p, xp + m0 * K, mc, wq, sp, bp, bias, N, K, group_size, bits, yp + m0 * N, workspace, st);
+    if (rc) return rc;
+  }
+  return MLXQ_OK;
+}
+
+extern "C" int mlxq_qmatmul(const void* x, int64_t M, const uint32_t* wq, const void* scales, const void* biases,
+                            const void* bias_vec, int64_t N, int64_t K, int group_size, int bits, void* y,
+                            void* workspace, size_t workspace_bytes, void* stream) {
+  return mlxq_qmatmul_algo(x, M, wq, scales, biases, bias_vec, N, K, group_size, bits, y, workspace,
+                           workspace_bytes, MLXQ_ALGO_AUTO, stream);
+}

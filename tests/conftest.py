@@ -1,0 +1,35 @@
+"""Shared test setup: import paths, the `gpu` marker, built libraries."""
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+PKG = ROOT / "mlx-llm_amd"
+ORACLE = ROOT / "oracle"
+for p in (PKG, ORACLE, ROOT / "tests"):
+    if str(p) not in sys.path:
+        sys.path.insert(0, str(p))
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (runs through libmlxq.so on cuda:0)")
+
+
+def _ensure_built():
+    if not (ORACLE / "liboracle.so").exists():
+        subprocess.run(["make", "-s", "-C", str(ORACLE)], check=True)
+    if not (PKG / "libmlxq.so").exists():
+        subprocess.run([sys.executable, str(PKG / "build.py")], check=True)
+
+
+_ensure_built()
+
+
+@pytest.fixture(scope="session")
+def torch_gpu():
+    import torch
+
+    assert torch.cuda.is_available(), "GPU test run without a visible GPU"
+    return torch

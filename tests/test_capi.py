@@ -1,0 +1,91 @@
+"""The C ABI library loads, exports every symbol include/mlxq.h declares, and
+rejects bad arguments with the reference's error classes -- all without a GPU
+(every call here returns before anything is launched)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+import mlxq
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared_symbols():
+    text = (ROOT / "include" / "mlxq.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mlxq_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_exports_every_declared_symbol():
+    L = mlxq.lib()
+    syms = declared_symbols()
+    assert len(syms) >= 10
+    for s in syms:
+        assert hasattr(L, s), s
+    assert set(syms) == set(mlxq.SIGNATURES), "ctypes signature table out of sync with the header"
+
+
+def test_version():
+    assert "gfx950" in mlxq.version()
+
+
+def test_gguf_geometry_matches_reference_table():
+    import json
+
+    kat = json.loads((ROOT / "tests" / "golden" / "gguf_kat.json").read_text())
+    for tag, (e, b) in kat["geometry"].items():
+        assert mlxq.gguf_block(int(tag)) == (e, b)
+    for tag in kat["supported_tags"]:
+        mlxq.gguf_block(tag)
+    for tag, n, nbytes in kat["byte_len"]:
+        assert mlxq.gguf_tensor_byte_len(tag, n) == nbytes
+    for tag in kat["unsupported_tags"]:  # dequant.rs:763-765
+        with pytest.raises(mlxq.Unsupported):
+            mlxq.gguf_block(tag)
+        with pytest.raises(mlxq.Unsupported):
+            mlxq.gguf_tensor_byte_len(tag, 256)
+
+
+def _gguf(tag, data_len, n, out_dtype=mlxq.F32):
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced: the checks fail first
+    return mlxq.lib().mlxq_gguf_dequantize(tag, fake, data_len, n, out_dtype, fake, None)
+
+
+def test_gguf_error_paths():
+    assert _gguf(2, 18, 31) == mlxq.ERR_SHAPE          # dequant.rs:159-163
+    assert b"not a multiple of 32" in mlxq.lib().mlxq_last_error()
+    assert _gguf(2, 17, 32) == mlxq.ERR_SHORT_BUFFER   # dequant.rs:166-171
+    assert b"needs 18 bytes" in mlxq.lib().mlxq_last_error()
+    assert _gguf(9, 64, 32) == mlxq.ERR_UNSUPPORTED    # dequant.rs:109-111
+    assert _gguf(16, 66, 256) == mlxq.ERR_UNSUPPORTED  # grid types: no device kernel
+    assert _gguf(2, 18, 32, out_dtype=mlxq.F16) == mlxq.ERR_UNSUPPORTED
+    assert _gguf(2, 0, 0) == mlxq.OK                   # empty tensor
+
+
+def test_quantize_and_qmatmul_argument_errors():
+    L = mlxq.lib()
+    p = ctypes.c_void_p(0x1000)
+    assert L.mlxq_quantize(p, mlxq.BF16, 4, 100, 64, 4, p, p, p, None) == mlxq.ERR_SHAPE
+    assert b"not divisible by group_size" in L.mlxq_last_error()
+    assert L.mlxq_quantize(p, mlxq.BF16, 4, 128, 64, 3, p, p, p, None) == mlxq.ERR_UNSUPPORTED
+    assert L.mlxq_quantize(p, mlxq.BF16, 4, 128, 48, 4, p, p, p, None) == mlxq.ERR_UNSUPPORTED
+    assert L.mlxq_quantize(p, mlxq.F16, 4, 128, 64, 4, p, p, p, None) == mlxq.ERR_UNSUPPORTED
+    assert L.mlxq_dequantize(p, p, p, mlxq.BF16, 4, 96, 64, 4, p, None) == mlxq.ERR_SHAPE
+    assert L.mlxq_qmatmul(p, 1, p, p, p, None, 64, 100, 64, 4, p, None, 0, None) == mlxq.ERR_SHAPE
+    assert L.mlxq_qmatmul(p, 1, p, p, p, None, 64, 128, 64, 2, p, None, 0, None) == mlxq.ERR_UNSUPPORTED
+    # a shape that needs split-K partials refuses a missing workspace
+    need = mlxq.workspace_size(1, 4096, 4096, 64, 4)
+    assert need > 0
+    assert L.mlxq_qmatmul(p, 1, p, p, p, None, 4096, 4096, 64, 4, p, None, 0, None) == mlxq.ERR_WORKSPACE
+    assert L.mlxq_qmatmul_algo(p, 1, p, p, p, None, 64, 128, 64, 4, p, None, 0, 7, None) == mlxq.ERR_INVALID
+    # M = 0 is a no-op
+    assert L.mlxq_qmatmul(p, 0, p, p, p, None, 64, 128, 64, 4, p, None, 0, None) == mlxq.OK
+
+
+def test_workspace_sizes_cover_every_decode_shape():
+    for k, n in [(4096, 4096), (4096, 1024), (4096, 14336), (14336, 4096)]:
+        for m in (1, 4, 16, 32, 2048):
+            for bits in (4, 8):
+                mlxq.workspace_size(m, n, k, 64, bits)

@@ -1,0 +1,87 @@
+"""Affine group-wise quantize / dequantize on the GPU vs the CPU restatement
+of MLX's algorithm: bit-exact codes, scales and biases."""
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import mlxq
+import oracle as orc
+from helpers import bf16_weights, dev, host
+
+pytestmark = pytest.mark.gpu
+KAT = json.loads((Path(__file__).resolve().parent / "golden" / "gguf_kat.json").read_text())
+
+
+def gpu_quantize(w, gs, bits, bf16):
+    import torch
+
+    wq, s, b = mlxq.quantize(dev(w, bf16=bf16), gs, bits)
+    torch.cuda.synchronize()
+    return host(wq), host(s), host(b)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+@pytest.mark.parametrize("bf16", [True, False])
+def test_codes_bit_exact(torch_gpu, bits, gs, bf16):
+    rows, cols = 96, 1024
+    w = bf16_weights(1000 + bits + gs, rows, cols)
+    if not bf16:
+        w = orc.normal(2000 + bits + gs, rows * cols, 0.0, 0.02).reshape(rows, cols)
+    w = w.copy()
+    # edge cases: constant group, zero group, one outlier, exact ramp
+    if bf16:
+        w[0, :gs] = orc.f32_to_bf16(np.float32([0.25]))[0]
+        w[1, :gs] = 0
+        w[2, 5] = orc.f32_to_bf16(np.float32([3.0]))[0]
+    else:
+        w[0, :gs] = 0.25
+        w[1, :gs] = 0
+        w[2, 5] = 3.0
+        w[3, :gs] = np.arange(gs) % 16
+    ref = orc.affine_quantize(w, gs, bits, orc.BF16 if bf16 else orc.F32)
+    got = gpu_quantize(w, gs, bits, bf16)
+    for r, g in zip(ref, got):
+        assert np.array_equal(np.asarray(r).view(np.uint8), np.asarray(g).view(np.uint8))
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_dequantize_bit_exact(torch_gpu, bits):
+    import torch
+
+    w = bf16_weights(31 + bits, 64, 512)
+    wq, s, b = orc.affine_quantize(w, 64, bits, orc.BF16)
+    ref = orc.affine_dequantize(wq, s, b, 64, bits, orc.BF16)
+    got = mlxq.dequantize(dev(wq), dev(s, bf16=True), dev(b, bf16=True), 64, bits)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(got), ref)
+    wf = orc.normal(40 + bits, 64 * 512, 0, 0.02).reshape(64, 512)
+    wq, s, b = orc.affine_quantize(wf, 64, bits, orc.F32)
+    ref = orc.affine_dequantize(wq, s, b, 64, bits, orc.F32)
+    got = mlxq.dequantize(dev(wq), dev(s), dev(b), 64, bits)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(got).view(np.uint32), ref.view(np.uint32))
+
+
+def test_reference_roundtrip_q8(torch_gpu):
+    import torch
+
+    a = KAT["affine"]["roundtrip_q8"]  # quant.rs:91-107
+    w = np.float32(a["w"]).reshape(a["shape"])
+    wq, s, b = mlxq.quantize(dev(w), 64, 8)
+    back = host(mlxq.dequantize(wq, s, b, 64, 8))
+    torch.cuda.synchronize()
+    assert np.max(np.abs(back - w)) < a["max_abs_err"]
+
+
+@pytest.mark.parametrize("shape", [(4096, 4096), (14336, 4096), (4096, 14336)])
+@pytest.mark.parametrize("bits", [4, 8])
+def test_llama_shapes_bit_exact(torch_gpu, shape, bits):
+    n, k = shape
+    w = bf16_weights(0x5EED0000 + n + k + bits, n, k)
+    ref = orc.affine_quantize(w, 64, bits, orc.BF16)
+    got = gpu_quantize(w, 64, bits, True)
+    for r, g in zip(ref, got):
+        assert np.array_equal(r.view(np.uint8), g.view(np.uint8))

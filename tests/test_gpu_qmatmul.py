@@ -1,0 +1,176 @@
+"""Quantized matmul (qmv decode GEMV, qmm MFMA GEMM) on the GPU vs the f64 CPU
+oracle over the same bf16 inputs.  Bar: max|y - ref| / max|ref| <= 1e-2
+(bf16 output, f32 accumulation); in practice the error is bf16 output
+rounding, so a tighter 4e-3 is asserted too."""
+import numpy as np
+import pytest
+
+import mlxq
+import oracle as orc
+from helpers import bf16_acts, bf16_weights, dev, host, rel_err
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-2
+TIGHT = 4e-3     # what the kernels actually achieve (bf16 output rounding ~2e-3)
+LLAMA = {"q_o": (4096, 4096), "k_v": (4096, 1024), "gate_up": (4096, 14336), "down": (14336, 4096)}
+
+
+def make_layer(seed, n, k, gs=64, bits=4, outlier_cols=0):
+    w = bf16_weights(seed, n, k)
+    if outlier_cols:
+        # scale a few input channels x20 to stress per-group scales (config 3)
+        cols = np.random.default_rng(seed).choice(k, outlier_cols, replace=False)
+        wf = orc.bf16_to_f32(w)
+        wf[:, cols] *= 20
+        w = orc.f32_to_bf16(wf)
+    wq, s, b = orc.affine_quantize(w, gs, bits, orc.BF16)
+    return wq, s, b
+
+
+def run(x, wq, s, b, gs, bits, algo=mlxq.ALGO_AUTO, bias=None):
+    import torch
+
+    y = mlxq.qmatmul(dev(x, bf16=True), dev(wq), dev(s, bf16=True), dev(b, bf16=True), gs, bits,
+                     bias=None if bias is None else dev(bias, bf16=True), algo=algo)
+    torch.cuda.synchronize()
+    return orc.bf16_to_f32(host(y))
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+@pytest.mark.parametrize("m", [1, 3, 16, 17, 32])
+def test_qmv_small(torch_gpu, bits, gs, m):
+    n, k = 200, 1024  # N not a multiple of 64: masked rows
+    wq, s, b = make_layer(10 + bits + gs, n, k, gs, bits)
+    x = bf16_acts(20 + m, m, k)
+    ref = orc.qmatmul_f64(x, wq, s, b, gs, bits)
+    y = run(x, wq, s, b, gs, bits, mlxq.ALGO_QMV)
+    assert rel_err(y, ref) <= TIGHT
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("name", list(LLAMA))
+@pytest.mark.parametrize("m", [1, 4, 16, 32])
+def test_qmv_llama_shapes(torch_gpu, bits, name, m):
+    k, n = LLAMA[name]
+    wq, s, b = make_layer(0x5EED0000 + k + n + bits, n, k, 64, bits)
+    x = bf16_acts(0x5EED1000 + m, m, k)
+    ref = orc.qmatmul_f64(x, wq, s, b, 64, bits)
+    y = run(x, wq, s, b, 64, bits)
+    err = rel_err(y, ref)
+    assert err <= TIGHT, err
+    assert err <= TOL
+
+
+def test_qmv_config1_single_decode(torch_gpu):
+    """Config 1: W 4096x4096 from N(0,0.02), Q4 g64, x 1x4096 N(0,1)."""
+    wq, s, b = make_layer(0x5EED0001, 4096, 4096, 64, 4)
+    x = bf16_acts(0x5EED0002, 1, 4096)
+    ref = orc.qmatmul_f64(x, wq, s, b, 64, 4)
+    y = run(x, wq, s, b, 64, 4)
+    assert rel_err(y, ref) <= TIGHT
+
+
+def test_qmv_repeat_reuses_workspace(torch_gpu):
+    """Split-K tickets are left at zero: back-to-back calls agree bit-for-bit."""
+    wq, s, b = make_layer(5, 4096, 4096, 64, 4)
+    x = bf16_acts(6, 4, 4096)
+    y1 = run(x, wq, s, b, 64, 4)
+    y2 = run(x, wq, s, b, 64, 4)
+    y3 = run(x[:1], wq, s, b, 64, 4)
+    assert np.array_equal(y1, y2)
+    assert np.array_equal(y3[0], y1[0]) or rel_err(y3, orc.qmatmul_f64(x[:1], wq, s, b, 64, 4)) <= TIGHT
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+@pytest.mark.parametrize("m", [16, 300])
+def test_qmm_small(torch_gpu, bits, gs, m):
+    n, k = 200, 512
+    wq, s, b = make_layer(50 + bits + gs, n, k, gs, bits)
+    x = bf16_acts(60 + m, m, k)
+    ref = orc.qmatmul_f64(x, wq, s, b, gs, bits)
+    y = run(x, wq, s, b, gs, bits, mlxq.ALGO_QMM)
+    assert rel_err(y, ref) <= TIGHT
+
+
+def test_bias_vector(torch_gpu):
+    n, k = 192, 256
+    wq, s, b = make_layer(70, n, k)
+    x = bf16_acts(71, 5, k)
+    bias = orc.f32_to_bf16(orc.normal(72, n, 0, 1))
+    ref = orc.qmatmul_f64(x, wq, s, b) + orc.bf16_to_f32(bias)[None, :]
+    for algo in (mlxq.ALGO_QMV, mlxq.ALGO_QMM):
+        assert rel_err(run(x, wq, s, b, 64, 4, algo, bias=bias), ref) <= TIGHT
+
+
+@pytest.mark.parametrize("name", ["gate_up", "down"])
+def test_qmm_config3_prefill(torch_gpu, name):
+    """Config 3: M=2048, Q4 g64, 0.1% outlier input channels x20; the oracle
+    checks a seeded sample of 64 rows (rows are independent)."""
+    k, n = LLAMA[name]
+    wq, s, b = make_layer(0x5EED0300 + k, n, k, 64, 4, outlier_cols=(k + 999) // 1000)
+    x = bf16_acts(0x5EED0301, 2048, k)
+    y = run(x, wq, s, b, 64, 4)
+    rows = np.sort(np.random.default_rng(3).choice(2048, 64, replace=False))
+    ref = orc.qmatmul_f64(x[rows], wq, s, b, 64, 4)
+    err = rel_err(y[rows], ref)
+    assert err <= TIGHT, err
+
+
+def test_qmv_and_qmm_agree(torch_gpu):
+    wq, s, b = make_layer(80, 1024, 2048)
+    x = bf16_acts(81, 32, 2048)
+    ref = orc.qmatmul_f64(x, wq, s, b)
+    assert rel_err(run(x, wq, s, b, 64, 4, mlxq.ALGO_QMV), ref) <= TIGHT
+    assert rel_err(run(x, wq, s, b, 64, 4, mlxq.ALGO_QMM), ref) <= TIGHT
+
+
+def test_reference_matmul_q8(torch_gpu):
+    import json
+    from pathlib import Path
+
+    a = json.loads((Path(__file__).resolve().parent / "golden" / "gguf_kat.json").read_text())["affine"]["matmul_q8"]
+    w = np.float32(a["w"]).reshape(a["shape"])
+    x = np.float32(a["x"]).reshape(1, 64)
+    wq, s, b = orc.affine_quantize(orc.f32_to_bf16(w), 64, 8, orc.BF16)
+    y = run(orc.f32_to_bf16(x), wq, s, b, 64, 8)
+    dense = x.astype(np.float64) @ w.astype(np.float64).T
+    assert np.max(np.abs(y - dense)) < a["max_abs_err"]  # quant.rs:111-125
+
+
+def test_graph_replay_matches_eager(torch_gpu):
+    """Capture qmv (split-K tickets) + qmm in one HIP graph; replay it several
+    times with eager work and synchronizations in between; every replay must
+    equal the eager result bit-for-bit."""
+    torch = torch_gpu
+    wq, s, b = make_layer(90, 4096, 4096)
+    x1 = dev(bf16_acts(91, 4, 4096), bf16=True)
+    x2 = dev(bf16_acts(92, 64, 4096), bf16=True)
+    d = [dev(t) for t in (wq,)] + [dev(t, bf16=True) for t in (s, b)]
+    c1 = mlxq.bind_qmatmul(x1, *d, 64, 4)
+    c2 = mlxq.bind_qmatmul(x2, *d, 64, 4)
+    e1, e2 = c1().clone(), c2().clone()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        c1()
+        c2()
+    for i in range(4):
+        c1.out.zero_()
+        c2.out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(c1.out, e1) and torch.equal(c2.out, e2), f"replay {i}"
+        mlxq.qmatmul(x1, *d, 64, 4)  # eager work between replays
+        torch.cuda.synchronize()
+
+
+def test_workspace_shared_across_shapes(torch_gpu):
+    """Alternate shapes with different tile counts and split counts on one
+    workspace: tickets stay valid (regression: partials once overlapped tickets)."""
+    shapes = [(4096, 4096), (4096, 14336), (4096, 1024), (14336, 4096), (4096, 14336)]
+    for i, (k, n) in enumerate(shapes):
+        wq, s, b = make_layer(100 + i, n, k)
+        x = bf16_acts(200 + i, 8, k)
+        assert rel_err(run(x, wq, s, b, 64, 4), orc.qmatmul_f64(x, wq, s, b)) <= TIGHT
