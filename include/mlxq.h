@@ -90,9 +90,11 @@ int mlxq_dequantize(const uint32_t* wq, const void* scales, const void* biases,
 /* Quantized matmul                                                    */
 /* ------------------------------------------------------------------ */
 
-/* Bytes of device workspace mlxq_qmatmul needs for this shape (0 possible).
- * The workspace must be zero-filled once before its first use; every call
- * leaves it zero-filled again on completion. */
+/* Bytes of device workspace mlxq_qmatmul needs for this shape.  The current
+ * kernels need none (0 for every shape); the argument is kept so a future
+ * split-K kernel can use caller-owned scratch without an ABI change.  A
+ * workspace, when one is required, must be zero-filled before first use and
+ * is left zero-filled by every call. */
 int mlxq_qmatmul_workspace_size(int64_t M, int64_t N, int64_t K,
                                 int group_size, int bits, size_t* bytes);
 

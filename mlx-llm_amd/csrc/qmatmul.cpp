@@ -2,6 +2,8 @@
 // qmv / qmm choice (MLX makes the same choice from M inside quantized_matmul).
 #include <hip/hip_runtime.h>
 
+#include <stdlib.h>
+
 #include <string>
 
 #include "common.hpp"
@@ -66,6 +68,10 @@ extern "C" int mlxq_qmatmul_algo(const void* x, int64_t M, const uint32_t* wq, c
 
   if (algo == MLXQ_ALGO_QMM) return launch_qmm(xp, M, wq, sp, bp, bias, N, K, group_size, bits, yp, st);
 
+  // decode rows on the vector ALUs (MLXQ_QMV_MFMA=1 forces the MFMA kernel)
+  if (M <= kQmvDotMaxM && qmv_dot_eligible(M, N, K, group_size, bits) && !getenv("MLXQ_QMV_MFMA"))
+    return launch_qmv_dot(xp, M, wq, sp, bp, bias, N, K, group_size, bits, yp, st);
+
   // qmv in chunks of at most 32 activation rows (one launch for decode shapes)
   const QmvPlan full = qmv_plan_for(M, N, K, group_size, bits);
   if (full.workspace_bytes() > 0) {
@@ -78,7 +84,7 @@ extern "C" int mlxq_qmatmul_algo(const void* x, int64_t M, const uint32_t* wq, c
   for (int64_t m0 = 0; m0 < M; m0 += kQmvMaxM) {
     const int64_t mc = std::min<int64_t>(kQmvMaxM, M - m0);
     const QmvPlan p = plan_qmv(mc, N, K, group_size, bits);
-    rc = launch_qmv(p, xp + m0 * K, mc, wq, sp, bp, bias, N, K, group_size, bits, yp + m0 * N, workspace, st);
+    rc = launch_qmv(p, xp + m0 * K, mc, wq, sp, bp, bias, N, K, group_size, bits, yp + m0 * N, st);
     if (rc) return rc;
   }
   return MLXQ_OK;

@@ -174,3 +174,53 @@ def test_workspace_shared_across_shapes(torch_gpu):
         wq, s, b = make_layer(100 + i, n, k)
         x = bf16_acts(200 + i, 8, k)
         assert rel_err(run(x, wq, s, b, 64, 4), orc.qmatmul_f64(x, wq, s, b)) <= TIGHT
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("k", [192, 320])
+def test_qmv_odd_k_uses_narrow_loader(torch_gpu, bits, k):
+    """K*bits/8 not a multiple of 64 bytes: the 8-byte group loader path."""
+    wq, s, b = make_layer(300 + k + bits, 130, k, 64, bits)
+    x = bf16_acts(301 + k, 3, k)
+    assert rel_err(run(x, wq, s, b, 64, bits, mlxq.ALGO_QMV), orc.qmatmul_f64(x, wq, s, b, 64, bits)) <= TIGHT
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("m", [1, 32])
+def test_qmv_forced_narrow_loader(torch_gpu, monkeypatch, bits, m):
+    monkeypatch.setenv("MLXQ_QMV_NARROW", "1")
+    k, n = LLAMA["down"]
+    wq, s, b = make_layer(400 + bits, n, k, 64, bits)
+    x = bf16_acts(401 + m, m, k)
+    assert rel_err(run(x, wq, s, b, 64, bits), orc.qmatmul_f64(x, wq, s, b, 64, bits)) <= TIGHT
+
+
+@pytest.mark.parametrize("sub", ["1", "2", "4"])
+def test_qmv_every_tile_height(torch_gpu, monkeypatch, sub):
+    monkeypatch.setenv("MLXQ_QMV_SUB", sub)
+    wq, s, b = make_layer(500, 1000, 2048, 64, 4)
+    x = bf16_acts(501, 20, 2048)
+    assert rel_err(run(x, wq, s, b, 64, 4), orc.qmatmul_f64(x, wq, s, b, 64, 4)) <= TIGHT
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
+@pytest.mark.parametrize("k", [384, 1152])
+def test_qmv_dot_decode_rows(torch_gpu, bits, gs, m, k):
+    """M <= 4 runs on the vector-ALU kernel; K=384/1152 give ragged chunk tails."""
+    if k % gs:
+        pytest.skip("K not a multiple of the group")
+    wq, s, b = make_layer(600 + bits + gs + k, 333, k, gs, bits)
+    x = bf16_acts(601 + m + k, m, k)
+    assert rel_err(run(x, wq, s, b, gs, bits), orc.qmatmul_f64(x, wq, s, b, gs, bits)) <= TIGHT
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("m", [1, 4])
+def test_qmv_mfma_path_for_decode_rows(torch_gpu, monkeypatch, bits, m):
+    monkeypatch.setenv("MLXQ_QMV_MFMA", "1")
+    k, n = LLAMA["q_o"]
+    wq, s, b = make_layer(700 + bits, n, k, 64, bits)
+    x = bf16_acts(701 + m, m, k)
+    assert rel_err(run(x, wq, s, b, 64, bits), orc.qmatmul_f64(x, wq, s, b, 64, bits)) <= TIGHT
