@@ -133,24 +133,26 @@ def main(argv=None) -> int:
     ms_per_step = dt * 1e3 / a.steps
     value = step_bytes * a.steps / dt / 1e9
 
-    # ---- per-launch HIP-event timing: per (bits, M) and per kernel shape ----
-    reps = 5
+    # ---- per-kernel HIP-event timing: events on the launch stream around
+    # batches of back-to-back launches of one shape (4 layer copies x reps),
+    # so the figure is the average launch duration, not event overhead ----
+    reps = 8
     per = {}
     for bits in BITS:
         for m in MS:
             for name, k, n in PROJ:
-                evs = []
                 fns = [mlxq.bind_qmatmul(xs[(m, k)], *layer[name], GS, bits, out=ys[(m, n)])
                        for layer in weights[bits]]
+                for fn in fns:
+                    fn()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
                 for r in range(reps):
                     for fn in fns:
-                        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                        e0.record()
                         fn()
-                        e1.record()
-                        evs.append((e0, e1))
+                e1.record()
                 torch.cuda.synchronize()
-                us = sum(e0.elapsed_time(e1) for e0, e1 in evs) * 1e3 / len(evs)
+                us = e0.elapsed_time(e1) * 1e3 / (reps * len(fns))
                 per[(bits, m, name)] = (us, qbytes(m, n, k, bits))
     kernels = {}
     for bits in BITS:
@@ -162,18 +164,29 @@ def main(argv=None) -> int:
                 "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 3),
                 "us_per_layer": round(tot_us, 2),
                 "by_proj_us": {nm: round(per[(bits, m, nm)][0], 2) for nm, _, _ in PROJ},
+                "by_proj_GBs": {nm: round(per[(bits, m, nm)][1] / per[(bits, m, nm)][0] / 1e3, 1) for nm, _, _ in PROJ},
             }
-    # dominant kernel class of the step: the (bits, M) decode GEMV with the most time
-    dom = max(kernels, key=lambda kk: kernels[kk]["us_per_layer"])
-    dom_bits, dom_m = int(dom[1]), int(dom.split("_m")[1])
-    launches = len(PROJ)
-    avg_us = kernels[dom]["us_per_layer"] / launches
-    avg_bytes = sum(per[(dom_bits, dom_m, nm)][1] for nm, _, _ in PROJ) / launches
-    achieved = avg_bytes / (avg_us * 1e-6) / 1e9
-    roofline = {"kernel": f"qmv_kernel<bits={dom_bits}, M={dom_m}> over the 7 projection shapes",
-                "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+    # dominant kernel of the step: the (bits, M, projection shape) with the
+    # most time per step (gate and up share one shape and one kernel)
+    shapes = {}
+    for (bits, m, nm), (us, nbytes) in per.items():
+        key = (bits, m, dict((p[0], (p[1], p[2])) for p in PROJ)[nm])
+        t, c, b = shapes.get(key, (0.0, 0, nbytes))
+        shapes[key] = (t + us, c + 1, nbytes)
+    (dbits, dm, (dk, dn)), (dt, dc, dbytes) = max(shapes.items(), key=lambda kv: kv[1][0])
+    avg_us = dt / dc
+    achieved = dbytes / (avg_us * 1e-6) / 1e9
+    kname = ("qmv_dot_kernel (vector ALU)" if dm <= 4 else "qmv_kernel (MFMA)")
+    roofline = {"kernel": f"{kname}, Q{dbits} g64, M={dm}, K={dk} -> N={dn}", "bound": "hbm",
+                "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                "avg_launch_us": round(avg_us, 3), "algorithmic_bytes_per_launch": int(avg_bytes)}
+                "avg_launch_us": round(avg_us, 3), "algorithmic_bytes_per_launch": int(dbytes),
+                "share_of_step": round(dt * LAYERS / (ms_per_step * 1e3), 3)}
+    # the north-star headline: Q4 g64 decode GEMV (M=1) at each projection shape
+    headline = {nm: {"us": round(per[(4, 1, nm)][0], 2),
+                     "GB/s": round(per[(4, 1, nm)][1] / per[(4, 1, nm)][0] / 1e3, 1),
+                     "frac_hbm": round(per[(4, 1, nm)][1] / per[(4, 1, nm)][0] / 1e3 / HBM_PEAK_GBS, 3)}
+                for nm, _, _ in PROJ}
     q4m1 = kernels["q4_m1"]
 
     out = {
@@ -188,7 +201,7 @@ def main(argv=None) -> int:
                                f"{LAYERS} distinct layer copies cycled",
                    "group_size": GS, "bytes_per_step": step_bytes},
         "roofline": roofline,
-        "headline_q4_m1": {"GB/s": q4m1["GB/s"], "frac_hbm": q4m1["frac_hbm"]},
+        "headline_q4_m1": {"GB/s": q4m1["GB/s"], "frac_hbm": q4m1["frac_hbm"], "by_proj": headline},
         "kernels": kernels,
     }
 
@@ -216,15 +229,14 @@ def bench_prefill(torch, mlxq, iters=10):
         for _ in range(3):
             mlxq.qmatmul(x, wq, s, b, 64, 4, out=y)
         torch.cuda.synchronize()
-        evs = []
+        fn = mlxq.bind_qmatmul(x, wq, s, b, 64, 4, out=y)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
         for _ in range(iters):
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
-            mlxq.qmatmul(x, wq, s, b, 64, 4, out=y)
-            e1.record()
-            evs.append((e0, e1))
+            fn()
+        e1.record()
         torch.cuda.synchronize()
-        us = sum(e0.elapsed_time(e1) for e0, e1 in evs) * 1e3 / iters
+        us = e0.elapsed_time(e1) * 1e3 / iters
         tf = 2.0 * 2048 * n * k / (us * 1e-6) / 1e12
         res[name] = {"us": round(us, 1), "TFLOP/s": round(tf, 1), "frac_mfma_bf16": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)}
         del w, wq, s, b, x, y
@@ -253,15 +265,13 @@ def bench_gguf(torch, mlxq, iters=10):
         for oname, o, ob in (("f32", out32, 4), ("bf16", out16, 2)):
             mlxq.gguf_dequantize(tag, raw, n, out=o)
             torch.cuda.synchronize()
-            evs = []
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
             for _ in range(iters):
-                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                e0.record()
                 mlxq.gguf_dequantize(tag, raw, n, out=o)
-                e1.record()
-                evs.append((e0, e1))
+            e1.record()
             torch.cuda.synchronize()
-            us = sum(e0.elapsed_time(e1) for e0, e1 in evs) * 1e3 / iters
+            us = e0.elapsed_time(e1) * 1e3 / iters
             gbs = (raw.numel() + n * ob) / (us * 1e-6) / 1e9
             entry[oname] = {"us": round(us, 1), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 3)}
         res[tname] = entry
