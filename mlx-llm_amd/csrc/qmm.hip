@@ -6,18 +6,23 @@
 // is large (prefill, batched decode).
 //
 // Design (MFMA-bound):
-//  * Workgroup tile 256 (M) x 128 (N), K step 64; 4 wavefronts in a 2x2 grid,
-//    each owning 128x64 of the output as 4x2 tiles of
-//    v_mfma_f32_32x32x16_bf16 (f32 accumulators).
-//  * Per K step the workgroup stages the activation tile (bf16, 256x64) and the
-//    weight tile into LDS.  The weight tile is dequantized once per workgroup
-//    on the way in: codes -> f32 -> scale*q + bias -> bf16 (round to nearest
-//    even), the same values MLX's qmm places in threadgroup memory.
-//  * Two LDS stages (2 x 55 KB of gfx950's 160 KB): global loads for step k+1
-//    are issued before the MFMAs of step k and written to the other stage
-//    after them, one barrier per step.  Rows are padded to 72 bf16 so the
-//    16-byte fragment reads of 16 consecutive rows hit distinct banks.
+//  * Workgroup tile BM x BN, K step 64, WM x WN wavefronts each owning
+//    (BM/WM) x (BN/WN) of the output as tiles of v_mfma_f32_32x32x16_bf16
+//    with f32 accumulators.  Default: 8 wavefronts (2 per SIMD), 256 x 256 or
+//    128 x 256 tiles (chosen from the grid size).
+//  * One or two threads own each weight row of the tile per K step: they load
+//    the row's 64 codes and scale/bias, dequantize them once for the whole
+//    workgroup (codes -> f32 -> scale*q + bias -> bf16, round to nearest
+//    even: the values MLX's qmm places in threadgroup memory) and write them
+//    to LDS.  Activations are copied to LDS as they are.
+//  * Latency: two LDS stages and two register stages.  The global loads of
+//    K step k+2 are issued before the MFMAs of step k; step k+1, already in
+//    registers, is written to the other LDS stage after them; one barrier per
+//    step.  Rows are padded to 72 bf16 so the 16-byte fragment reads of 16
+//    consecutive rows hit distinct banks.
 #include <hip/hip_runtime.h>
+
+#include <stdlib.h>
 
 #include <string>
 
@@ -32,11 +37,24 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int BM = 256, BN = 128, BK = 64;
-constexpr int kThreads = 256;
-constexpr int LDR = BK + 8;                       // padded LDS row, bf16 elements
-constexpr int kStageElems = (BM + BN) * LDR;      // bf16 per stage
-constexpr int kLdsBytes = 2 * kStageElems * 2;    // two stages
+constexpr int BK = 64;
+constexpr int LDR = BK + 8;  // padded LDS row, bf16 elements
+
+// Tile BM x BN, WM x WN wavefronts (each (BM/WM) x (BN/WN) of the output).
+template <int BM, int BN, int WM, int WN, int BITS>
+struct QmmGeom {
+  static constexpr int THREADS = 64 * WM * WN;
+  static constexpr int STAGE = (BM + BN) * LDR;           // bf16 per LDS stage
+  static constexpr int LDS_BYTES = 2 * STAGE * 2;          // two stages
+  static constexpr int TM = BM / WM / 32;                  // 32-row MFMA tiles per wave
+  static constexpr int TN = BN / WN / 32;                  // 32-col MFMA tiles per wave
+  static constexpr int AU4 = BM * 8 / THREADS;             // activation uint4 per thread per step
+  static constexpr int PARTS = THREADS / BN;               // threads per weight row (1 or 2)
+  static constexpr int CPT = BK / PARTS;                   // codes per thread per step
+  static constexpr int BU4 = CPT * BITS / 128;             // code uint4 per thread per step
+  static_assert(THREADS % BN == 0 && (PARTS == 1 || PARTS == 2), "weight rows map onto threads");
+  static_assert(BM * 8 % THREADS == 0, "activation chunks map onto threads");
+};
 
 __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
   bf16x2 v;
@@ -45,169 +63,203 @@ __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-template <int BITS>
-struct BRegs {
-  static constexpr int W = BITS == 4 ? 4 : 8;  // code words per thread per K step (32 elements)
-  uint32_t w[W];
-  float s, b;
+// One K step of global data held in registers by one thread.
+template <typename Gm>
+struct Stage {
+  uint4 a[Gm::AU4];
+  uint4 b[Gm::BU4];
+  float s[2], z[2];  // scale/bias of the thread's codes (two groups only for g32 with 64 codes)
 };
 
-template <int BITS, int GS>
-__global__ __launch_bounds__(kThreads) void qmm_kernel(const uint16_t* __restrict__ x, int M,
-                                                        const uint32_t* __restrict__ wq,
-                                                        const uint16_t* __restrict__ scales,
-                                                        const uint16_t* __restrict__ biases,
-                                                        const uint16_t* __restrict__ bias_vec, int N, int K,
-                                                        uint16_t* __restrict__ y) {
+template <int BITS, int GS, int BM, int BN, int WM, int WN>
+__global__ __launch_bounds__(64 * WM * WN, 1) void qmm_kernel(const uint16_t* __restrict__ x, int M,
+                                                               const uint32_t* __restrict__ wq,
+                                                               const uint16_t* __restrict__ scales,
+                                                               const uint16_t* __restrict__ biases,
+                                                               const uint16_t* __restrict__ bias_vec, int N, int K,
+                                                               uint16_t* __restrict__ y) {
+  using Gm = QmmGeom<BM, BN, WM, WN, BITS>;
+  using St = Stage<Gm>;
+  constexpr int T = Gm::THREADS;
   extern __shared__ __align__(16) uint16_t lds[];
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WN, wn = wave % WN;
   const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
   const int KT = K / BK;
   const int G = K / GS;
   const int64_t row_words = static_cast<int64_t>(K) * BITS / 32;
 
-  // ---- activation tile loader: 8 rows x 16 B per wave instruction ----
-  const int a_chunk = tid & 7;    // 8 bf16 of the 64-wide K step
-  const int a_row0 = tid >> 3;    // + 32*i, i < 8
-  const uint4* a_src[8];
-  bool a_ok[8];
+  // activation loader: 8 threads per row (16 B each), rows tid/8 + (T/8) i
+  const int a_chunk = tid & 7, a_row0 = tid >> 3;
+  const uint4* a_src = reinterpret_cast<const uint4*>(x) + a_chunk;
+  int a_off[Gm::AU4];  // uint4 offset of each row (rows past M repeat row M-1; results dropped)
 #pragma unroll
-  for (int i = 0; i < 8; i++) {
-    const int m = m0 + a_row0 + 32 * i;
-    a_ok[i] = m < M;
-    a_src[i] = reinterpret_cast<const uint4*>(x + static_cast<int64_t>(a_ok[i] ? m : 0) * K + a_chunk * 8);
-  }
-  // ---- weight tile loader: one row, 32 consecutive K per thread ----
-  const int b_row = tid >> 1, b_half = tid & 1;
+  for (int i = 0; i < Gm::AU4; i++) a_off[i] = min(m0 + a_row0 + (T / 8) * i, M - 1) * (K / 8);
+  // weight loader: PARTS threads per row, each CPT consecutive codes
+  const int b_row = tid / Gm::PARTS, b_part = tid % Gm::PARTS;
   const int b_n = min(n0 + b_row, N - 1);
-  const uint32_t* b_src = wq + b_n * row_words + b_half * (32 * BITS / 32);
+  const uint4* b_src = reinterpret_cast<const uint4*>(wq + b_n * row_words) + b_part * Gm::BU4;
   const uint16_t* s_src = scales + static_cast<int64_t>(b_n) * G;
   const uint16_t* z_src = biases + static_cast<int64_t>(b_n) * G;
 
-  uint4 areg[8];
-  BRegs<BITS> breg;
-
-  auto load_tiles = [&](int kt) {
+  auto load = [&](St& r, int kt) {
     const int k0 = kt * BK;
 #pragma unroll
-    for (int i = 0; i < 8; i++) areg[i] = a_ok[i] ? a_src[i][k0 / 8] : make_uint4(0, 0, 0, 0);
-    const uint32_t* p = b_src + static_cast<int64_t>(k0) * BITS / 32;
+    for (int i = 0; i < Gm::AU4; i++) r.a[i] = a_src[a_off[i] + k0 / 8];
 #pragma unroll
-    for (int i = 0; i < BRegs<BITS>::W; i += 4) {
-      uint4 v = *reinterpret_cast<const uint4*>(p + i);
-      breg.w[i] = v.x; breg.w[i + 1] = v.y; breg.w[i + 2] = v.z; breg.w[i + 3] = v.w;
+    for (int i = 0; i < Gm::BU4; i++) r.b[i] = b_src[k0 * BITS / 128 + i];
+    const int kc = k0 + b_part * Gm::CPT;  // first code of this thread
+    if constexpr (GS == 32 && Gm::CPT == 64) {
+      r.s[0] = bf16_bits_to_f32(s_src[kc / 32]);
+      r.s[1] = bf16_bits_to_f32(s_src[kc / 32 + 1]);
+      r.z[0] = bf16_bits_to_f32(z_src[kc / 32]);
+      r.z[1] = bf16_bits_to_f32(z_src[kc / 32 + 1]);
+    } else {
+      r.s[0] = r.s[1] = bf16_bits_to_f32(s_src[kc / GS]);
+      r.z[0] = r.z[1] = bf16_bits_to_f32(z_src[kc / GS]);
     }
-    const int g = (k0 + 32 * b_half) / GS;
-    breg.s = bf16_bits_to_f32(s_src[g]);
-    breg.b = bf16_bits_to_f32(z_src[g]);
   };
 
-  auto store_tiles = [&](int stage) {
-    uint16_t* sa = lds + stage * kStageElems;
+  auto store = [&](const St& r, int stage) {
+    uint16_t* sa = lds + stage * Gm::STAGE;
     uint16_t* sb = sa + BM * LDR;
 #pragma unroll
-    for (int i = 0; i < 8; i++)
-      *reinterpret_cast<uint4*>(sa + (a_row0 + 32 * i) * LDR + a_chunk * 8) = areg[i];
-    uint32_t packed[16];
+    for (int i = 0; i < Gm::AU4; i++)
+      *reinterpret_cast<uint4*>(sa + (a_row0 + (T / 8) * i) * LDR + a_chunk * 8) = r.a[i];
+    constexpr int NW = Gm::BU4 * 4;  // code words
+    uint32_t w[NW];
+#pragma unroll
+    for (int i = 0; i < Gm::BU4; i++) {
+      w[4 * i] = r.b[i].x; w[4 * i + 1] = r.b[i].y; w[4 * i + 2] = r.b[i].z; w[4 * i + 3] = r.b[i].w;
+    }
+    uint32_t packed[Gm::CPT / 2];
     if constexpr (BITS == 4) {
 #pragma unroll
-      for (int w = 0; w < 4; w++) {
-        const uint32_t q = breg.w[w];
+      for (int wi = 0; wi < NW; wi++) {  // word wi: codes 8 wi .. 8 wi + 7
+        const float sc = r.s[wi / 4], zz = r.z[wi / 4];
+        const uint32_t q = w[wi];
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-          const float lo = breg.s * static_cast<float>((q >> (8 * j)) & 0xFu) + breg.b;
-          const float hi = breg.s * static_cast<float>((q >> (8 * j + 4)) & 0xFu) + breg.b;
-          packed[4 * w + j] = pack_bf16(lo, hi);
-        }
+        for (int j = 0; j < 4; j++)
+          packed[4 * wi + j] = pack_bf16(sc * static_cast<float>((q >> (8 * j)) & 0xFu) + zz,
+                                         sc * static_cast<float>((q >> (8 * j + 4)) & 0xFu) + zz);
       }
     } else {
 #pragma unroll
-      for (int w = 0; w < 8; w++) {
-        const uint32_t q = breg.w[w];
-        const float v0 = breg.s * static_cast<float>(q & 0xFFu) + breg.b;
-        const float v1 = breg.s * static_cast<float>((q >> 8) & 0xFFu) + breg.b;
-        const float v2 = breg.s * static_cast<float>((q >> 16) & 0xFFu) + breg.b;
-        const float v3 = breg.s * static_cast<float>(q >> 24) + breg.b;
-        packed[2 * w] = pack_bf16(v0, v1);
-        packed[2 * w + 1] = pack_bf16(v2, v3);
+      for (int wi = 0; wi < NW; wi++) {  // word wi: codes 4 wi .. 4 wi + 3
+        const float sc = r.s[wi / 8], zz = r.z[wi / 8];
+        const uint32_t q = w[wi];
+        packed[2 * wi] = pack_bf16(sc * static_cast<float>(q & 0xFFu) + zz, sc * static_cast<float>((q >> 8) & 0xFFu) + zz);
+        packed[2 * wi + 1] = pack_bf16(sc * static_cast<float>((q >> 16) & 0xFFu) + zz, sc * static_cast<float>(q >> 24) + zz);
       }
     }
-    uint4* dst = reinterpret_cast<uint4*>(sb + b_row * LDR + b_half * 32);
+    uint4* dst = reinterpret_cast<uint4*>(sb + b_row * LDR + b_part * Gm::CPT);
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < Gm::CPT / 8; i++)
       dst[i] = make_uint4(packed[4 * i], packed[4 * i + 1], packed[4 * i + 2], packed[4 * i + 3]);
   };
 
-  f32x16 acc[4][2];
+  f32x16 acc[Gm::TM][Gm::TN];
 #pragma unroll
-  for (int i = 0; i < 4; i++)
+  for (int i = 0; i < Gm::TM; i++)
 #pragma unroll
-    for (int j = 0; j < 2; j++)
+    for (int j = 0; j < Gm::TN; j++)
 #pragma unroll
       for (int v = 0; v < 16; v++) acc[i][j][v] = 0.f;
 
   const int frag_row = lane & 31;
   const int frag_k = (lane >> 5) * 8;
+  constexpr int WROWS = BM / WM, WCOLS = BN / WN;
 
-  load_tiles(0);
-  store_tiles(0);
+  St r0, r1;
+  load(r0, 0);
+  if (KT > 1) load(r1, 1);
+  __builtin_amdgcn_sched_barrier(0);
+  store(r0, 0);
   __syncthreads();
-  for (int kt = 0; kt < KT; kt++) {
+  // One K step: LDS stage kt&1 holds step kt, `ready` holds step kt+1 and
+  // `target` receives step kt+2.  Called with (r0, r1) and (r1, r0) in turn
+  // so that the register roles are static.
+  auto step = [&](int kt, St& target, St& ready) {
     const int cur = kt & 1;
-    const bool more = kt + 1 < KT;
-    if (more) load_tiles(kt + 1);
-    const uint16_t* sa = lds + cur * kStageElems + (wm * 128 + frag_row) * LDR + frag_k;
-    const uint16_t* sb = lds + cur * kStageElems + BM * LDR + (wn * 64 + frag_row) * LDR + frag_k;
+    if (kt + 2 < KT) load(target, kt + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    const uint16_t* sa = lds + cur * Gm::STAGE + (wm * WROWS + frag_row) * LDR + frag_k;
+    const uint16_t* sb = lds + cur * Gm::STAGE + BM * LDR + (wn * WCOLS + frag_row) * LDR + frag_k;
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ks++) {
-      bf16x8 a[4], b[2];
+      bf16x8 a[Gm::TM], b[Gm::TN];
 #pragma unroll
-      for (int i = 0; i < 4; i++)
+      for (int i = 0; i < Gm::TM; i++)
         a[i] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(sa + 32 * i * LDR + ks * 16));
 #pragma unroll
-      for (int j = 0; j < 2; j++)
+      for (int j = 0; j < Gm::TN; j++)
         b[j] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(sb + 32 * j * LDR + ks * 16));
 #pragma unroll
-      for (int i = 0; i < 4; i++)
+      for (int i = 0; i < Gm::TM; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < Gm::TN; j++)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
     }
-    if (more) store_tiles(cur ^ 1);
+    if (kt + 1 < KT) store(ready, cur ^ 1);
     __syncthreads();
+  };
+  for (int kt = 0; kt < KT; kt += 2) {
+    step(kt, r0, r1);
+    if (kt + 1 < KT) step(kt + 1, r1, r0);
   }
 
   // C layout of a 32x32 MFMA tile: lane holds column lane%32 and rows
   // 8*(v/4) + 4*(lane/32) + v%4.
 #pragma unroll
-  for (int j = 0; j < 2; j++) {
-    const int n = n0 + wn * 64 + 32 * j + (lane & 31);
+  for (int j = 0; j < Gm::TN; j++) {
+    const int n = n0 + wn * WCOLS + 32 * j + (lane & 31);
     if (n >= N) continue;
     const float bb = bias_vec ? bf16_bits_to_f32(bias_vec[n]) : 0.f;
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < Gm::TM; i++)
 #pragma unroll
       for (int v = 0; v < 16; v++) {
-        const int m = m0 + wm * 128 + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+        const int m = m0 + wm * WROWS + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
         if (m < M) y[static_cast<int64_t>(m) * N + n] = static_cast<uint16_t>(f32_to_bf16_bits(acc[i][j][v] + bb));
       }
   }
 }
 
-template <int BITS, int GS>
+template <int BITS, int GS, int BM, int BN, int WM, int WN>
 int launch(const uint16_t* x, int M, const uint32_t* wq, const uint16_t* s, const uint16_t* b, const uint16_t* bias,
            int N, int K, uint16_t* y, hipStream_t st) {
-  static bool attr_set = false;
+  using Gm = QmmGeom<BM, BN, WM, WN, BITS>;
+  auto kern = qmm_kernel<BITS, GS, BM, BN, WM, WN>;
+  static bool attr_set = false;  // once per process; the attribute is per function
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&qmm_kernel<BITS, GS>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       Gm::LDS_BYTES);
     if (e != hipSuccess) return fail(MLXQ_ERR_DEVICE, std::string("qmm: set LDS size: ") + hipGetErrorString(e));
     attr_set = true;
   }
   dim3 grid(ceil_div(N, BN), ceil_div(M, BM));
-  hipLaunchKernelGGL((qmm_kernel<BITS, GS>), grid, dim3(kThreads), kLdsBytes, st, x, M, wq, s, b, bias, N, K, y);
+  hipLaunchKernelGGL(kern, grid, dim3(Gm::THREADS), Gm::LDS_BYTES, st, x, M, wq, s, b, bias, N, K, y);
   return check_launch("qmm");
+}
+
+template <int BITS, int GS>
+int launch_cfg(const uint16_t* x, int M, const uint32_t* wq, const uint16_t* s, const uint16_t* b, const uint16_t* bias,
+               int N, int K, uint16_t* y, hipStream_t st) {
+  // 8 wavefronts (2 per SIMD).  256 x 256 tiles (4 x 2 waves of 64 x 128)
+  // when the grid then still has >= 1.5 workgroups per CU, else 128 x 256
+  // (2 x 4 waves of 64 x 64) -- the faster of the measured configurations
+  // at the Llama-3-8B prefill shapes.  MLXQ_QMM_CFG overrides (tuning).
+  const int64_t tiles256 = ceil_div(N, 256) * ceil_div(M, 256);
+  int cfg = tiles256 >= 384 ? 4 : 3;
+  if (const char* e = getenv("MLXQ_QMM_CFG")) cfg = atoi(e);
+  switch (cfg) {
+    case 1: return launch<BITS, GS, 256, 256, 2, 4>(x, M, wq, s, b, bias, N, K, y, st);
+    case 2: return launch<BITS, GS, 256, 128, 2, 2>(x, M, wq, s, b, bias, N, K, y, st);
+    case 3: return launch<BITS, GS, 128, 256, 2, 4>(x, M, wq, s, b, bias, N, K, y, st);
+    case 4: return launch<BITS, GS, 256, 256, 4, 2>(x, M, wq, s, b, bias, N, K, y, st);
+    default: return launch<BITS, GS, 128, 256, 2, 2>(x, M, wq, s, b, bias, N, K, y, st);
+  }
 }
 
 }  // namespace
@@ -216,13 +268,13 @@ int launch_qmm(const uint16_t* x, int64_t M, const uint32_t* wq, const uint16_t*
                const uint16_t* bias, int64_t N, int64_t K, int group_size, int bits, uint16_t* y, hipStream_t st) {
   const int m = static_cast<int>(M), n = static_cast<int>(N), k = static_cast<int>(K);
   if (bits == 4) {
-    if (group_size == 32) return launch<4, 32>(x, m, wq, s, b, bias, n, k, y, st);
-    if (group_size == 64) return launch<4, 64>(x, m, wq, s, b, bias, n, k, y, st);
-    return launch<4, 128>(x, m, wq, s, b, bias, n, k, y, st);
+    if (group_size == 32) return launch_cfg<4, 32>(x, m, wq, s, b, bias, n, k, y, st);
+    if (group_size == 64) return launch_cfg<4, 64>(x, m, wq, s, b, bias, n, k, y, st);
+    return launch_cfg<4, 128>(x, m, wq, s, b, bias, n, k, y, st);
   }
-  if (group_size == 32) return launch<8, 32>(x, m, wq, s, b, bias, n, k, y, st);
-  if (group_size == 64) return launch<8, 64>(x, m, wq, s, b, bias, n, k, y, st);
-  return launch<8, 128>(x, m, wq, s, b, bias, n, k, y, st);
+  if (group_size == 32) return launch_cfg<8, 32>(x, m, wq, s, b, bias, n, k, y, st);
+  if (group_size == 64) return launch_cfg<8, 64>(x, m, wq, s, b, bias, n, k, y, st);
+  return launch_cfg<8, 128>(x, m, wq, s, b, bias, n, k, y, st);
 }
 
 }  // namespace mlxq
