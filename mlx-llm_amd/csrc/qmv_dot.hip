@@ -25,6 +25,9 @@
 //    order (deterministic), then bf16 y (+ bias) is stored.
 #include <hip/hip_runtime.h>
 
+#include <cstdio>
+#include <cstdlib>
+
 #include "common.hpp"
 #include "qmatmul.hpp"
 
@@ -33,8 +36,7 @@ namespace {
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kWaves = 8;
-constexpr int kThreads = kWaves * 64;
+constexpr int kMaxWaves = 8;  // waves per workgroup: 4 or 8 (chosen per shape)
 
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
@@ -92,9 +94,10 @@ __device__ __forceinline__ float pick_param(const uint32_t* v, int base, int j) 
   }
 }
 
-// PT: activation pieces (8 bf16 each) per thread in the LDS prologue.
-template <int BITS, int GS, int MV, int SUB, int RC, int PT>
-__global__ __launch_bounds__(kThreads) void qmv_dot_kernel(const uint16_t* __restrict__ x,
+// PT: activation pieces (8 bf16 each) per thread in the LDS prologue;
+// WV: waves per workgroup.
+template <int BITS, int GS, int MV, int SUB, int RC, int PT, int WV>
+__global__ __launch_bounds__(64 * WV) void qmv_dot_kernel(const uint16_t* __restrict__ x,
                                                             const uint32_t* __restrict__ wq,
                                                             const uint16_t* __restrict__ scales,
                                                             const uint16_t* __restrict__ biases,
@@ -108,7 +111,7 @@ __global__ __launch_bounds__(kThreads) void qmv_dot_kernel(const uint16_t* __res
   extern __shared__ __align__(16) uint8_t smem[];
   uint16_t* xl = reinterpret_cast<uint16_t*>(smem);                   // [MV][K] bf16 (pair order)
   float* xsum = reinterpret_cast<float*>(smem + MV * K * 2);           // [MV][K / KL]
-  float* red = xsum + MV * (K / Gm::KL);                               // [kWaves][MV][R]
+  float* red = xsum + MV * (K / Gm::KL);                               // [WV][MV][R]
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -145,8 +148,7 @@ __global__ __launch_bounds__(kThreads) void qmv_dot_kernel(const uint16_t* __res
   // Every load is unconditional, with indices clamped into the wave's full
   // rounds (a wave without one clamps to chunk 0): straight-line code, so the
   // compiler's waits stay exact and the round stays in registers (all
-  // register indices are compile-time).  The one prefetch past the last round
-  // re-reads an already cached round and is never used.
+  // register indices are compile-time).
   auto fetch = [&](Rnd& T, int c0) {
     c0 = max(min(c0, cfull - RC), 0);
     const int g0 = c0 * Gm::NGC / Gm::CPG;
@@ -255,12 +257,19 @@ __global__ __launch_bounds__(kThreads) void qmv_dot_kernel(const uint16_t* __res
     }
   };
 
-  // 4) full rounds of RC chunks, the next one always in flight
-  for (int c0 = cbeg; c0 + RC <= cfull; c0 += RC) {
-    fetch(nxt, c0 + RC);
-    __builtin_amdgcn_sched_barrier(0);  // next round in flight before this one is computed
+  // 4) full rounds of RC chunks, the next one in flight while one is
+  //    computed; the last round is peeled so that nothing is fetched past
+  //    the wave's range (a wasted fetch would add a memory round trip to
+  //    the end of every wave)
+  if (cfull > cbeg) {
+    int c0 = cbeg;
+    for (; c0 + RC < cfull; c0 += RC) {
+      fetch(nxt, c0 + RC);
+      __builtin_amdgcn_sched_barrier(0);  // next round in flight before this one is computed
+      compute(cur, c0);
+      cur = nxt;
+    }
     compute(cur, c0);
-    cur = nxt;
   }
   // ragged end of the wave's range (< RC chunks): each lane gathers its own
   // group's parameters
@@ -296,12 +305,12 @@ __global__ __launch_bounds__(kThreads) void qmv_dot_kernel(const uint16_t* __res
       if (gq == 0) red[(wave * MV + m) * R + 16 * s + r16] = v;
     }
   __syncthreads();
-  for (int i = tid; i < MV * R; i += kThreads) {
+  for (int i = tid; i < MV * R; i += 64 * WV) {
     const int m = i / R, r = i % R, n = n0 + r;
     if (n >= N) continue;
     float sum = red[m * R + r];
 #pragma unroll
-    for (int wv = 1; wv < kWaves; wv++) sum += red[(wv * MV + m) * R + r];
+    for (int wv = 1; wv < WV; wv++) sum += red[(wv * MV + m) * R + r];
     if (bias_vec) sum += bf16_bits_to_f32(bias_vec[n]);
     y[static_cast<int64_t>(m) * N + n] = static_cast<uint16_t>(f32_to_bf16_bits(sum));
   }
@@ -309,70 +318,127 @@ __global__ __launch_bounds__(kThreads) void qmv_dot_kernel(const uint16_t* __res
 
 constexpr int kRound = 4;  // chunks per round
 
-// Pieces (8 activations) per thread in the prologue: whole segments, <= 8.
-int prologue_pieces(int64_t M, int64_t K, int bits) {
+// Pieces (8 activations) per thread in the prologue: whole segments.
+int prologue_pieces(int64_t M, int64_t K, int bits, int wv) {
   const int64_t segp = 64 * 8 / bits / 4 / 8;
-  int64_t pt = ceil_div(M * K / 8, kThreads);
+  int64_t pt = ceil_div(M * K / 8, 64 * wv);
   pt = ceil_div(std::max<int64_t>(pt, segp), segp) * segp;
   return static_cast<int>(pt);
 }
 
-template <int BITS, int GS, int MV, int SUB, int PT>
-int launch(int64_t row_tiles, size_t lds, int cw, const uint16_t* x, const uint32_t* wq, const uint16_t* s,
-           const uint16_t* b, const uint16_t* bias, int N, int K, uint16_t* y, hipStream_t st) {
-  auto kern = qmv_dot_kernel<BITS, GS, MV, SUB, kRound, PT>;
-  if (lds > 64 * 1024) {
-    static bool raised = false;  // once per process; the attribute is per function
-    if (!raised) {
-      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-      if (e != hipSuccess) return fail(MLXQ_ERR_DEVICE, std::string("qmv_dot: LDS size: ") + hipGetErrorString(e));
-      raised = true;
-    }
+struct DotArgs {
+  const uint16_t* x;
+  const uint32_t* wq;
+  const uint16_t *s, *b, *bias;
+  int N, K;
+  uint16_t* y;
+  hipStream_t st;
+};
+
+struct DotCfg {
+  int sub = 1, wv = 8, pt = 0, cw = 0;
+  int64_t tiles = 0;
+  size_t lds = 0;
+};
+
+// query: report resident workgroups per CU for this configuration instead of
+// launching (the choice between configurations needs it).
+template <int BITS, int GS, int MV, int SUB, int PT, int WV>
+int run(const DotCfg& c, const DotArgs& a, int* query) {
+  auto kern = qmv_dot_kernel<BITS, GS, MV, SUB, kRound, PT, WV>;
+  static bool raised = false;  // once per process; the attribute is per function
+  if (c.lds > 64 * 1024 && !raised) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (e != hipSuccess) return fail(MLXQ_ERR_DEVICE, std::string("qmv_dot: LDS size: ") + hipGetErrorString(e));
+    raised = true;
   }
-  hipLaunchKernelGGL(kern, dim3(row_tiles), dim3(kThreads), lds, st, x, wq, s, b, bias, N, K, cw, y);
+  if (query) {
+    static int cached = -1;  // the kernel's registers fix it; LDS is checked per call below
+    static size_t cached_lds = 0;
+    if (cached < 0 || cached_lds != c.lds) {
+      int nb = 0;
+      hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void*>(kern), 64 * WV,
+                                                                  c.lds);
+      if (e != hipSuccess) return fail(MLXQ_ERR_DEVICE, std::string("qmv_dot: occupancy: ") + hipGetErrorString(e));
+      cached = nb;
+      cached_lds = c.lds;
+    }
+    *query = cached;
+    return MLXQ_OK;
+  }
+  hipLaunchKernelGGL(kern, dim3(c.tiles), dim3(64 * WV), c.lds, a.st, a.x, a.wq, a.s, a.b, a.bias, a.N, a.K, c.cw, a.y);
   return check_launch("qmv_dot");
 }
 
-template <int BITS, int GS, int MV, int SUB>
-int launch_pt(int pt, int64_t row_tiles, size_t lds, int cw, const uint16_t* x, const uint32_t* wq,
-              const uint16_t* s, const uint16_t* b, const uint16_t* bias, int N, int K, uint16_t* y,
-              hipStream_t st) {
+template <int BITS, int GS, int MV, int SUB, int WV>
+int run_pt(const DotCfg& c, const DotArgs& a, int* q) {
   constexpr int SEGP = 64 * 8 / BITS / 4 / 8;
-  if (pt <= SEGP) return launch<BITS, GS, MV, SUB, SEGP>(row_tiles, lds, cw, x, wq, s, b, bias, N, K, y, st);
-  if (pt <= 2 * SEGP) return launch<BITS, GS, MV, SUB, 2 * SEGP>(row_tiles, lds, cw, x, wq, s, b, bias, N, K, y, st);
+  if (c.pt <= SEGP) return run<BITS, GS, MV, SUB, SEGP, WV>(c, a, q);
+  if (c.pt <= 2 * SEGP) return run<BITS, GS, MV, SUB, 2 * SEGP, WV>(c, a, q);
   if constexpr (4 * SEGP <= 8) {
-    if (pt <= 4 * SEGP) return launch<BITS, GS, MV, SUB, 4 * SEGP>(row_tiles, lds, cw, x, wq, s, b, bias, N, K, y, st);
+    if (c.pt <= 4 * SEGP) return run<BITS, GS, MV, SUB, 4 * SEGP, WV>(c, a, q);
   }
   return fail(MLXQ_ERR_INVALID, "qmv_dot: activation prologue too large");
 }
 
-template <int BITS, int GS, int SUB>
-int launch_m(int64_t M, int pt, int64_t row_tiles, size_t lds, int cw, const uint16_t* x, const uint32_t* wq,
-             const uint16_t* s, const uint16_t* b, const uint16_t* bias, int N, int K, uint16_t* y,
-             hipStream_t st) {
+template <int BITS, int GS, int SUB, int WV>
+int run_m(int64_t M, const DotCfg& c, const DotArgs& a, int* q) {
   switch (M) {
-    case 1: return launch_pt<BITS, GS, 1, SUB>(pt, row_tiles, lds, cw, x, wq, s, b, bias, N, K, y, st);
-    case 2: return launch_pt<BITS, GS, 2, SUB>(pt, row_tiles, lds, cw, x, wq, s, b, bias, N, K, y, st);
-    case 3: return launch_pt<BITS, GS, 3, SUB>(pt, row_tiles, lds, cw, x, wq, s, b, bias, N, K, y, st);
-    default: return launch_pt<BITS, GS, 4, SUB>(pt, row_tiles, lds, cw, x, wq, s, b, bias, N, K, y, st);
+    case 1: return run_pt<BITS, GS, 1, SUB, WV>(c, a, q);
+    case 2: return run_pt<BITS, GS, 2, SUB, WV>(c, a, q);
+    case 3: return run_pt<BITS, GS, 3, SUB, WV>(c, a, q);
+    default: return run_pt<BITS, GS, 4, SUB, WV>(c, a, q);
   }
 }
 
 template <int BITS, int GS>
-int launch_sub(int sub, int64_t M, int pt, int64_t row_tiles, size_t lds, int cw, const uint16_t* x,
-               const uint32_t* wq, const uint16_t* s, const uint16_t* b, const uint16_t* bias, int N, int K,
-               uint16_t* y, hipStream_t st) {
-  if (sub == 1) return launch_m<BITS, GS, 1>(M, pt, row_tiles, lds, cw, x, wq, s, b, bias, N, K, y, st);
-  return launch_m<BITS, GS, 2>(M, pt, row_tiles, lds, cw, x, wq, s, b, bias, N, K, y, st);
+int run_cfg(int64_t M, const DotCfg& c, const DotArgs& a, int* q) {
+  if (c.sub == 1) return c.wv == 4 ? run_m<BITS, GS, 1, 4>(M, c, a, q) : run_m<BITS, GS, 1, 8>(M, c, a, q);
+  return c.wv == 4 ? run_m<BITS, GS, 2, 4>(M, c, a, q) : run_m<BITS, GS, 2, 8>(M, c, a, q);
+}
+
+int dispatch(int64_t M, int group_size, int bits, const DotCfg& c, const DotArgs& a, int* q) {
+  if (bits == 4) {
+    if (group_size == 32) return run_cfg<4, 32>(M, c, a, q);
+    if (group_size == 64) return run_cfg<4, 64>(M, c, a, q);
+    return run_cfg<4, 128>(M, c, a, q);
+  }
+  if (group_size == 32) return run_cfg<8, 32>(M, c, a, q);
+  if (group_size == 64) return run_cfg<8, 64>(M, c, a, q);
+  return run_cfg<8, 128>(M, c, a, q);
+}
+
+size_t lds_bytes(int64_t M, int64_t K, int bits, int sub, int wv) {
+  const int64_t kl = 64 * 8 / bits / 4;
+  return static_cast<size_t>(M * K * 2 + M * (K / kl) * 4 + wv * M * 16 * sub * 4);
+}
+
+DotCfg make_cfg(int64_t M, int64_t N, int64_t K, int bits, int sub, int wv) {
+  DotCfg c;
+  c.sub = sub;
+  c.wv = wv;
+  c.pt = prologue_pieces(M, K, bits, wv);
+  c.tiles = ceil_div(N, 16 * sub);
+  c.lds = lds_bytes(M, K, bits, sub, wv);
+  // each wave owns a contiguous range of whole rounds of chunks
+  const int64_t chunks = K * bits / 8 / 64;
+  c.cw = static_cast<int>(ceil_div(ceil_div(chunks, wv), kRound) * kRound);
+  return c;
+}
+
+bool cfg_ok(const DotCfg& c) { return c.pt <= 8 && c.lds <= 160 * 1024; }
+
+int cu_count() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) return 256;
+  return cus;
 }
 
 }  // namespace
 
-size_t qmv_dot_lds_bytes(int64_t M, int64_t K, int bits, int sub) {
-  const int64_t kl = 64 * 8 / bits / 4;
-  return static_cast<size_t>(M * K * 2 + M * (K / kl) * 4 + kWaves * M * 16 * sub * 4);
-}
+size_t qmv_dot_lds_bytes(int64_t M, int64_t K, int bits, int sub) { return lds_bytes(M, K, bits, sub, kMaxWaves); }
 
 bool qmv_dot_eligible(int64_t M, int64_t N, int64_t K, int group_size, int bits) {
   if (M < 1 || M > kQmvDotMaxM) return false;
@@ -380,31 +446,39 @@ bool qmv_dot_eligible(int64_t M, int64_t N, int64_t K, int group_size, int bits)
   const int64_t gb = static_cast<int64_t>(group_size) * bits / 8;
   const int64_t ngr = kRound * (gb >= 64 ? 1 : 64 / gb) / (gb > 64 ? gb / 64 : 1);  // groups per round
   if ((K / group_size) % std::min<int64_t>(ngr, 8)) return false;  // aligned vector loads of round params
-  if (prologue_pieces(M, K, bits) > 8) return false;                // activations staged through registers
-  (void)N;
-  return qmv_dot_lds_bytes(M, K, bits, 2) <= 160 * 1024;
+  return cfg_ok(make_cfg(M, N, K, bits, 2, kMaxWaves));             // activations staged through registers
 }
 
 int launch_qmv_dot(const uint16_t* x, int64_t M, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
                    const uint16_t* bias, int64_t N, int64_t K, int group_size, int bits, uint16_t* y,
                    hipStream_t st) {
-  // 16 rows per workgroup while that keeps <= ~2 workgroups per CU, else 32
-  const int sub = ceil_div(N, 16) > 512 ? 2 : 1;
-  const int64_t row_tiles = ceil_div(N, 16 * sub);
-  const size_t lds = qmv_dot_lds_bytes(M, K, bits, sub);
-  // each wave owns a contiguous range of whole rounds of chunks
-  const int64_t chunks = K * bits / 8 / 64;
-  const int cw = static_cast<int>(ceil_div(ceil_div(chunks, kWaves), kRound) * kRound);
-  const int pt = prologue_pieces(M, K, bits);
-  const int n = static_cast<int>(N), k = static_cast<int>(K);
-  if (bits == 4) {
-    if (group_size == 32) return launch_sub<4, 32>(sub, M, pt, row_tiles, lds, cw, x, wq, s, b, bias, n, k, y, st);
-    if (group_size == 64) return launch_sub<4, 64>(sub, M, pt, row_tiles, lds, cw, x, wq, s, b, bias, n, k, y, st);
-    return launch_sub<4, 128>(sub, M, pt, row_tiles, lds, cw, x, wq, s, b, bias, n, k, y, st);
-  }
-  if (group_size == 32) return launch_sub<8, 32>(sub, M, pt, row_tiles, lds, cw, x, wq, s, b, bias, n, k, y, st);
-  if (group_size == 64) return launch_sub<8, 64>(sub, M, pt, row_tiles, lds, cw, x, wq, s, b, bias, n, k, y, st);
-  return launch_sub<8, 128>(sub, M, pt, row_tiles, lds, cw, x, wq, s, b, bias, n, k, y, st);
+  const DotArgs a{x, wq, s, b, bias, static_cast<int>(N), static_cast<int>(K), y, st};
+  // Pick rows per workgroup (16 or 32) and waves per workgroup (4 or 8) so
+  // that the whole grid is resident at once (no second, partly filled pass
+  // of workgroups), preferring the most waves in flight.
+  static const int cus = cu_count();
+  DotCfg best;
+  int64_t best_pass = -1, best_waves = 0;
+  int forced_sub = 0, forced_wv = 0;
+  if (const char* e = getenv("MLXQ_QMV_DOT")) sscanf(e, "%d,%d", &forced_sub, &forced_wv);
+  for (int sub = 1; sub <= 2; sub++)
+    for (int wv = 4; wv <= 8; wv += 4) {
+      if ((forced_sub && sub != forced_sub) || (forced_wv && wv != forced_wv)) continue;
+      const DotCfg c = make_cfg(M, N, K, bits, sub, wv);
+      if (!cfg_ok(c)) continue;
+      int nb = 0;
+      if (int rc = dispatch(M, group_size, bits, c, a, &nb)) return rc;
+      const int64_t slots = std::max<int64_t>(1, static_cast<int64_t>(nb) * cus);
+      const int64_t pass = ceil_div(c.tiles, slots);
+      const int64_t waves = std::min(c.tiles, slots) * wv;
+      if (best_pass < 0 || pass < best_pass || (pass == best_pass && waves > best_waves)) {
+        best = c;
+        best_pass = pass;
+        best_waves = waves;
+      }
+    }
+  if (best_pass < 0) return fail(MLXQ_ERR_INVALID, "qmv_dot: no configuration fits this shape");
+  return dispatch(M, group_size, bits, best, a, nullptr);
 }
 
 }  // namespace mlxq
