@@ -119,6 +119,35 @@ int mlxq_qmatmul_algo(const void* x, int64_t M, const uint32_t* wq,
                       size_t workspace_bytes, int algo, void* stream);
 
 /* ------------------------------------------------------------------ */
+/* Decode layer chain around the projections (bf16, MLX rounding points) */
+/* ------------------------------------------------------------------ */
+
+/* Replaces mlx_rs::fast::rms_norm reached from primitives::nn::rms_norm
+ * (src/primitives/nn.rs:35-37), applied before q/k/v and gate/up
+ * (src/models/llama.rs:698,728) and before lm_head (:596).
+ * x, y: [rows, dim] bf16; weight: [dim] bf16; dim % 8 == 0.
+ * y = bf16(weight * bf16(x * 1/sqrt(mean(x^2) + eps))), sums in f32. */
+int mlxq_rms_norm(const void* x, const void* weight, int64_t rows, int64_t dim,
+                  float eps, void* y, void* stream);
+
+/* Replaces silu(gate) followed by multiply(gate, up) in LlamaMlp::forward
+ * (src/models/llama.rs:1040-1045; silu at src/primitives/nn.rs:50-52).
+ * n bf16 elements (n % 8 == 0):
+ * y = bf16(bf16(g * bf16(1/(1+exp(-g)))) * u). */
+int mlxq_silu_mul(const void* gate, const void* up, int64_t n, void* y,
+                  void* stream);
+
+/* Replaces the residual add(x, attn) / add(h, ffn)
+ * (src/models/llama.rs:729-733): y = bf16(a + b), n % 8 == 0. */
+int mlxq_add(const void* a, const void* b, int64_t n, void* y, void* stream);
+
+/* Replaces repeat_kv (src/primitives/attention.rs:45-55) for one position:
+ * x [rows, kv_heads, head_dim] -> y [rows, kv_heads*groups, head_dim], output
+ * head h = KV head h / groups.  head_dim % 8 == 0. */
+int mlxq_repeat_kv(const void* x, int64_t rows, int kv_heads, int head_dim,
+                   int groups, void* y, void* stream);
+
+/* ------------------------------------------------------------------ */
 /* GGUF block dequantization                                           */
 /* ------------------------------------------------------------------ */
 

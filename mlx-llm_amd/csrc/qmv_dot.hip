@@ -143,14 +143,15 @@ __global__ __launch_bounds__(64 * WV) void qmv_dot_kernel(const uint16_t* __rest
     srow[s] = scales + static_cast<int64_t>(n) * G;
     brow[s] = biases + static_cast<int64_t>(n) * G;
   }
-  const int cbeg = wave * cw, cend = min(chunks, cbeg + cw);
-  const int cfull = cbeg + (max(cend - cbeg, 0) / RC) * RC;  // end of the wave's full rounds
-  // Every load is unconditional, with indices clamped into the wave's full
-  // rounds (a wave without one clamps to chunk 0): straight-line code, so the
-  // compiler's waits stay exact and the round stays in registers (all
-  // register indices are compile-time).
+  // The wave's chunk range [cbeg, cend) lies inside the row; its full rounds
+  // end at cfull.  A round is fetched only when it ends at or before cfull,
+  // so every load stays inside the row.  A wave whose range holds no full
+  // round fetches none (the branches on cfull are wave-uniform).  Inside
+  // fetch all register indices are compile-time, so a round stays in
+  // registers.
+  const int cbeg = min(wave * cw, chunks), cend = min(chunks, cbeg + cw);
+  const int cfull = cbeg + ((cend - cbeg) / RC) * RC;  // end of the wave's full rounds
   auto fetch = [&](Rnd& T, int c0) {
-    c0 = max(min(c0, cfull - RC), 0);
     const int g0 = c0 * Gm::NGC / Gm::CPG;
 #pragma unroll
     for (int s = 0; s < SUB; s++) {
@@ -163,7 +164,7 @@ __global__ __launch_bounds__(64 * WV) void qmv_dot_kernel(const uint16_t* __rest
       for (int s = 0; s < SUB; s++) T.w[u][s] = wrow[s][static_cast<int64_t>(c0 + u) * 4];
   };
   Rnd cur, nxt;
-  fetch(cur, cbeg);
+  if (cfull > cbeg) fetch(cur, cbeg);
   __builtin_amdgcn_sched_barrier(0);  // the whole first round is in flight before the prologue
 
   // 3) activations -> LDS in the Q4 pair order, plus per-segment sums

@@ -42,6 +42,10 @@ SIGNATURES = {
     "mlxq_qmatmul_workspace_size": (ctypes.c_int, [_i64, _i64, _i64, ctypes.c_int, ctypes.c_int, ctypes.POINTER(_sz)]),
     "mlxq_qmatmul": (ctypes.c_int, [_vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, ctypes.c_int, ctypes.c_int, _vp, _vp, _sz, _vp]),
     "mlxq_qmatmul_algo": (ctypes.c_int, [_vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, ctypes.c_int, ctypes.c_int, _vp, _vp, _sz, ctypes.c_int, _vp]),
+    "mlxq_rms_norm": (ctypes.c_int, [_vp, _vp, _i64, _i64, ctypes.c_float, _vp, _vp]),
+    "mlxq_silu_mul": (ctypes.c_int, [_vp, _vp, _i64, _vp, _vp]),
+    "mlxq_add": (ctypes.c_int, [_vp, _vp, _i64, _vp, _vp]),
+    "mlxq_repeat_kv": (ctypes.c_int, [_vp, _i64, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp, _vp]),
     "mlxq_gguf_block": (ctypes.c_int, [_u32, ctypes.POINTER(_i64), ctypes.POINTER(_i64)]),
     "mlxq_gguf_tensor_byte_len": (ctypes.c_int, [_u32, _i64, ctypes.POINTER(_i64)]),
     "mlxq_gguf_dequantize": (ctypes.c_int, [_u32, _vp, _i64, _i64, ctypes.c_int, _vp, _vp]),
@@ -203,6 +207,40 @@ def bind_qmatmul(x, wq, scales, biases, group_size: int = 64, bits: int = 4, out
     call.out = y
     call.workspace = ws
     return call
+
+
+def rms_norm(x, weight, eps: float, out=None):
+    """MLX fast::rms_norm over the last axis (bf16)."""
+    torch = _torch()
+    d = x.shape[-1]
+    y = out if out is not None else torch.empty_like(x)
+    check(lib().mlxq_rms_norm(_ptr(x), _ptr(weight), x.numel() // d, d, eps, _ptr(y), _stream()))
+    return y
+
+
+def silu_mul(gate, up, out=None):
+    """silu(gate) * up with MLX's bf16 rounding points."""
+    torch = _torch()
+    y = out if out is not None else torch.empty_like(gate)
+    check(lib().mlxq_silu_mul(_ptr(gate), _ptr(up), gate.numel(), _ptr(y), _stream()))
+    return y
+
+
+def add(a, b, out=None):
+    torch = _torch()
+    y = out if out is not None else torch.empty_like(a)
+    check(lib().mlxq_add(_ptr(a), _ptr(b), a.numel(), _ptr(y), _stream()))
+    return y
+
+
+def repeat_kv(x, kv_heads: int, head_dim: int, groups: int, out=None):
+    """x [rows, kv_heads*head_dim] -> [rows, kv_heads*groups*head_dim] (heads repeated in place)."""
+    torch = _torch()
+    rows = x.numel() // (kv_heads * head_dim)
+    y = out if out is not None else torch.empty((rows, kv_heads * groups * head_dim), dtype=x.dtype,
+                                                device=x.device)
+    check(lib().mlxq_repeat_kv(_ptr(x), rows, kv_heads, head_dim, groups, _ptr(y), _stream()))
+    return y
 
 
 def gguf_block(tag: int):

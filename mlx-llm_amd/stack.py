@@ -1,0 +1,192 @@
+"""Quantized Llama decode stack over the mlxq C ABI.
+
+The layer chain of the reference's CausalLm decode step
+(src/models/llama.rs:689-735 per layer, q/k/v/o at :806-835, the MLP at
+:1040-1045, final norm + lm_head at :595-603) with every projection
+quantized (Q4/Q8, MLX affine layout) and attention replaced by the identity
+on v, its 8 KV heads repeated to the 32 query heads (the attention of a
+single cached position).  Only the quantized GEMV/GEMM path and the bf16
+ops around it run:
+
+    n1 = rms_norm(x, ln1);  q, k, v = n1 Wq^T, n1 Wk^T, n1 Wv^T
+    h  = x + repeat_kv(v) Wo^T
+    n2 = rms_norm(h, ln2);  x' = h + (silu(n2 Wg^T) * (n2 Wu^T)) Wd^T
+    logits = rms_norm(x_L, norm) Wlm^T
+
+Every op is a libmlxq kernel; torch provides device memory, streams and
+graph capture.  The lm_head is quantized too (the reference keeps it dense,
+src/models/llama.rs:122-128; the benchmark configuration asks for Q4).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import mlxq
+
+PROJ = ("q", "k", "v", "o", "gate", "up", "down")
+
+
+@dataclass
+class StackConfig:
+    layers: int = 32
+    hidden: int = 4096
+    intermediate: int = 14336
+    heads: int = 32
+    kv_heads: int = 8
+    head_dim: int = 128
+    vocab: int = 128256
+    eps: float = 1e-5
+    group_size: int = 64
+    bits: int = 4
+
+    @property
+    def groups(self) -> int:
+        return self.heads // self.kv_heads
+
+    def proj_shape(self, name: str) -> tuple[int, int]:
+        """(out N, in K) of a projection (Hugging Face [out, in] layout)."""
+        h, i, q, kv = self.hidden, self.intermediate, self.heads * self.head_dim, self.kv_heads * self.head_dim
+        return {"q": (q, h), "k": (kv, h), "v": (kv, h), "o": (h, q), "gate": (i, h), "up": (i, h),
+                "down": (h, i), "lm_head": (self.vocab, h)}[name]
+
+    def as_dict(self) -> dict:
+        return dict(layers=self.layers, hidden=self.hidden, intermediate=self.intermediate, heads=self.heads,
+                    kv_heads=self.kv_heads, head_dim=self.head_dim, vocab=self.vocab, eps=self.eps,
+                    group_size=self.group_size, bits=self.bits)
+
+
+def llama3_8b(**kw) -> StackConfig:
+    return StackConfig(**kw)
+
+
+@dataclass
+class QLinear:
+    """A quantized projection in MLX's packed layout (all device tensors)."""
+    wq: object
+    scales: object
+    biases: object
+    n: int
+    k: int
+
+    def bytes(self) -> int:
+        return self.wq.numel() * 4 + self.scales.numel() * 2 + self.biases.numel() * 2
+
+
+@dataclass
+class Layer:
+    proj: dict = field(default_factory=dict)
+    ln1: object = None
+    ln2: object = None
+
+
+class DecodeStack:
+    """Random-init quantized Llama stack (seeded N(0, 0.02) weights quantized on
+    device) with preallocated activations for a fixed batch, so one decode step
+    can be captured in a HIP graph and replayed."""
+
+    def __init__(self, cfg: StackConfig, batch: int = 1, seed: int = 0, device="cuda", norm_noise: float = 0.0):
+        import torch
+        self.cfg, self.batch, self.device = cfg, batch, torch.device(device)
+        g = torch.Generator(device=self.device)
+
+        def qlin(name, idx):
+            n, k = cfg.proj_shape(name)
+            g.manual_seed(seed * 1_000_003 + idx)
+            w = (torch.randn((n, k), generator=g, device=self.device) * 0.02).to(torch.bfloat16)
+            wq, s, b = mlxq.quantize(w, cfg.group_size, cfg.bits)
+            del w
+            return QLinear(wq, s, b, n, k)
+
+        def norm_w(idx):
+            w = torch.ones(cfg.hidden, device=self.device)
+            if norm_noise:
+                g.manual_seed(seed * 1_000_003 + idx)
+                w = w + norm_noise * torch.randn(cfg.hidden, generator=g, device=self.device)
+            return w.to(torch.bfloat16)
+
+        self.layers = []
+        idx = 0
+        for _ in range(cfg.layers):
+            L = Layer()
+            for p in PROJ:
+                L.proj[p] = qlin(p, idx)
+                idx += 1
+            L.ln1, L.ln2 = norm_w(idx), norm_w(idx + 1)
+            idx += 2
+            self.layers.append(L)
+        self.norm = norm_w(idx)
+        self.lm_head = qlin("lm_head", idx + 1)
+
+        M, bf = batch, torch.bfloat16
+        e = lambda n: torch.empty((M, n), dtype=bf, device=self.device)  # noqa: E731
+        q_dim, kv_dim = cfg.heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
+        self.x = e(cfg.hidden)          # step input (hidden state entering layer 0)
+        self.xa, self.xb = e(cfg.hidden), e(cfg.hidden)  # residual stream ping-pong
+        self.n = e(cfg.hidden)
+        self.h = e(cfg.hidden)
+        self.q, self.k, self.v = e(q_dim), e(kv_dim), e(kv_dim)
+        self.attn = e(q_dim)
+        self.o = e(cfg.hidden)
+        self.g, self.u, self.a = e(cfg.intermediate), e(cfg.intermediate), e(cfg.intermediate)
+        self.d = e(cfg.hidden)
+        self.logits = e(cfg.vocab)
+
+    def weight_bytes(self) -> int:
+        """Packed weight bytes one decode step streams (codes + scales + biases)."""
+        return sum(p.bytes() for L in self.layers for p in L.proj.values()) + self.lm_head.bytes()
+
+    def _lin(self, x, p: QLinear, out):
+        return mlxq.qmatmul(x, p.wq, p.scales, p.biases, self.cfg.group_size, self.cfg.bits, out=out)
+
+    def forward(self):
+        """One decode step on the current stream: self.x -> self.logits."""
+        c = self.cfg
+        x = self.x
+        for i, L in enumerate(self.layers):
+            P = L.proj
+            mlxq.rms_norm(x, L.ln1, c.eps, out=self.n)
+            self._lin(self.n, P["q"], self.q)
+            self._lin(self.n, P["k"], self.k)
+            self._lin(self.n, P["v"], self.v)
+            mlxq.repeat_kv(self.v, c.kv_heads, c.head_dim, c.groups, out=self.attn)
+            self._lin(self.attn, P["o"], self.o)
+            mlxq.add(x, self.o, out=self.h)
+            mlxq.rms_norm(self.h, L.ln2, c.eps, out=self.n)
+            self._lin(self.n, P["gate"], self.g)
+            self._lin(self.n, P["up"], self.u)
+            mlxq.silu_mul(self.g, self.u, out=self.a)
+            self._lin(self.a, P["down"], self.d)
+            x = self.xa if i % 2 == 0 else self.xb
+            mlxq.add(self.h, self.d, out=x)
+        mlxq.rms_norm(x, self.norm, c.eps, out=self.n)
+        self._lin(self.n, self.lm_head, self.logits)
+        return self.logits
+
+    def capture(self):
+        """Capture forward() in a HIP graph; returns the graph (replay() runs one step)."""
+        import torch
+        s = torch.cuda.Stream(device=self.device)
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            self.forward()  # warm-up outside the capture (kernel attributes, occupancy queries)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            self.forward()
+        torch.cuda.synchronize()
+        return graph
+
+    def host_weights(self):
+        """Packed weights as numpy (uint32 codes, bf16 bits) for a CPU checker."""
+        import numpy as np
+        import torch
+
+        def h16(t):
+            return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+        def hq(p: QLinear):
+            return (p.wq.cpu().numpy().view(np.uint32), h16(p.scales), h16(p.biases))
+
+        layers = [dict({k: hq(v) for k, v in L.proj.items()}, ln1=h16(L.ln1), ln2=h16(L.ln2)) for L in self.layers]
+        return layers, h16(self.norm), hq(self.lm_head)

@@ -770,3 +770,60 @@ int orc_qmatmul_f64(const uint16_t* x, int64_t M, const uint32_t* wq,
   return 0;
 }
 
+
+/* ---------------------------------------------------------------- decode layer chain
+ * bf16 ops around the projections, at MLX's rounding points. */
+
+static float bf16_round(float f) { return orc_bf16_to_f32(orc_f32_to_bf16(f)); }
+
+/* src/primitives/nn.rs:35-37 -> mlx fast::rms_norm: the f32 row statistic,
+ * x * inv rounded to bf16, then the weight product rounded to bf16. */
+int orc_rms_norm_bf16(const uint16_t* x, const uint16_t* w, int64_t rows, int64_t dim,
+                      float eps, uint16_t* y) {
+  if (rows < 0 || dim <= 0) return 1;
+  for (int64_t r = 0; r < rows; r++) {
+    const uint16_t* xr = x + r * dim;
+    double ss = 0.0;
+    for (int64_t i = 0; i < dim; i++) {
+      double v = (double)orc_bf16_to_f32(xr[i]);
+      ss += v * v;
+    }
+    const float inv = (float)(1.0 / sqrt((double)(float)(ss / (double)dim) + (double)eps));
+    for (int64_t i = 0; i < dim; i++) {
+      float n = bf16_round(orc_bf16_to_f32(xr[i]) * inv);
+      y[r * dim + i] = orc_f32_to_bf16(orc_bf16_to_f32(w[i]) * n);
+    }
+  }
+  return 0;
+}
+
+/* src/models/llama.rs:1040-1045 (silu at src/primitives/nn.rs:50-52, then
+ * multiply): sigmoid, g * sigmoid and the product with up each rounded to bf16. */
+int orc_silu_mul_bf16(const uint16_t* g, const uint16_t* u, int64_t n, uint16_t* y) {
+  if (n < 0) return 1;
+  for (int64_t i = 0; i < n; i++) {
+    float gv = orc_bf16_to_f32(g[i]);
+    float s = bf16_round(1.0f / (1.0f + expf(-gv)));
+    float a = bf16_round(gv * s);
+    y[i] = orc_f32_to_bf16(a * orc_bf16_to_f32(u[i]));
+  }
+  return 0;
+}
+
+/* residual add (src/models/llama.rs:729-733): bf16(a + b). */
+int orc_add_bf16(const uint16_t* a, const uint16_t* b, int64_t n, uint16_t* y) {
+  if (n < 0) return 1;
+  for (int64_t i = 0; i < n; i++) y[i] = orc_f32_to_bf16(orc_bf16_to_f32(a[i]) + orc_bf16_to_f32(b[i]));
+  return 0;
+}
+
+/* repeat_kv (src/primitives/attention.rs:45-55) for one position: output
+ * head h = KV head h / groups. */
+int orc_repeat_kv(const uint16_t* x, int64_t rows, int kv_heads, int head_dim, int groups, uint16_t* y) {
+  if (rows < 0 || kv_heads <= 0 || head_dim <= 0 || groups <= 0) return 1;
+  int64_t in_row = (int64_t)kv_heads * head_dim, out_row = in_row * groups;
+  for (int64_t r = 0; r < rows; r++)
+    for (int64_t h = 0; h < (int64_t)kv_heads * groups; h++)
+      memcpy(y + r * out_row + h * head_dim, x + r * in_row + (h / groups) * head_dim, (size_t)head_dim * 2);
+  return 0;
+}

@@ -84,6 +84,18 @@ int orc_qmatmul_f32(const uint16_t* x, int64_t M, const uint32_t* wq,
 int orc_gguf_dequantize_mt(uint32_t tag, const uint8_t* data, int64_t data_len,
                            int64_t n, float* out, int threads);
 
+/* ---- decode layer chain (bf16 in/out, MLX rounding points) ----
+ * rms_norm: src/primitives/nn.rs:35-37; silu_mul: src/models/llama.rs:1040-1045;
+ * add: llama.rs:729-733; repeat_kv: src/primitives/attention.rs:45-55.
+ * pinned: closed forms, scipy's expit, torch's bf16 casts and the
+ * reference's repeat_kv known answer (tests/test_oracle.py). */
+int orc_rms_norm_bf16(const uint16_t* x, const uint16_t* w, int64_t rows, int64_t dim,
+                      float eps, uint16_t* y);
+int orc_silu_mul_bf16(const uint16_t* g, const uint16_t* u, int64_t n, uint16_t* y);
+int orc_add_bf16(const uint16_t* a, const uint16_t* b, int64_t n, uint16_t* y);
+int orc_repeat_kv(const uint16_t* x, int64_t rows, int kv_heads, int head_dim, int groups,
+                  uint16_t* y);
+
 #ifdef __cplusplus
 }
 #endif

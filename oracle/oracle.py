@@ -54,6 +54,10 @@ def lib() -> ctypes.CDLL:
         L.orc_affine_dequantize.argtypes = [ctypes.c_int, _P, _P, _P, _i64, _i64, ctypes.c_int, ctypes.c_int, _P]
         L.orc_qmatmul_f64.argtypes = [_P, _i64, _P, _P, _P, _i64, _i64, ctypes.c_int, ctypes.c_int, _P]
         L.orc_qmatmul_f32.argtypes = [_P, _i64, _P, _P, _P, _i64, _i64, ctypes.c_int, ctypes.c_int, _P, ctypes.c_int]
+        L.orc_rms_norm_bf16.argtypes = [_P, _P, _i64, _i64, ctypes.c_float, _P]
+        L.orc_silu_mul_bf16.argtypes = [_P, _P, _i64, _P]
+        L.orc_add_bf16.argtypes = [_P, _P, _i64, _P]
+        L.orc_repeat_kv.argtypes = [_P, _i64, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P]
         _lib = L
     return _lib
 
@@ -173,3 +177,67 @@ def qmatmul_f32(x_bf16, wq, s_bf16, b_bf16, group_size: int = 64, bits: int = 4,
     _chk(lib().orc_qmatmul_f32(_p(x_bf16), m, _p(np.ascontiguousarray(wq)), _p(np.ascontiguousarray(s_bf16)),
                                _p(np.ascontiguousarray(b_bf16)), n, k, group_size, bits, _p(y), threads))
     return y
+
+
+# ---------------------------------------------------------------- decode layer chain
+def _u16(a):
+    return np.ascontiguousarray(a, dtype=np.uint16)
+
+
+def rms_norm(x_bf16, w_bf16, eps: float) -> np.ndarray:
+    x = _u16(x_bf16)
+    y = np.empty_like(x)
+    d = x.shape[-1]
+    _chk(lib().orc_rms_norm_bf16(_p(x), _p(_u16(w_bf16)), x.size // d, d, eps, _p(y)))
+    return y
+
+
+def silu_mul(g_bf16, u_bf16) -> np.ndarray:
+    g, u = _u16(g_bf16), _u16(u_bf16)
+    y = np.empty_like(g)
+    _chk(lib().orc_silu_mul_bf16(_p(g), _p(u), g.size, _p(y)))
+    return y
+
+
+def add(a_bf16, b_bf16) -> np.ndarray:
+    a, b = _u16(a_bf16), _u16(b_bf16)
+    y = np.empty_like(a)
+    _chk(lib().orc_add_bf16(_p(a), _p(b), a.size, _p(y)))
+    return y
+
+
+def repeat_kv(x_bf16, kv_heads: int, head_dim: int, groups: int) -> np.ndarray:
+    x = _u16(x_bf16)
+    rows = x.size // (kv_heads * head_dim)
+    y = np.empty((rows, kv_heads * groups * head_dim), dtype=np.uint16)
+    _chk(lib().orc_repeat_kv(_p(x), rows, kv_heads, head_dim, groups, _p(y)))
+    return y
+
+
+def qlinear_bf16(x_bf16, w, group_size: int, bits: int) -> np.ndarray:
+    """A quantized projection with its bf16 output rounding (f64 sums -> f32 -> bf16)."""
+    wq, s, b = w
+    y = qmatmul_f64(x_bf16, wq, s, b, group_size, bits)
+    return f32_to_bf16(y.astype(np.float32))
+
+
+def decode_stack(x_bf16, layers, final_norm, lm_head, cfg) -> np.ndarray:
+    """One decode step of the quantized Llama layer chain with attention replaced
+    by the identity on v (GQA heads repeated): src/models/llama.rs:689-735
+    (layer), :806-835 (q/k/v/o), :1040-1045 (MLP), :595-603 (final norm and
+    lm_head).  layers: dicts with packed (wq, scales, biases) numpy triples
+    under q, k, v, o, gate, up, down and bf16 norm weights ln1, ln2.
+    Returns bf16 logits [M, vocab]."""
+    gs, bits, eps = cfg["group_size"], cfg["bits"], cfg["eps"]
+    groups = cfg["heads"] // cfg["kv_heads"]
+    x = _u16(x_bf16)
+    for L in layers:
+        n1 = rms_norm(x, L["ln1"], eps)
+        # q and k only feed attention, which the chain replaces: no effect on the output
+        v = qlinear_bf16(n1, L["v"], gs, bits)
+        attn = repeat_kv(v, cfg["kv_heads"], cfg["head_dim"], groups)
+        h = add(x, qlinear_bf16(attn, L["o"], gs, bits))
+        n2 = rms_norm(h, L["ln2"], eps)
+        a = silu_mul(qlinear_bf16(n2, L["gate"], gs, bits), qlinear_bf16(n2, L["up"], gs, bits))
+        x = add(h, qlinear_bf16(a, L["down"], gs, bits))
+    return qlinear_bf16(rms_norm(x, final_norm, eps), lm_head, gs, bits)

@@ -224,3 +224,16 @@ def test_qmv_mfma_path_for_decode_rows(torch_gpu, monkeypatch, bits, m):
     wq, s, b = make_layer(700 + bits, n, k, 64, bits)
     x = bf16_acts(701 + m, m, k)
     assert rel_err(run(x, wq, s, b, 64, bits), orc.qmatmul_f64(x, wq, s, b, 64, bits)) <= TIGHT
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("cfg", ["1,4", "1,8", "2,4", "2,8"])
+@pytest.mark.parametrize("k", [512, 1024])
+def test_qmv_dot_short_rows_every_config(torch_gpu, monkeypatch, bits, cfg, k):
+    """Short rows leave most waves of a workgroup with an empty chunk range:
+    they must fetch nothing (every load stays inside the row), for each
+    rows-per-workgroup / waves-per-workgroup configuration."""
+    monkeypatch.setenv("MLXQ_QMV_DOT", cfg)
+    wq, s, b = make_layer(800 + bits + k, 1000, k, 64, bits)
+    x = bf16_acts(801 + k, 2, k)
+    assert rel_err(run(x, wq, s, b, 64, bits), orc.qmatmul_f64(x, wq, s, b, 64, bits)) <= TIGHT

@@ -1,0 +1,56 @@
+"""Quantized decode stack (the Llama layer chain with attention replaced by
+the identity on v) on the GPU against the CPU oracle's chain of the same
+ops, same packed weights and same bf16 rounding points.
+
+The oracle sums each projection in f64; the GPU in f32 in another order.
+Rounding differences then propagate through the chain, so the logits are
+compared by max |y - ref| / max |ref| <= 1e-2 (the qmatmul parity bar).
+"""
+import numpy as np
+import pytest
+
+import oracle as orc
+from helpers import dev, host, rel_err
+from stack import DecodeStack, StackConfig
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+
+SMALL = dict(layers=3, hidden=512, intermediate=1536, heads=8, kv_heads=2, head_dim=64, vocab=1000)
+
+
+def _run(cfg: StackConfig, batch: int, graph: bool):
+    st = DecodeStack(cfg, batch=batch, seed=7, norm_noise=0.1)
+    x = orc.f32_to_bf16(orc.normal(1234 + batch, batch * cfg.hidden, 0.0, 1.0)).reshape(batch, cfg.hidden)
+    st.x.copy_(dev(x, True))
+    if graph:
+        g = st.capture()
+        g.replay()
+        g.replay()  # a replay must give the same result as the first
+    else:
+        st.forward()
+    got = host(st.logits)
+    layers, norm, lm = st.host_weights()
+    want = orc.decode_stack(x, layers, norm, lm, cfg.as_dict())
+    return got, want
+
+
+@pytest.mark.parametrize("batch", [1, 4, 16])
+def test_small_stack(torch_gpu, batch):
+    got, want = _run(StackConfig(**SMALL), batch, graph=False)
+    assert rel_err(orc.bf16_to_f32(got), orc.bf16_to_f32(want).astype(np.float64)) <= TOL
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_small_stack_graph(torch_gpu, bits):
+    got, want = _run(StackConfig(bits=bits, **SMALL), 2, graph=True)
+    assert rel_err(orc.bf16_to_f32(got), orc.bf16_to_f32(want).astype(np.float64)) <= TOL
+
+
+@pytest.mark.parametrize("batch", [1, 16])
+def test_llama3_8b_width_two_layers(torch_gpu, batch):
+    """Config-5 widths (hidden 4096, intermediate 14336, 32/8 heads x 128,
+    vocab 128256, Q4 g64) with two layers, so the f64 CPU chain stays short."""
+    got, want = _run(StackConfig(layers=2), batch, graph=True)
+    assert rel_err(orc.bf16_to_f32(got), orc.bf16_to_f32(want).astype(np.float64)) <= TOL

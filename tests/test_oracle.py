@@ -360,3 +360,88 @@ def test_f64_gemm_matches_numpy(bits):
     assert np.allclose(got, ref, rtol=1e-12, atol=1e-12)
     got32 = orc.qmatmul_f32(x, wq, s, b, 64, bits, threads=2)
     assert np.max(np.abs(got32 - ref)) <= 1e-4 * np.max(np.abs(ref))
+
+
+# ---------------------------------------------------------------- decode layer chain ops
+def _torch_bf16(a: np.ndarray) -> np.ndarray:
+    """f32 -> bf16 bits through torch's own cast (an implementation independent of the oracle)."""
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+
+
+def test_rms_norm_known_answer():
+    # x = [3, 4] (mean square 12.5), w = 1, eps = 0: x / sqrt(12.5) = [0.848528.., 1.131370..]
+    x = orc.f32_to_bf16(np.array([[3.0, 4.0]], dtype=np.float32))
+    w = orc.f32_to_bf16(np.ones(2, dtype=np.float32))
+    y = orc.bf16_to_f32(orc.rms_norm(x, w, 0.0))
+    want = _torch_bf16(np.array([3 / np.sqrt(12.5), 4 / np.sqrt(12.5)], dtype=np.float32))
+    assert np.array_equal(orc.f32_to_bf16(y).ravel(), want)
+
+
+def test_rms_norm_invariants():
+    x = orc.f32_to_bf16(orc.normal(5, 4 * 512, 0.0, 3.0)).reshape(4, 512)
+    ones = orc.f32_to_bf16(np.ones(512, dtype=np.float32))
+    y = orc.rms_norm(x, ones, 0.0)
+    # scaling the input by a power of two leaves the output unchanged (eps = 0)
+    x4 = orc.f32_to_bf16(orc.bf16_to_f32(x) * 4.0)
+    assert np.array_equal(orc.rms_norm(x4, ones, 0.0), y)
+    # a weight of 2 doubles every output exactly; unit weight gives unit RMS
+    twos = orc.f32_to_bf16(np.full(512, 2.0, dtype=np.float32))
+    assert np.array_equal(orc.bf16_to_f32(orc.rms_norm(x, twos, 0.0)), 2.0 * orc.bf16_to_f32(y))
+    rms = np.sqrt(np.mean(orc.bf16_to_f32(y).astype(np.float64) ** 2, axis=1))
+    assert np.all(np.abs(rms - 1.0) < 4e-3)
+    # eps enters under the root: a zero row stays zero, a tiny row is damped
+    z = np.zeros((1, 512), dtype=np.uint16)
+    assert not orc.bf16_to_f32(orc.rms_norm(z, ones, 1e-5)).any()
+
+
+def test_rms_norm_matches_float64_formula_within_a_bf16_step():
+    x = orc.f32_to_bf16(orc.normal(6, 8 * 256, 0.0, 1.0)).reshape(8, 256)
+    w = orc.f32_to_bf16(orc.normal(7, 256, 1.0, 0.1))
+    xf, wf = orc.bf16_to_f32(x).astype(np.float64), orc.bf16_to_f32(w).astype(np.float64)
+    ref = wf * xf / np.sqrt(np.mean(xf * xf, axis=1, keepdims=True) + 1e-5)
+    got = orc.bf16_to_f32(orc.rms_norm(x, w, 1e-5)).astype(np.float64)
+    # two bf16 roundings: at most ~2^-8 relative each
+    assert np.all(np.abs(got - ref) <= np.abs(ref) * 2 ** -7 + 1e-30)
+
+
+def test_silu_mul_against_scipy_expit():
+    from scipy.special import expit
+
+    g = orc.f32_to_bf16(np.concatenate([orc.normal(8, 4000, 0.0, 4.0), [0.0, 1.0, -1.0, 30.0, -30.0, 88.0, -88.0]]).astype(np.float32))
+    u = orc.f32_to_bf16(orc.normal(9, g.size, 0.0, 1.0))
+    gf, uf = orc.bf16_to_f32(g), orc.bf16_to_f32(u)
+    s = orc.bf16_to_f32(_torch_bf16(expit(gf.astype(np.float64)).astype(np.float32)))
+    a = orc.bf16_to_f32(_torch_bf16(gf * s))
+    want = _torch_bf16(a * uf)
+    got = orc.silu_mul(g, u)
+    # scipy's expit vs libm expf may differ in the last f32 bit, which can move a bf16 tie
+    assert np.mean(got == want) > 0.999
+    assert np.all(np.abs(orc.bf16_to_f32(got) - orc.bf16_to_f32(want)) <= np.abs(orc.bf16_to_f32(want)) * 2 ** -7)
+    ones = orc.f32_to_bf16(np.ones(4, dtype=np.float32))
+    # silu(0) = 0, silu(1) = sigmoid(1) = 0.7310585786.., silu(30) = 30, silu(-30) ~ -0
+    v = orc.bf16_to_f32(orc.silu_mul(orc.f32_to_bf16(np.array([0.0, 1.0, 30.0, -30.0], dtype=np.float32)), ones))
+    assert v[0] == 0.0 and v[2] == 30.0 and abs(v[3]) < 1e-10
+    assert v[1] == orc.bf16_to_f32(_torch_bf16(np.array([0.7310585786300049], dtype=np.float32)))[0]
+
+
+def test_add_matches_torch_bf16_add():
+    import torch
+
+    a = orc.f32_to_bf16(orc.normal(10, 5000, 0.0, 2.0))
+    b = orc.f32_to_bf16(orc.normal(11, 5000, 0.0, 2.0))
+    ta = torch.from_numpy(a.view(np.int16)).view(torch.bfloat16)
+    tb = torch.from_numpy(b.view(np.int16)).view(torch.bfloat16)
+    want = (ta + tb).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(orc.add(a, b), want)
+
+
+def test_repeat_kv_reference_known_answer():
+    # src/primitives/attention.rs:294-300: heads [0,1], [2,3] with 2 groups ->
+    # head0, head0, head1, head1
+    x = orc.f32_to_bf16(np.array([0.0, 1.0, 2.0, 3.0], dtype=np.float32)).reshape(1, 4)
+    y = orc.bf16_to_f32(orc.repeat_kv(x, 2, 2, 2)).ravel()
+    assert y.tolist() == [0.0, 1.0, 0.0, 1.0, 2.0, 3.0, 2.0, 3.0]
+    # groups = 1 is the identity (attention.rs:281-285)
+    assert np.array_equal(orc.repeat_kv(x, 2, 2, 1), x)
