@@ -13,6 +13,7 @@ Extra fields (same JSON line):
   kernels       per (bits, M) decode GEMV GB/s and % of 8 TB/s
   prefill       config 3: qmm at M=2048, Q4, 4096->14336 and 14336->4096, TFLOP/s
   gguf          config 4: block dequant of a 14336x4096 tensor, GB/s per type
+  decode_stack  config 5: quantized Llama-3-8B decode step, tokens/s at batch 1 and 16
   cpu_baseline  the CPU restatement (oracle, OpenMP) on a bounded sample
 """
 from __future__ import annotations
@@ -208,6 +209,7 @@ def main(argv=None) -> int:
     if not a.quick:
         out["prefill"] = bench_prefill(torch, mlxq)
         out["gguf"] = bench_gguf(torch, mlxq)
+        out["decode_stack"] = bench_stack(torch)
     if not a.quick and not a.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(torch, weights, xs, a.cpu_seconds)
     print(json.dumps(out), flush=True)
@@ -276,6 +278,42 @@ def bench_gguf(torch, mlxq, iters=10):
             entry[oname] = {"us": round(us, 1), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 3)}
         res[tname] = entry
         del raw
+    return res
+
+
+def bench_stack(torch, steps=20, batches=(1, 16)):
+    """Config 5: one decode step of the quantized Llama-3-8B layer chain (32
+    layers, Q4 g64 projections and lm_head, attention = identity on v),
+    captured as a HIP graph; tokens/s = batch / step time."""
+    from stack import DecodeStack, llama3_8b
+
+    cfg = llama3_8b()
+    st = DecodeStack(cfg, batch=max(batches), seed=5)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0x5EED0500)
+    st.x.copy_(torch.randn(st.x.shape, generator=g, device="cuda").to(torch.bfloat16))
+    wbytes = st.weight_bytes()
+    res = {"model": "Llama-3-8B shapes, random init, 32 layers, Q4 g64 (lm_head Q4)",
+           "weight_bytes_per_step": wbytes,
+           "tokens_per_s_bound_b1": round(HBM_PEAK_GBS * 1e9 / wbytes, 1)}
+    for b in batches:
+        graph = st.capture(b)
+        for _ in range(3):
+            graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        gbs = wbytes / (ms * 1e-3) / 1e9
+        res[f"batch{b}"] = {"ms_per_step": round(ms, 3), "tokens_per_s": round(b / (ms * 1e-3), 1),
+                            "weight_GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 3)}
+        del graph
+    del st
+    torch.cuda.empty_cache()
     return res
 
 

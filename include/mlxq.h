@@ -118,6 +118,40 @@ int mlxq_qmatmul_algo(const void* x, int64_t M, const uint32_t* wq,
                       int group_size, int bits, void* y, void* workspace,
                       size_t workspace_bytes, int algo, void* stream);
 
+/* One projection of a fused decode call (mlxq_qmatmul_fused). */
+typedef struct {
+  const uint32_t* wq;    /* [N, K*bits/32] packed codes                     */
+  const void* scales;    /* [N, K/group_size] bf16                          */
+  const void* biases;    /* [N, K/group_size] bf16                          */
+  const void* bias;      /* [N] bf16 dense bias, or NULL                    */
+  const void* residual;  /* [M, N] bf16, or NULL: y = bf16(r + bf16(x W^T)) */
+  void* y;               /* [M, N] bf16 output                              */
+  int64_t N;
+} mlxq_projection;
+
+/* Decode-step fusion of the layer chain around the projections
+ * (src/models/llama.rs:689-735): one launch computes
+ *   x' = rms_norm(x, norm_weight, eps)          if norm_weight != NULL
+ *        (nn.rs:35-37, as mlxq_rms_norm),
+ *   x' = repeat_kv(x, kv_heads, head_dim, groups) if groups > 1
+ *        (attention.rs:45-55; x rows then hold K/groups values),
+ *   x' = x                                      otherwise,
+ * and then, for nproj <= 3 projections of the same x' (q, k, v at
+ * llama.rs:806-812), y_i = x' W_i^T (+ bias_i) (+ residual_i: the residual
+ * add of llama.rs:729-733, rounded as add(r, bf16(x' W^T))).
+ * swiglu != 0 (requires norm_weight and nproj == 2): y_0 = silu(x' W_0^T) *
+ * (x' W_1^T) with the rounding of mlxq_silu_mul (llama.rs:1040-1045).
+ * Results equal the unfused sequence of mlxq_rms_norm / mlxq_repeat_kv /
+ * mlxq_qmatmul / mlxq_add / mlxq_silu_mul up to f32 summation order.
+ * Covers the decode kernel's shapes (1 <= M <= 4, K*bits/8 % 64 == 0);
+ * other shapes return MLXQ_ERR_UNSUPPORTED before any launch, and the
+ * caller issues the unfused calls.  No workspace, no allocation. */
+int mlxq_qmatmul_fused(const void* x, int64_t M, int64_t K,
+                       const void* norm_weight, float eps, int kv_heads,
+                       int head_dim, int groups, const mlxq_projection* proj,
+                       int nproj, int swiglu, int group_size, int bits,
+                       void* stream);
+
 /* ------------------------------------------------------------------ */
 /* Decode layer chain around the projections (bf16, MLX rounding points) */
 /* ------------------------------------------------------------------ */

@@ -96,3 +96,53 @@ extern "C" int mlxq_qmatmul(const void* x, int64_t M, const uint32_t* wq, const 
   return mlxq_qmatmul_algo(x, M, wq, scales, biases, bias_vec, N, K, group_size, bits, y, workspace,
                            workspace_bytes, MLXQ_ALGO_AUTO, stream);
 }
+
+extern "C" int mlxq_qmatmul_fused(const void* x, int64_t M, int64_t K, const void* norm_weight, float eps,
+                                  int kv_heads, int head_dim, int groups, const mlxq_projection* proj, int nproj,
+                                  int swiglu, int group_size, int bits, void* stream) {
+  clear_error();
+  if (!proj || nproj < 1 || nproj > 3) return fail(MLXQ_ERR_INVALID, "qmatmul_fused: 1 to 3 projections");
+  if (swiglu && (nproj != 2 || !norm_weight))
+    return fail(MLXQ_ERR_UNSUPPORTED, "qmatmul_fused: SwiGLU needs gate/up and a norm weight");
+  if (norm_weight && groups > 1) return fail(MLXQ_ERR_UNSUPPORTED, "qmatmul_fused: norm and head repeat together");
+  for (int i = 0; i < nproj; i++) {
+    int rc = check_shape(M, proj[i].N, K, group_size, bits);
+    if (rc) return rc;
+    if (!proj[i].wq || !proj[i].scales || !proj[i].biases || !proj[i].y)
+      return fail(MLXQ_ERR_INVALID, "qmatmul_fused: null projection pointer");
+    if (reinterpret_cast<uintptr_t>(proj[i].wq) & 15u)
+      return fail(MLXQ_ERR_INVALID, "qmatmul_fused: wq must be 16-byte aligned");
+  }
+  if (M == 0) return MLXQ_OK;
+  if (!x || (reinterpret_cast<uintptr_t>(x) & 15u)) return fail(MLXQ_ERR_INVALID, "qmatmul_fused: bad x");
+  if (norm_weight && (reinterpret_cast<uintptr_t>(norm_weight) & 15u))
+    return fail(MLXQ_ERR_INVALID, "qmatmul_fused: norm_weight must be 16-byte aligned");
+  if (norm_weight && !(eps >= 0.f)) return fail(MLXQ_ERR_INVALID, "qmatmul_fused: eps must be >= 0");
+  if (K % 8) return fail(MLXQ_ERR_SHAPE, "qmatmul_fused: K must be a multiple of 8");
+  QmvFused f{};
+  f.x = static_cast<const uint16_t*>(x);
+  f.M = M;
+  f.K = K;
+  f.x_stride = K;
+  f.norm_w = static_cast<const uint16_t*>(norm_weight);
+  f.eps = eps;
+  if (groups > 1) {
+    if (kv_heads <= 0 || head_dim <= 0 || static_cast<int64_t>(kv_heads) * head_dim * groups != K)
+      return fail(MLXQ_ERR_SHAPE, "qmatmul_fused: kv_heads * head_dim * groups must equal K");
+    f.rep = groups;
+    f.rep_hd = head_dim;
+    f.x_stride = K / groups;
+  }
+  f.nproj = nproj;
+  for (int i = 0; i < nproj; i++)
+    f.proj[i] = QmvProj{proj[i].wq, static_cast<const uint16_t*>(proj[i].scales),
+                        static_cast<const uint16_t*>(proj[i].biases), static_cast<const uint16_t*>(proj[i].bias),
+                        static_cast<const uint16_t*>(proj[i].residual), static_cast<uint16_t*>(proj[i].y),
+                        proj[i].N};
+  f.swiglu = swiglu != 0;
+  f.group_size = group_size;
+  f.bits = bits;
+  if (M > kQmvDotMaxM)
+    return fail(MLXQ_ERR_UNSUPPORTED, "qmatmul_fused: M > " + std::to_string(kQmvDotMaxM) + " is not fused");
+  return launch_qmv_dot_fused(f, as_stream(stream));
+}

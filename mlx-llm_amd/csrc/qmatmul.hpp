@@ -33,6 +33,31 @@ int launch_qmv_dot(const uint16_t* x, int64_t M, const uint32_t* wq, const uint1
                    const uint16_t* bias, int64_t N, int64_t K, int group_size, int bits, uint16_t* y,
                    hipStream_t st);
 
+// Fused decode GEMV: up to 3 projections of the same activations (optionally
+// RMS-normalized or GQA head-repeated while staged), each with an optional
+// residual added to its bf16 output; or gate/up with the SwiGLU epilogue.
+struct QmvProj {
+  const uint32_t* wq;
+  const uint16_t* s;
+  const uint16_t* b;
+  const uint16_t* bias;  // [N] or null
+  const uint16_t* res;   // [M, N] residual or null
+  uint16_t* y;           // [M, N]
+  int64_t N;
+};
+struct QmvFused {
+  const uint16_t* x;
+  int64_t M, K, x_stride;
+  const uint16_t* norm_w;  // [K] or null
+  float eps;
+  int rep_hd, rep;         // rep > 1: activation k reads source (k / (rep_hd*rep)) * rep_hd + k % rep_hd
+  int nproj;
+  QmvProj proj[3];
+  bool swiglu;             // proj[0] = gate, proj[1] = up; y = silu(gate) * up into proj[0].y
+  int group_size, bits;
+};
+int launch_qmv_dot_fused(const QmvFused& f, hipStream_t st);
+
 // qmm: LDS-dequant bf16 MFMA GEMM, any M, K % 64 == 0.  No workspace.
 int launch_qmm(const uint16_t* x, int64_t M, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
                const uint16_t* bias, int64_t N, int64_t K, int group_size, int bits, uint16_t* y, hipStream_t st);

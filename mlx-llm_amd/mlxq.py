@@ -42,6 +42,9 @@ SIGNATURES = {
     "mlxq_qmatmul_workspace_size": (ctypes.c_int, [_i64, _i64, _i64, ctypes.c_int, ctypes.c_int, ctypes.POINTER(_sz)]),
     "mlxq_qmatmul": (ctypes.c_int, [_vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, ctypes.c_int, ctypes.c_int, _vp, _vp, _sz, _vp]),
     "mlxq_qmatmul_algo": (ctypes.c_int, [_vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, ctypes.c_int, ctypes.c_int, _vp, _vp, _sz, ctypes.c_int, _vp]),
+    "mlxq_qmatmul_fused": (ctypes.c_int, [_vp, _i64, _i64, _vp, ctypes.c_float, ctypes.c_int, ctypes.c_int,
+                                          ctypes.c_int, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                          ctypes.c_int, _vp]),
     "mlxq_rms_norm": (ctypes.c_int, [_vp, _vp, _i64, _i64, ctypes.c_float, _vp, _vp]),
     "mlxq_silu_mul": (ctypes.c_int, [_vp, _vp, _i64, _vp, _vp]),
     "mlxq_add": (ctypes.c_int, [_vp, _vp, _i64, _vp, _vp]),
@@ -50,6 +53,12 @@ SIGNATURES = {
     "mlxq_gguf_tensor_byte_len": (ctypes.c_int, [_u32, _i64, ctypes.POINTER(_i64)]),
     "mlxq_gguf_dequantize": (ctypes.c_int, [_u32, _vp, _i64, _i64, ctypes.c_int, _vp, _vp]),
 }
+
+
+class Projection(ctypes.Structure):
+    """mlxq_projection (include/mlxq.h)."""
+    _fields_ = [("wq", _vp), ("scales", _vp), ("biases", _vp), ("bias", _vp), ("residual", _vp), ("y", _vp),
+                ("N", _i64)]
 
 
 class MlxqError(RuntimeError):
@@ -207,6 +216,24 @@ def bind_qmatmul(x, wq, scales, biases, group_size: int = 64, bits: int = 4, out
     call.out = y
     call.workspace = ws
     return call
+
+
+def qmatmul_fused(x, projs, group_size: int = 64, bits: int = 4, norm_weight=None, eps: float = 0.0,
+                  repeat=None, swiglu: bool = False):
+    """One fused decode launch (mlxq_qmatmul_fused).  projs: list of dicts with
+    wq, scales, biases, y and optional bias / residual (device tensors);
+    repeat: (kv_heads, head_dim, groups) for a GQA head-repeated input.
+    Raises Unsupported for shapes outside the fused decode kernel."""
+    k = x.shape[-1] * (repeat[2] if repeat else 1)
+    m = x.numel() // x.shape[-1]
+    arr = (Projection * len(projs))()
+    for i, p in enumerate(projs):
+        arr[i] = Projection(_ptr(p["wq"]), _ptr(p["scales"]), _ptr(p["biases"]), _ptr(p.get("bias")),
+                            _ptr(p.get("residual")), _ptr(p["y"]), p["wq"].shape[0])
+    kvh, hd, groups = repeat if repeat else (0, 0, 1)
+    check(lib().mlxq_qmatmul_fused(_ptr(x), m, k, _ptr(norm_weight), eps, kvh, hd, groups, arr, len(projs),
+                                   int(swiglu), group_size, bits, _stream()))
+    return projs[0]["y"]
 
 
 def rms_norm(x, weight, eps: float, out=None):

@@ -81,8 +81,9 @@ class Layer:
 
 class DecodeStack:
     """Random-init quantized Llama stack (seeded N(0, 0.02) weights quantized on
-    device) with preallocated activations for a fixed batch, so one decode step
-    can be captured in a HIP graph and replayed."""
+    device) with activations preallocated for up to `batch` rows, so a decode
+    step of any batch b <= batch can be captured in a HIP graph and replayed
+    (the step works on the first b rows of every buffer)."""
 
     def __init__(self, cfg: StackConfig, batch: int = 1, seed: int = 0, device="cuda", norm_noise: float = 0.0):
         import torch
@@ -138,42 +139,110 @@ class DecodeStack:
     def _lin(self, x, p: QLinear, out):
         return mlxq.qmatmul(x, p.wq, p.scales, p.biases, self.cfg.group_size, self.cfg.bits, out=out)
 
-    def forward(self):
-        """One decode step on the current stream: self.x -> self.logits."""
+    def forward(self, b: int | None = None, fused: bool = True):
+        """One decode step of b rows on the current stream: self.x[:b] -> self.logits[:b].
+        fused: per layer, four launches of the fused decode kernel (norm + q/k/v,
+        head repeat + o + residual, norm + gate/up + SwiGLU, down + residual)
+        wherever it covers the shape; a call it does not cover (it rejects the
+        shape before launching anything) runs as the op-by-op chain."""
+        if not fused:
+            return self._forward_ops(b)
         c = self.cfg
-        x = self.x
+        b = self.batch if b is None else b
+        gs, bits = c.group_size, c.bits
+        n, h, q, k, v, attn, o = (t[:b] for t in (self.n, self.h, self.q, self.k, self.v, self.attn, self.o))
+        g, u, a, d = (t[:b] for t in (self.g, self.u, self.a, self.d))
+        lin = self._lin
+
+        def fz(x, projs, fallback, **kw):
+            try:
+                mlxq.qmatmul_fused(x, projs, gs, bits, **kw)
+            except mlxq.Unsupported:
+                fallback()
+
+        x = self.x[:b]
         for i, L in enumerate(self.layers):
             P = L.proj
-            mlxq.rms_norm(x, L.ln1, c.eps, out=self.n)
-            self._lin(self.n, P["q"], self.q)
-            self._lin(self.n, P["k"], self.k)
-            self._lin(self.n, P["v"], self.v)
-            mlxq.repeat_kv(self.v, c.kv_heads, c.head_dim, c.groups, out=self.attn)
-            self._lin(self.attn, P["o"], self.o)
-            mlxq.add(x, self.o, out=self.h)
-            mlxq.rms_norm(self.h, L.ln2, c.eps, out=self.n)
-            self._lin(self.n, P["gate"], self.g)
-            self._lin(self.n, P["up"], self.u)
-            mlxq.silu_mul(self.g, self.u, out=self.a)
-            self._lin(self.a, P["down"], self.d)
-            x = self.xa if i % 2 == 0 else self.xb
-            mlxq.add(self.h, self.d, out=x)
-        mlxq.rms_norm(x, self.norm, c.eps, out=self.n)
-        self._lin(self.n, self.lm_head, self.logits)
-        return self.logits
+            xn = (self.xa if i % 2 == 0 else self.xb)[:b]
 
-    def capture(self):
-        """Capture forward() in a HIP graph; returns the graph (replay() runs one step)."""
+            def qkv(x=x, P=P, L=L):
+                mlxq.rms_norm(x, L.ln1, c.eps, out=n)
+                lin(n, P["q"], q), lin(n, P["k"], k), lin(n, P["v"], v)
+
+            def oproj(x=x, P=P):
+                mlxq.repeat_kv(v, c.kv_heads, c.head_dim, c.groups, out=attn)
+                lin(attn, P["o"], o)
+                mlxq.add(x, o, out=h)
+
+            def mlp_in(P=P, L=L):
+                mlxq.rms_norm(h, L.ln2, c.eps, out=n)
+                lin(n, P["gate"], g), lin(n, P["up"], u)
+                mlxq.silu_mul(g, u, out=a)
+
+            def down(P=P, xn=xn):
+                lin(a, P["down"], d)
+                mlxq.add(h, d, out=xn)
+
+            fz(x, [self._proj(P["q"], q), self._proj(P["k"], k), self._proj(P["v"], v)], qkv,
+               norm_weight=L.ln1, eps=c.eps)
+            fz(v, [self._proj(P["o"], h, res=x)], oproj, repeat=(c.kv_heads, c.head_dim, c.groups))
+            fz(h, [self._proj(P["gate"], a), self._proj(P["up"], u)], mlp_in, norm_weight=L.ln2, eps=c.eps,
+               swiglu=True)
+            fz(a, [self._proj(P["down"], xn, res=h)], down)
+            x = xn
+
+        def head(x=x):
+            mlxq.rms_norm(x, self.norm, c.eps, out=n)
+            lin(n, self.lm_head, self.logits[:b])
+
+        fz(x, [self._proj(self.lm_head, self.logits[:b])], head, norm_weight=self.norm, eps=c.eps)
+        return self.logits[:b]
+
+    def _proj(self, p: QLinear, y, res=None):
+        d = {"wq": p.wq, "scales": p.scales, "biases": p.biases, "y": y}
+        if res is not None:
+            d["residual"] = res
+        return d
+
+    def _forward_ops(self, b: int | None = None):
+        c = self.cfg
+        b = self.batch if b is None else b
+        assert 1 <= b <= self.batch
+        n, h, q, k, v, attn, o = (t[:b] for t in (self.n, self.h, self.q, self.k, self.v, self.attn, self.o))
+        g, u, a, d = (t[:b] for t in (self.g, self.u, self.a, self.d))
+        x = self.x[:b]
+        for i, L in enumerate(self.layers):
+            P = L.proj
+            mlxq.rms_norm(x, L.ln1, c.eps, out=n)
+            self._lin(n, P["q"], q)
+            self._lin(n, P["k"], k)
+            self._lin(n, P["v"], v)
+            mlxq.repeat_kv(v, c.kv_heads, c.head_dim, c.groups, out=attn)
+            self._lin(attn, P["o"], o)
+            mlxq.add(x, o, out=h)
+            mlxq.rms_norm(h, L.ln2, c.eps, out=n)
+            self._lin(n, P["gate"], g)
+            self._lin(n, P["up"], u)
+            mlxq.silu_mul(g, u, out=a)
+            self._lin(a, P["down"], d)
+            x = (self.xa if i % 2 == 0 else self.xb)[:b]
+            mlxq.add(h, d, out=x)
+        mlxq.rms_norm(x, self.norm, c.eps, out=n)
+        self._lin(n, self.lm_head, self.logits[:b])
+        return self.logits[:b]
+
+    def capture(self, b: int | None = None, fused: bool = True):
+        """Capture forward(b) in a HIP graph; returns the graph (replay() runs one step)."""
         import torch
         s = torch.cuda.Stream(device=self.device)
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
-            self.forward()  # warm-up outside the capture (kernel attributes, occupancy queries)
+            self.forward(b, fused)  # warm-up outside the capture (kernel attributes, occupancy queries)
         torch.cuda.current_stream().wait_stream(s)
         torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, stream=s):
-            self.forward()
+            self.forward(b, fused)
         torch.cuda.synchronize()
         return graph
 

@@ -1,0 +1,107 @@
+"""Fused decode launches (mlxq_qmatmul_fused) against the CPU oracle's chain
+of the same unfused ops: rms_norm / repeat_kv -> quantized projections ->
+residual add / SwiGLU, same packed weights, same bf16 rounding points.
+Bar: max|y - ref| / max|ref| <= 1e-2 (the qmatmul parity bar)."""
+import numpy as np
+import pytest
+
+import mlxq
+import oracle as orc
+from helpers import bf16_acts, bf16_weights, dev, host, rel_err
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-2
+
+
+def qlayer(seed, n, k, gs, bits):
+    wq, s, b = orc.affine_quantize(bf16_weights(seed, n, k), gs, bits, orc.BF16)
+    return (wq, s, b), {"wq": dev(wq), "scales": dev(s, True), "biases": dev(b, True)}
+
+
+def out_like(m, n):
+    import torch
+
+    return torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+
+
+def check(got, want):
+    assert rel_err(orc.bf16_to_f32(host(got)), orc.bf16_to_f32(want).astype(np.float64)) <= TOL
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("m", [1, 2, 4])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+def test_norm_qkv(torch_gpu, bits, m, gs):
+    k = 2048
+    x = bf16_acts(10 + m, m, k)
+    w = orc.f32_to_bf16(orc.normal(11, k, 1.0, 0.1))
+    shapes = [2048, 512, 512]
+    host_w, projs = [], []
+    for i, n in enumerate(shapes):
+        hw, dw = qlayer(20 + i + bits, n, k, gs, bits)
+        host_w.append(hw)
+        dw["y"] = out_like(m, n)
+        projs.append(dw)
+    mlxq.qmatmul_fused(dev(x, True), projs, gs, bits, norm_weight=dev(w, True), eps=1e-5)
+    xn = orc.rms_norm(x, w, 1e-5)
+    for hw, p in zip(host_w, projs):
+        check(p["y"], orc.qlinear_bf16(xn, hw, gs, bits))
+
+
+@pytest.mark.parametrize("m", [1, 3])
+def test_repeat_o_residual(torch_gpu, m):
+    kvh, hd, groups = 8, 128, 4
+    k = kvh * hd * groups
+    v = bf16_acts(30 + m, m, kvh * hd)
+    r = bf16_acts(31 + m, m, 4096)
+    hw, dw = qlayer(32, 4096, k, 64, 4)
+    dw["y"] = out_like(m, 4096)
+    dw["residual"] = dev(r, True)
+    mlxq.qmatmul_fused(dev(v, True), [dw], 64, 4, repeat=(kvh, hd, groups))
+    want = orc.add(r, orc.qlinear_bf16(orc.repeat_kv(v, kvh, hd, groups), hw, 64, 4))
+    check(dw["y"], want)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("m", [1, 2])
+def test_norm_gate_up_swiglu(torch_gpu, bits, m):
+    k, n = 4096, 14336
+    x = bf16_acts(40 + m, m, k)
+    w = orc.f32_to_bf16(orc.normal(41, k, 1.0, 0.1))
+    hg, dg = qlayer(42, n, k, 64, bits)
+    hu, du = qlayer(43, n, k, 64, bits)
+    dg["y"], du["y"] = out_like(m, n), out_like(m, n)
+    mlxq.qmatmul_fused(dev(x, True), [dg, du], 64, bits, norm_weight=dev(w, True), eps=1e-5, swiglu=True)
+    xn = orc.rms_norm(x, w, 1e-5)
+    want = orc.silu_mul(orc.qlinear_bf16(xn, hg, 64, bits), orc.qlinear_bf16(xn, hu, 64, bits))
+    check(dg["y"], want)
+
+
+def test_down_residual_and_short_gate(torch_gpu):
+    """Residual epilogue at K = 14336; and a gate/up pair whose N is not a
+    multiple of 16 (ragged last row tile)."""
+    m = 2
+    a = bf16_acts(50, m, 14336)
+    r = bf16_acts(51, m, 4096)
+    hw, dw = qlayer(52, 4096, 14336, 64, 4)
+    dw["y"], dw["residual"] = out_like(m, 4096), dev(r, True)
+    mlxq.qmatmul_fused(dev(a, True), [dw], 64, 4)
+    check(dw["y"], orc.add(r, orc.qlinear_bf16(a, hw, 64, 4)))
+
+    x = bf16_acts(53, 1, 1024)
+    w = orc.f32_to_bf16(orc.normal(54, 1024, 1.0, 0.1))
+    hg, dg = qlayer(55, 1000, 1024, 64, 4)
+    hu, du = qlayer(56, 1000, 1024, 64, 4)
+    dg["y"], du["y"] = out_like(1, 1000), out_like(1, 1000)
+    mlxq.qmatmul_fused(dev(x, True), [dg, du], 64, 4, norm_weight=dev(w, True), eps=1e-5, swiglu=True)
+    xn = orc.rms_norm(x, w, 1e-5)
+    check(dg["y"], orc.silu_mul(orc.qlinear_bf16(xn, hg, 64, 4), orc.qlinear_bf16(xn, hu, 64, 4)))
+
+
+def test_unsupported_shapes_launch_nothing(torch_gpu):
+    hw, dw = qlayer(60, 256, 512, 64, 4)
+    dw["y"] = out_like(5, 256)
+    with pytest.raises(mlxq.Unsupported):  # M > 4 is not fused
+        mlxq.qmatmul_fused(dev(bf16_acts(61, 5, 512), True), [dw], 64, 4)
+    with pytest.raises(mlxq.Unsupported):  # SwiGLU without a norm weight
+        mlxq.qmatmul_fused(dev(bf16_acts(61, 1, 512), True), [dw, dict(dw)], 64, 4, swiglu=True)

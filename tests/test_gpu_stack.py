@@ -20,25 +20,26 @@ TOL = 1e-2
 SMALL = dict(layers=3, hidden=512, intermediate=1536, heads=8, kv_heads=2, head_dim=64, vocab=1000)
 
 
-def _run(cfg: StackConfig, batch: int, graph: bool):
+def _run(cfg: StackConfig, batch: int, graph: bool, fused: bool = True):
     st = DecodeStack(cfg, batch=batch, seed=7, norm_noise=0.1)
     x = orc.f32_to_bf16(orc.normal(1234 + batch, batch * cfg.hidden, 0.0, 1.0)).reshape(batch, cfg.hidden)
     st.x.copy_(dev(x, True))
     if graph:
-        g = st.capture()
+        g = st.capture(fused=fused)
         g.replay()
         g.replay()  # a replay must give the same result as the first
     else:
-        st.forward()
+        st.forward(fused=fused)
     got = host(st.logits)
     layers, norm, lm = st.host_weights()
     want = orc.decode_stack(x, layers, norm, lm, cfg.as_dict())
     return got, want
 
 
+@pytest.mark.parametrize("fused", [True, False])
 @pytest.mark.parametrize("batch", [1, 4, 16])
-def test_small_stack(torch_gpu, batch):
-    got, want = _run(StackConfig(**SMALL), batch, graph=False)
+def test_small_stack(torch_gpu, batch, fused):
+    got, want = _run(StackConfig(**SMALL), batch, graph=False, fused=fused)
     assert rel_err(orc.bf16_to_f32(got), orc.bf16_to_f32(want).astype(np.float64)) <= TOL
 
 
@@ -48,7 +49,7 @@ def test_small_stack_graph(torch_gpu, bits):
     assert rel_err(orc.bf16_to_f32(got), orc.bf16_to_f32(want).astype(np.float64)) <= TOL
 
 
-@pytest.mark.parametrize("batch", [1, 16])
+@pytest.mark.parametrize("batch", [1, 3, 16])
 def test_llama3_8b_width_two_layers(torch_gpu, batch):
     """Config-5 widths (hidden 4096, intermediate 14336, 32/8 heads x 128,
     vocab 128256, Q4 g64) with two layers, so the f64 CPU chain stays short."""
