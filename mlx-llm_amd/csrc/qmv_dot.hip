@@ -1,7 +1,7 @@
 // Host side of the vector-ALU decode GEMV (kernel: qmv_dot_kernel.hpp):
 // eligibility, launch configuration, and the plain (F = 0) instantiation.
-// The fused forms are instantiated in qmv_dot_norm.hip / qmv_dot_swiglu.hip
-// so the three compile in parallel.
+// The fused forms are instantiated in qmv_dot_norm.hip, qmv_dot_swiglu.hip
+// and qmv_dot_repeat.hip so the four compile in parallel.
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
@@ -27,6 +27,8 @@ int prologue_pieces(int64_t M, int64_t K, int bits, int wv) {
 
 size_t lds_bytes(int64_t M, int64_t K, int bits, int sub, int wv) {
   const int64_t kl = 64 * 8 / bits / 4;
+  // staged activations, segment sums, the cross-wave reduction (which also
+  // holds the RMSNorm partial sums before the contraction)
   return static_cast<size_t>(M * K * 2 + M * (K / kl) * 4 + wv * M * 16 * sub * 4);
 }
 
@@ -40,6 +42,7 @@ int cu_count() {
 int call(int f, int64_t M, int gs, int bits, const Cfg& c, const Params& a, hipStream_t st, int* q) {
   if (f == 0) return dispatch<0>(M, gs, bits, c, a, st, q);
   if (f == kNorm) return dispatch<kNorm>(M, gs, bits, c, a, st, q);
+  if (f == kRepeat) return dispatch<kRepeat>(M, gs, bits, c, a, st, q);
   return dispatch<kNorm | kSwiGLU>(M, gs, bits, c, a, st, q);
 }
 
@@ -72,7 +75,8 @@ int launch_qmv_dot_fused(const QmvFused& f, hipStream_t st) {
   if (f.rep > 1 && (f.rep_hd <= 0 || f.rep_hd % 8 || K % (static_cast<int64_t>(f.rep_hd) * f.rep)))
     return fail(MLXQ_ERR_SHAPE, "qmv_dot: head repeat does not tile K");
   if (f.swiglu && !f.norm_w) return fail(MLXQ_ERR_UNSUPPORTED, "qmv_dot: SwiGLU form expects a normalized input");
-  const int form = f.swiglu ? (kNorm | kSwiGLU) : (f.norm_w ? kNorm : 0);
+  if (f.rep > 1 && f.norm_w) return fail(MLXQ_ERR_UNSUPPORTED, "qmv_dot: norm and head repeat together");
+  const int form = f.swiglu ? (kNorm | kSwiGLU) : f.norm_w ? kNorm : f.rep > 1 ? kRepeat : 0;
 
   Params a{};
   a.x = f.x;
@@ -81,7 +85,9 @@ int launch_qmv_dot_fused(const QmvFused& f, hipStream_t st) {
   a.K = static_cast<int>(K);
   a.x_stride = static_cast<int>(f.x_stride);
   a.rep = f.rep > 1 ? f.rep : 1;
-  a.rep_hd = f.rep > 1 ? f.rep_hd : 1;
+  a.rep_hd8 = f.rep > 1 ? f.rep_hd / 8 : 1;
+  a.rcp_hd8 = 1.0f / static_cast<float>(a.rep_hd8);
+  a.rcp_grp = 1.0f / static_cast<float>(a.rep_hd8 * a.rep);
   a.nseg = f.nproj;
   for (int i = 0; i < f.nproj; i++) {
     const QmvProj& P = f.proj[i];
@@ -90,8 +96,8 @@ int launch_qmv_dot_fused(const QmvFused& f, hipStream_t st) {
 
   // Pick rows per workgroup (16 or 32) and waves per workgroup (4 or 8) so
   // that the whole grid is resident at once (no second, partly filled pass
-  // of workgroups), preferring the most waves in flight.  SwiGLU pairs a
-  // gate and an up sub-tile: always 2 sub-tiles of the same 16 rows.
+  // of workgroups), preferring the most waves in flight.  SwiGLU streams 16
+  // rows of gate and up in one workgroup, half of its waves on each.
   static const int cus = cu_count();
   const int64_t chunks = K * f.bits / 8 / 64;
   Cfg best;
@@ -100,7 +106,7 @@ int launch_qmv_dot_fused(const QmvFused& f, hipStream_t st) {
   if (const char* e = getenv("MLXQ_QMV_DOT")) sscanf(e, "%d,%d", &forced_sub, &forced_wv);
   for (int sub = 1; sub <= 2; sub++)
     for (int wv = 4; wv <= 8; wv += 4) {
-      if (f.swiglu && sub != 2) continue;
+      if (f.swiglu && sub != 1) continue;
       if (!f.swiglu && ((forced_sub && sub != forced_sub) || (forced_wv && wv != forced_wv))) continue;
       Cfg c;
       c.sub = sub;
@@ -108,8 +114,7 @@ int launch_qmv_dot_fused(const QmvFused& f, hipStream_t st) {
       c.pt = prologue_pieces(M, K, f.bits, wv);
       c.lds = lds_bytes(M, K, f.bits, sub, wv);
       if (c.pt > 8 || c.lds > 160 * 1024) continue;
-      const int rows = f.swiglu ? 16 : 16 * sub;
-      for (int i = 0; i < (f.swiglu ? 1 : f.nproj); i++) c.tiles += ceil_div(f.proj[i].N, rows);
+      for (int i = 0; i < (f.swiglu ? 1 : f.nproj); i++) c.tiles += ceil_div(f.proj[i].N, 16 * sub);
       int nb = 0;
       if (int rc = call(form, M, f.group_size, f.bits, c, a, st, &nb)) return rc;
       const int64_t slots = std::max<int64_t>(1, static_cast<int64_t>(nb) * cus);
@@ -123,8 +128,10 @@ int launch_qmv_dot_fused(const QmvFused& f, hipStream_t st) {
     }
   if (best_pass < 0) return fail(MLXQ_ERR_INVALID, "qmv_dot: no configuration fits this shape");
   // each wave owns a contiguous range of whole rounds of chunks
-  a.cw = static_cast<int>(ceil_div(ceil_div(chunks, best.wv), kRound) * kRound);
-  const int rows = f.swiglu ? 16 : 16 * best.sub;
+  const int rc = round_chunks(f.bits, f.group_size, best.sub);
+  const int kw = f.swiglu ? best.wv / 2 : best.wv;  // waves sharing one row tile's K
+  a.cw = static_cast<int>(ceil_div(ceil_div(chunks, kw), rc) * rc);
+  const int rows = 16 * best.sub;
   int64_t end = 0;
   for (int i = 0; i < f.nproj; i++) {
     if (!(f.swiglu && i)) end += ceil_div(f.proj[i].N, rows);

@@ -28,15 +28,17 @@
 //
 // Fused forms (the decode layer chain of src/models/llama.rs:689-735 around
 // the projections, at MLX's bf16 rounding points):
-//  * kNorm: the activations are RMS-normalized while they are staged
-//    (nn.rs:35-37): x' = bf16(w * bf16(x * 1/sqrt(mean(x^2) + eps))).
-//  * GQA head repeat of the activations (attention.rs:45-55) by index
-//    remapping of the staging loads (runtime, rep > 1).
+//  * kNorm: RMSNorm of the activations while they are staged (nn.rs:35-37),
+//    at MLX's rounding points: x' = bf16(w * bf16(x * inv)), inv =
+//    1/sqrt(mean(x^2) + eps) from f32 sums (one extra barrier).
+//  * kRepeat: GQA head repeat of the activations (attention.rs:45-55) by
+//    index remapping of the staging loads.
 //  * Several projections of the same activations in one launch (q, k, v):
 //    the workgroups are split over up to kMaxSegs weight matrices.
 //  * residual epilogue (llama.rs:729-733): y = bf16(r + bf16(acc)).
-//  * kSwiGLU: gate and up rows of the same index in one workgroup and the
-//    epilogue y = bf16(bf16(g * bf16(sigmoid(g))) * u) with g, u the bf16
+//  * kSwiGLU: gate and up rows of the same index in one workgroup (its first
+//    half of waves streams the gate rows, the second half the up rows) and
+//    the epilogue y = bf16(bf16(g * bf16(sigmoid(g))) * u) with g, u the bf16
 //    projection outputs (llama.rs:1040-1045).
 #pragma once
 
@@ -55,7 +57,16 @@ constexpr int kMaxWaves = 8;  // waves per workgroup: 4 or 8 (chosen per shape)
 constexpr int kRound = 4;     // chunks per round
 constexpr int kMaxSegs = 3;   // weight matrices per launch
 
-enum : int { kNorm = 1, kSwiGLU = 2 };
+enum : int { kNorm = 1, kSwiGLU = 2, kRepeat = 4 };
+
+// chunks per round: 4, or 2 when a wave streams 2 row sub-tiles (keeps the
+// two rounds in flight within 128 registers) and a 2-chunk round still
+// covers an even number of groups (whole 32-bit parameter words)
+constexpr int round_chunks(int bits, int gs, int sub) {
+  const int gb = gs * bits / 8;
+  const int groups4 = kRound * (gb >= 64 ? 1 : 64 / gb) / (gb > 64 ? gb / 64 : 1);
+  return sub >= 2 && groups4 >= 4 ? 2 : kRound;
+}
 
 struct Seg {
   const uint32_t* wq;
@@ -75,7 +86,8 @@ struct Params {
   int K;
   int cw;  // chunks per wave
   int x_stride;
-  int rep_hd, rep;  // GQA remap of the activation index (rep == 1: none)
+  int rep_hd8, rep;        // kRepeat: head size in 8-element pieces, query heads per KV head
+  float rcp_hd8, rcp_grp;  // 1 / rep_hd8, 1 / (rep_hd8 * rep) (division by reciprocal)
   int nseg;
   Seg seg[kMaxSegs];
 };
@@ -85,6 +97,21 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
 }
 
 __device__ __forceinline__ float bf16_round(float v) { return bf16_bits_to_f32(f32_to_bf16_bits(v)); }
+
+// two f32 -> packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32)
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+  bf16x2 v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// n / d for 0 <= n < 2^24, d >= 1, given rcp = 1/d: the f32 quotient is
+// within one of the true one; one correction each way makes it exact.
+__device__ __forceinline__ int div_rcp(int n, int d, float rcp) {
+  int q = static_cast<int>(static_cast<float>(n) * rcp);
+  q -= q * d > n;
+  q += (q + 1) * d <= n;
+  return q;
+}
 
 template <int BITS, int GS, int RC>
 struct DotGeom {
@@ -144,7 +171,7 @@ template <int BITS, int GS, int MV, int SUB, int RC, int PT, int WV, int F>
 __global__ __launch_bounds__(64 * WV) void qmv_dot_kernel(const Params p) {
   using Gm = DotGeom<BITS, GS, RC>;
   using Rnd = DotRound<BITS, GS, SUB, RC>;
-  static_assert(!(F & kSwiGLU) || SUB == 2, "SwiGLU pairs a gate and an up sub-tile");
+  static_assert(!(F & kSwiGLU) || SUB == 1, "SwiGLU splits the waves, not the rows");
   constexpr int R = 16 * SUB;
   constexpr int SEGP = Gm::KL / 8;  // pieces per segment
   constexpr float OFF = BITS == 4 ? 128.f : 0.f;
@@ -163,10 +190,13 @@ __global__ __launch_bounds__(64 * WV) void qmv_dot_kernel(const Params p) {
   const int64_t row_u4 = static_cast<int64_t>(K) * BITS / 128;
 
   // row tile of this workgroup: weight matrix `sg`, rows n0 .. n0 + R
-  // (SwiGLU: rows n0 .. n0 + 16 of both the gate and the up matrix)
+  // (SwiGLU: rows n0 .. n0 + 16; waves [0, WV/2) stream the gate matrix,
+  // waves [WV/2, WV) the up matrix, each half over the whole K)
+  constexpr int KW = (F & kSwiGLU) ? WV / 2 : WV;  // waves sharing one row tile's K
   int sg = 0, n0;
   if constexpr (F & kSwiGLU) {
     n0 = blockIdx.x * 16;
+    sg = wave / KW;
   } else {
     const int t = blockIdx.x;
     while (sg + 1 < p.nseg && t >= p.seg[sg].tile_end) sg++;
@@ -177,15 +207,28 @@ __global__ __launch_bounds__(64 * WV) void qmv_dot_kernel(const Params p) {
   //    them never waits for the (later, slower) weight loads
   const int kp8 = K / 8;  // pieces per activation row
   const int pieces = MV * kp8;
+  // activation row of piece i (M <= 4: compares instead of a division)
+  auto row_of = [&](int i) {
+    int m = 0;
+#pragma unroll
+    for (int t = 1; t < MV; t++) m += i >= t * kp8;
+    return m;
+  };
   uint4 xp[PT];
   uint4 nw[(F & kNorm) ? PT : 1];
 #pragma unroll
   for (int j = 0; j < PT; j++) {  // clamped, unconditional: no branch, no early wait
     const int i = min(tid * PT + j, pieces - 1);
-    const int m = i / kp8, k = (i - m * kp8) * 8;
-    const int src = p.rep > 1 ? (k / (p.rep_hd * p.rep)) * p.rep_hd + k % p.rep_hd : k;
-    xp[j] = *reinterpret_cast<const uint4*>(p.x + static_cast<int64_t>(m) * p.x_stride + src);
-    if constexpr (F & kNorm) nw[j] = reinterpret_cast<const uint4*>(p.norm_w)[k / 8];
+    const int m = row_of(i), k8 = i - m * kp8;
+    int src8 = k8;
+    if constexpr (F & kRepeat) {  // query head h reads KV head h / rep
+      const int grp = p.rep_hd8 * p.rep;
+      const int hq = div_rcp(k8, grp, p.rcp_grp);
+      const int r = k8 - hq * grp;
+      src8 = hq * p.rep_hd8 + (r - div_rcp(r, p.rep_hd8, p.rcp_hd8) * p.rep_hd8);
+    }
+    xp[j] = *reinterpret_cast<const uint4*>(p.x + static_cast<int64_t>(m) * p.x_stride + src8 * 8);
+    if constexpr (F & kNorm) nw[j] = reinterpret_cast<const uint4*>(p.norm_w)[k8];
   }
   __builtin_amdgcn_sched_barrier(0);  // keep the activation loads first
 
@@ -195,8 +238,8 @@ __global__ __launch_bounds__(64 * WV) void qmv_dot_kernel(const Params p) {
   const uint16_t* brow[SUB];
 #pragma unroll
   for (int s = 0; s < SUB; s++) {
-    const Seg& S = p.seg[(F & kSwiGLU) ? s : sg];
-    const int n = min(n0 + ((F & kSwiGLU) ? 0 : 16 * s) + r16, S.N - 1);  // rows past N repeat row N-1
+    const Seg& S = p.seg[sg];
+    const int n = min(n0 + 16 * s + r16, S.N - 1);  // rows past N repeat row N-1
     wrow[s] = reinterpret_cast<const uint4*>(S.wq) + n * row_u4 + gq;
     srow[s] = S.s + static_cast<int64_t>(n) * G;
     brow[s] = S.b + static_cast<int64_t>(n) * G;
@@ -207,7 +250,7 @@ __global__ __launch_bounds__(64 * WV) void qmv_dot_kernel(const Params p) {
   // round fetches none (the branches on cfull are wave-uniform).  Inside
   // fetch all register indices are compile-time, so a round stays in
   // registers.
-  const int cbeg = min(wave * p.cw, chunks), cend = min(chunks, cbeg + p.cw);
+  const int cbeg = min((wave % KW) * p.cw, chunks), cend = min(chunks, cbeg + p.cw);
   const int cfull = cbeg + ((cend - cbeg) / RC) * RC;  // end of the wave's full rounds
   auto fetch = [&](Rnd& T, int c0) {
     const int g0 = c0 * Gm::NGC / Gm::CPG;
@@ -225,22 +268,24 @@ __global__ __launch_bounds__(64 * WV) void qmv_dot_kernel(const Params p) {
   if (cfull > cbeg) fetch(cur, cbeg);
   __builtin_amdgcn_sched_barrier(0);  // the whole first round is in flight before the prologue
 
-  // 3a) RMSNorm: sum of squares per activation row over the workgroup
+  // 3a) RMSNorm: sums of x^2 per activation row over the workgroup, then
+  //     x' = bf16(w * bf16(x * inv)) in registers
   if constexpr (F & kNorm) {
+    float* ssq = red;  // [WV][MV]; red is next written after two more barriers
     float ss[MV];
 #pragma unroll
     for (int m = 0; m < MV; m++) ss[m] = 0.f;
 #pragma unroll
     for (int j = 0; j < PT; j++) {
       const int i = tid * PT + j;
-      const uint32_t ws[4] = {xp[j].x, xp[j].y, xp[j].z, xp[j].w};
+      const uint32_t xs[4] = {xp[j].x, xp[j].y, xp[j].z, xp[j].w};
       float q = 0.f;
 #pragma unroll
       for (int h = 0; h < 4; h++) {
-        const float a = bf16_bits_to_f32(ws[h] & 0xFFFFu), b = bf16_bits_to_f32(ws[h] >> 16);
+        const float a = bf16_bits_to_f32(xs[h] & 0xFFFFu), b = bf16_bits_to_f32(xs[h] >> 16);
         q = fmaf(a, a, fmaf(b, b, q));
       }
-      const int mi = i / kp8;
+      const int mi = row_of(min(i, pieces - 1));
 #pragma unroll
       for (int m = 0; m < MV; m++) ss[m] += (i < pieces && mi == m) ? q : 0.f;
     }
@@ -248,7 +293,7 @@ __global__ __launch_bounds__(64 * WV) void qmv_dot_kernel(const Params p) {
     for (int m = 0; m < MV; m++) {
 #pragma unroll
       for (int o = 32; o > 0; o >>= 1) ss[m] += __shfl_xor(ss[m], o, 64);
-      if (lane == 0) red[wave * MV + m] = ss[m];
+      if (lane == 0) ssq[wave * MV + m] = ss[m];
     }
     __syncthreads();
     float inv[MV];
@@ -256,12 +301,12 @@ __global__ __launch_bounds__(64 * WV) void qmv_dot_kernel(const Params p) {
     for (int m = 0; m < MV; m++) {
       float t = 0.f;
 #pragma unroll
-      for (int w = 0; w < WV; w++) t += red[w * MV + m];
+      for (int w = 0; w < WV; w++) t += ssq[w * MV + m];
       inv[m] = 1.0f / sqrtf(t / static_cast<float>(K) + p.eps);
     }
 #pragma unroll
     for (int j = 0; j < PT; j++) {
-      const int mi = min(tid * PT + j, pieces - 1) / kp8;
+      const int mi = row_of(min(tid * PT + j, pieces - 1));
       float iv = inv[0];
 #pragma unroll
       for (int m = 1; m < MV; m++) iv = mi == m ? inv[m] : iv;
@@ -270,10 +315,9 @@ __global__ __launch_bounds__(64 * WV) void qmv_dot_kernel(const Params p) {
       uint32_t o[4];
 #pragma unroll
       for (int h = 0; h < 4; h++) {
-        const float n0v = bf16_round(bf16_bits_to_f32(xs[h] & 0xFFFFu) * iv);
-        const float n1v = bf16_round(bf16_bits_to_f32(xs[h] >> 16) * iv);
-        o[h] = f32_to_bf16_bits(bf16_bits_to_f32(gw[h] & 0xFFFFu) * n0v) |
-               (f32_to_bf16_bits(bf16_bits_to_f32(gw[h] >> 16) * n1v) << 16);
+        const uint32_t nx = pack_bf16(bf16_bits_to_f32(xs[h] & 0xFFFFu) * iv, bf16_bits_to_f32(xs[h] >> 16) * iv);
+        o[h] = pack_bf16(bf16_bits_to_f32(gw[h] & 0xFFFFu) * bf16_bits_to_f32(nx & 0xFFFFu),
+                         bf16_bits_to_f32(gw[h] >> 16) * bf16_bits_to_f32(nx >> 16));
       }
       xp[j] = make_uint4(o[0], o[1], o[2], o[3]);
     }
@@ -418,10 +462,10 @@ __global__ __launch_bounds__(64 * WV) void qmv_dot_kernel(const Params p) {
       if (gq == 0) red[(wave * MV + m) * R + 16 * s + r16] = v;
     }
   __syncthreads();
-  auto wave_sum = [&](int m, int r) {
-    float sum = red[m * R + r];
+  auto wave_sum = [&](int m, int r, int w0) {  // waves w0 .. w0 + KW
+    float sum = red[(w0 * MV + m) * R + r];
 #pragma unroll
-    for (int w = 1; w < WV; w++) sum += red[(w * MV + m) * R + r];
+    for (int w = 1; w < KW; w++) sum += red[((w0 + w) * MV + m) * R + r];
     return sum;
   };
   if constexpr (F & kSwiGLU) {
@@ -430,7 +474,7 @@ __global__ __launch_bounds__(64 * WV) void qmv_dot_kernel(const Params p) {
     for (int i = tid; i < MV * 16; i += 64 * WV) {
       const int m = i / 16, r = i % 16, n = n0 + r;
       if (n >= Sg.N) continue;
-      float g = wave_sum(m, r), u = wave_sum(m, 16 + r);
+      float g = wave_sum(m, r, 0), u = wave_sum(m, r, KW);
       if (Sg.bias) g += bf16_bits_to_f32(Sg.bias[n]);
       if (Su.bias) u += bf16_bits_to_f32(Su.bias[n]);
       g = bf16_round(g);
@@ -444,7 +488,7 @@ __global__ __launch_bounds__(64 * WV) void qmv_dot_kernel(const Params p) {
     for (int i = tid; i < MV * R; i += 64 * WV) {
       const int m = i / R, r = i % R, n = n0 + r;
       if (n >= S.N) continue;
-      float sum = wave_sum(m, r);
+      float sum = wave_sum(m, r, 0);
       if (S.bias) sum += bf16_bits_to_f32(S.bias[n]);
       const int64_t o = static_cast<int64_t>(m) * S.N + n;
       if (S.res) sum = bf16_bits_to_f32(S.res[o]) + bf16_round(sum);
@@ -465,7 +509,7 @@ struct Cfg {
 // instead of launching (the choice between configurations needs it).
 template <int BITS, int GS, int MV, int SUB, int PT, int WV, int F>
 int run(const Cfg& c, const Params& a, hipStream_t st, int* query) {
-  auto kern = qmv_dot_kernel<BITS, GS, MV, SUB, kRound, PT, WV, F>;
+  auto kern = qmv_dot_kernel<BITS, GS, MV, SUB, round_chunks(BITS, GS, SUB), PT, WV, F>;
   static bool raised = false;  // once per process; the attribute is per function
   if (c.lds > 64 * 1024 && !raised) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -515,7 +559,7 @@ int run_m(int64_t M, const Cfg& c, const Params& a, hipStream_t st, int* q) {
 template <int BITS, int GS, int F>
 int run_cfg(int64_t M, const Cfg& c, const Params& a, hipStream_t st, int* q) {
   if constexpr (F & kSwiGLU) {
-    return c.wv == 4 ? run_m<BITS, GS, 2, 4, F>(M, c, a, st, q) : run_m<BITS, GS, 2, 8, F>(M, c, a, st, q);
+    return c.wv == 4 ? run_m<BITS, GS, 1, 4, F>(M, c, a, st, q) : run_m<BITS, GS, 1, 8, F>(M, c, a, st, q);
   } else {
     if (c.sub == 1) return c.wv == 4 ? run_m<BITS, GS, 1, 4, F>(M, c, a, st, q) : run_m<BITS, GS, 1, 8, F>(M, c, a, st, q);
     return c.wv == 4 ? run_m<BITS, GS, 2, 4, F>(M, c, a, st, q) : run_m<BITS, GS, 2, 8, F>(M, c, a, st, q);
@@ -538,6 +582,7 @@ int dispatch(int64_t M, int group_size, int bits, const Cfg& c, const Params& a,
 extern template int dispatch<0>(int64_t, int, int, const Cfg&, const Params&, hipStream_t, int*);
 extern template int dispatch<kNorm>(int64_t, int, int, const Cfg&, const Params&, hipStream_t, int*);
 extern template int dispatch<kNorm | kSwiGLU>(int64_t, int, int, const Cfg&, const Params&, hipStream_t, int*);
+extern template int dispatch<kRepeat>(int64_t, int, int, const Cfg&, const Params&, hipStream_t, int*);
 
 }  // namespace dot
 }  // namespace mlxq

@@ -54,4 +54,5 @@ def test_llama3_8b_width_two_layers(torch_gpu, batch):
     """Config-5 widths (hidden 4096, intermediate 14336, 32/8 heads x 128,
     vocab 128256, Q4 g64) with two layers, so the f64 CPU chain stays short."""
     got, want = _run(StackConfig(layers=2), batch, graph=True)
+    print("rel_err", rel_err(orc.bf16_to_f32(got), orc.bf16_to_f32(want).astype(np.float64)))
     assert rel_err(orc.bf16_to_f32(got), orc.bf16_to_f32(want).astype(np.float64)) <= TOL
