@@ -72,6 +72,22 @@ extern "C" int mlxq_qmatmul_algo(const void* x, int64_t M, const uint32_t* wq, c
   if (M <= kQmvDotMaxM && qmv_dot_eligible(M, N, K, group_size, bits) && !getenv("MLXQ_QMV_MFMA"))
     return launch_qmv_dot(xp, M, wq, sp, bp, bias, N, K, group_size, bits, yp, st);
 
+  // MLXQ_QMV_STREAM=1: the streaming matrix-core kernel (the fused entry
+  // point's M > 4 form) for plain calls too; measured at parity or slower
+  // than the block kernel below for most plain shapes, so not the default
+  if (M <= kQmvMaxM && qmv_mfma_eligible(M, K, group_size, bits) && getenv("MLXQ_QMV_STREAM")) {
+    QmvFused f{};
+    f.x = xp;
+    f.M = M;
+    f.K = K;
+    f.x_stride = K;
+    f.nproj = 1;
+    f.proj[0] = QmvProj{wq, sp, bp, bias, nullptr, yp, N};
+    f.group_size = group_size;
+    f.bits = bits;
+    return launch_qmv_mfma(f, st);
+  }
+
   // qmv in chunks of at most 32 activation rows (one launch for decode shapes)
   const QmvPlan full = qmv_plan_for(M, N, K, group_size, bits);
   if (full.workspace_bytes() > 0) {
@@ -142,7 +158,11 @@ extern "C" int mlxq_qmatmul_fused(const void* x, int64_t M, int64_t K, const voi
   f.swiglu = swiglu != 0;
   f.group_size = group_size;
   f.bits = bits;
-  if (M > kQmvDotMaxM)
-    return fail(MLXQ_ERR_UNSUPPORTED, "qmatmul_fused: M > " + std::to_string(kQmvDotMaxM) + " is not fused");
+  if (M > kQmvDotMaxM) {  // matrix-core form: plain, residual and multi-projection only
+    if (f.norm_w || f.swiglu || f.rep > 1 || M > kQmvMaxM)
+      return fail(MLXQ_ERR_UNSUPPORTED, "qmatmul_fused: for M > " + std::to_string(kQmvDotMaxM) +
+                                            " only the residual / multi-projection forms (M <= 32) are fused");
+    return launch_qmv_mfma(f, as_stream(stream));
+  }
   return launch_qmv_dot_fused(f, as_stream(stream));
 }

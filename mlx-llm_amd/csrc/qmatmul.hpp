@@ -58,6 +58,12 @@ struct QmvFused {
 };
 int launch_qmv_dot_fused(const QmvFused& f, hipStream_t st);
 
+// qmv_mfma: matrix-core GEMV for M <= kQmvMaxM with the streaming structure
+// of qmv_dot; plain and residual / multi-projection forms (no norm, SwiGLU or
+// head repeat: those return MLXQ_ERR_UNSUPPORTED).
+bool qmv_mfma_eligible(int64_t M, int64_t K, int group_size, int bits);
+int launch_qmv_mfma(const QmvFused& f, hipStream_t st);
+
 // qmm: LDS-dequant bf16 MFMA GEMM, any M, K % 64 == 0.  No workspace.
 int launch_qmm(const uint16_t* x, int64_t M, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
                const uint16_t* bias, int64_t N, int64_t K, int group_size, int bits, uint16_t* y, hipStream_t st);

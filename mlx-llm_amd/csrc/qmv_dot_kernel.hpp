@@ -83,6 +83,7 @@ struct Params {
   const uint16_t* x;       // activations, row stride x_stride
   const uint16_t* norm_w;  // [K] RMSNorm weight (kNorm)
   float eps;
+  int M;  // activation rows (the MFMA form; the vector-ALU form has M compiled in)
   int K;
   int cw;  // chunks per wave
   int x_stride;

@@ -165,18 +165,22 @@ class DecodeStack:
             P = L.proj
             xn = (self.xa if i % 2 == 0 else self.xb)[:b]
 
+            # where the single fused launch does not cover the shape (b > 4),
+            # the norm / head repeat / SwiGLU run as their own kernels and the
+            # projections still share launches with their residual adds
             def qkv(x=x, P=P, L=L):
                 mlxq.rms_norm(x, L.ln1, c.eps, out=n)
-                lin(n, P["q"], q), lin(n, P["k"], k), lin(n, P["v"], v)
+                fz(n, [self._proj(P["q"], q), self._proj(P["k"], k), self._proj(P["v"], v)],
+                   lambda: (lin(n, P["q"], q), lin(n, P["k"], k), lin(n, P["v"], v)))
 
             def oproj(x=x, P=P):
                 mlxq.repeat_kv(v, c.kv_heads, c.head_dim, c.groups, out=attn)
-                lin(attn, P["o"], o)
-                mlxq.add(x, o, out=h)
+                fz(attn, [self._proj(P["o"], h, res=x)], lambda: (lin(attn, P["o"], o), mlxq.add(x, o, out=h)))
 
             def mlp_in(P=P, L=L):
                 mlxq.rms_norm(h, L.ln2, c.eps, out=n)
-                lin(n, P["gate"], g), lin(n, P["up"], u)
+                fz(n, [self._proj(P["gate"], g), self._proj(P["up"], u)],
+                   lambda: (lin(n, P["gate"], g), lin(n, P["up"], u)))
                 mlxq.silu_mul(g, u, out=a)
 
             def down(P=P, xn=xn):

@@ -98,10 +98,29 @@ def test_down_residual_and_short_gate(torch_gpu):
     check(dg["y"], orc.silu_mul(orc.qlinear_bf16(xn, hg, 64, 4), orc.qlinear_bf16(xn, hu, 64, 4)))
 
 
+@pytest.mark.parametrize("m", [5, 16, 32])
+def test_matrix_core_residual_multi(torch_gpu, m):
+    """M > 4 runs the matrix-core form: several projections and residuals."""
+    x = bf16_acts(70 + m, m, 4096)
+    outs, want = [], []
+    for i, n in enumerate([4096, 1024]):
+        hw, dw = qlayer(71 + i, n, 4096, 64, 4)
+        r = bf16_acts(75 + i, m, n)
+        dw["y"], dw["residual"] = out_like(m, n), dev(r, True)
+        outs.append(dw)
+        want.append(orc.add(r, orc.qlinear_bf16(x, hw, 64, 4)))
+    mlxq.qmatmul_fused(dev(x, True), outs, 64, 4)
+    for d, w in zip(outs, want):
+        check(d["y"], w)
+
+
 def test_unsupported_shapes_launch_nothing(torch_gpu):
     hw, dw = qlayer(60, 256, 512, 64, 4)
     dw["y"] = out_like(5, 256)
-    with pytest.raises(mlxq.Unsupported):  # M > 4 is not fused
-        mlxq.qmatmul_fused(dev(bf16_acts(61, 5, 512), True), [dw], 64, 4)
+    w = dev(orc.f32_to_bf16(np.ones(512, dtype=np.float32)), True)
+    with pytest.raises(mlxq.Unsupported):  # the norm form needs M <= 4
+        mlxq.qmatmul_fused(dev(bf16_acts(61, 5, 512), True), [dw], 64, 4, norm_weight=w, eps=1e-5)
+    with pytest.raises(mlxq.Unsupported):  # more than 32 rows
+        mlxq.qmatmul_fused(dev(bf16_acts(61, 33, 512), True), [dw], 64, 4)
     with pytest.raises(mlxq.Unsupported):  # SwiGLU without a norm weight
         mlxq.qmatmul_fused(dev(bf16_acts(61, 1, 512), True), [dw, dict(dw)], 64, 4, swiglu=True)
