@@ -202,6 +202,22 @@ int mlxq_gguf_tensor_byte_len(uint32_t tag, int64_t n, int64_t* bytes);
 int mlxq_gguf_dequantize(uint32_t tag, const void* data, int64_t data_len,
                          int64_t n, int out_dtype, void* out, void* stream);
 
+/* Fused on-device convert of one projection weight, replacing for a GGUF
+ * tensor with a projection key the host chain of convert
+ * (src/gguf/convert.rs:131 dequantize, :133-137 q/k un-permute via
+ * permute_inverse_qk :232-256, :156 cast to bf16) and the snapshot writer's
+ * requant (:176 -> src/snapshot.rs:100-107 -> quant.rs:44).
+ * data: device bytes of the [rows, cols] GGUF tensor (tags as
+ * mlxq_gguf_dequantize); permute_heads > 0 un-permutes rows with that head
+ * count (llama q: num_heads, k: num_kv_heads), 0 leaves them.  Output: MLX
+ * affine wq [rows, cols*bits/32], bf16 scales/biases [rows, cols/group_size],
+ * bit-identical with mlxq_gguf_dequantize(BF16) -> row gather ->
+ * mlxq_quantize(BF16), with no intermediate tensor. */
+int mlxq_gguf_requantize(uint32_t tag, const void* data, int64_t data_len,
+                         int64_t rows, int64_t cols, int permute_heads,
+                         int group_size, int bits, uint32_t* wq, void* scales,
+                         void* biases, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -31,7 +31,7 @@ COMMON = [
     "-Wall", "-Wno-unused-result", "-Wno-unused-command-line-argument",
     f"-I{ROOT / 'include'}", f"-I{CSRC}",
 ]
-NO_CONTRACT = {"gguf.hip", "affine.hip"}
+NO_CONTRACT = {"gguf.hip", "affine.hip", "gguf_requant.hip"}
 
 
 def sources() -> list[Path]:

@@ -2,10 +2,7 @@
 //
 // Reference: QuantizedLinear::quantize / dequantize_weight
 // (src/primitives/quant.rs:38-53, :73-81) -> mlx_rs::ops::{quantize,dequantize}
-// (MLX 0.31.2).  Per group of `group_size` consecutive elements along a row:
-//   scale = max((max-min)/n_bins, 1e-7); the edge with the larger magnitude
-//   becomes the bias and the scale is snapped so that 0 is exactly on the grid;
-//   code = clamp(rint((w - bias)/scale), 0, n_bins), packed LSB-first.
+// (MLX 0.31.2); the per-group arithmetic is in affine_group.hpp.
 // Layout: every lane owns 8 consecutive elements; the group_size/8 lanes of a
 // group reduce min/max with butterfly shuffles, then each lane packs its own
 // codes into one (Q4) or two (Q8) uint32 words, so loads and stores are fully
@@ -15,6 +12,7 @@
 
 #include <string>
 
+#include "affine_group.hpp"
 #include "common.hpp"
 
 namespace mlxq {
@@ -67,52 +65,11 @@ __global__ __launch_bounds__(kThreads) void affine_quantize_kernel(const void* _
 #pragma unroll
     for (int i = 0; i < 8; i++) v[i] = 0.f;
   }
-  float w_max = v[0], w_min = v[0];
-#pragma unroll
-  for (int i = 1; i < 8; i++) {
-    w_max = fmaxf(w_max, v[i]);
-    w_min = fminf(w_min, v[i]);
-  }
-  // Butterfly within the LPG lanes of this group (groups never straddle a
-  // wavefront: LPG divides 64 and the lane index is group-aligned).
-#pragma unroll
-  for (int off = 1; off < LPG; off <<= 1) {
-    w_max = fmaxf(w_max, __shfl_xor(w_max, off, 64));
-    w_min = fminf(w_min, __shfl_xor(w_min, off, 64));
-  }
-  if (!active) return;
-
-  constexpr float n_bins = static_cast<float>((1 << BITS) - 1);
-  const float eps = 1e-7f;
-  const bool mask = fabsf(w_min) > fabsf(w_max);
-  float scale = fmaxf((w_max - w_min) / n_bins, eps);
-  scale = mask ? scale : -scale;
-  const float edge = mask ? w_min : w_max;
-  const float q0 = __builtin_rintf(edge / scale);
-  float bias = 0.f;
-  if (q0 != 0.f) {
-    scale = edge / q0;
-    bias = edge;
-  }
-
   uint32_t codes[8];
-#pragma unroll
-  for (int i = 0; i < 8; i++) {
-    float q = __builtin_rintf((v[i] - bias) / scale);
-    q = fminf(fmaxf(q, 0.f), n_bins);
-    codes[i] = static_cast<uint32_t>(q);
-  }
-  if constexpr (BITS == 4) {
-    uint32_t word = 0;
-#pragma unroll
-    for (int i = 0; i < 8; i++) word |= codes[i] << (4 * i);
-    wq[lane] = word;
-  } else {
-    uint2 words;
-    words.x = codes[0] | (codes[1] << 8) | (codes[2] << 16) | (codes[3] << 24);
-    words.y = codes[4] | (codes[5] << 8) | (codes[6] << 16) | (codes[7] << 24);
-    reinterpret_cast<uint2*>(wq)[lane] = words;
-  }
+  float scale, bias;
+  quantize_group8<BITS, LPG>(v, codes, scale, bias);
+  if (!active) return;
+  store_codes8<BITS>(wq, lane, codes);
   if ((threadIdx.x & (LPG - 1)) == 0) {
     const int64_t g = lane / LPG;
     store1<DT>(scales, g, scale);

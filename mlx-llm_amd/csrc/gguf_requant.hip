@@ -1,0 +1,178 @@
+// Fused GGUF -> MLX affine requantization of a projection weight, on device.
+//
+// Reference: the convert chain of src/gguf/convert.rs for a projection
+// tensor: dequantize (:131, dequant.rs:156-211), the llama q/k row
+// un-permute (:133-137, permute_inverse_qk :232-256), the cast to bf16
+// (:156, as_dtype(bf16): round to nearest even) and the snapshot writer's
+// requant (:176 -> snapshot.rs:100-107 -> quant.rs:44, mlx quantize of the
+// bf16 tensor).  The reference materializes the whole f32 tensor on the host
+// and then the bf16 copy; here every lane gathers the 8 consecutive elements
+// of its output row straight from the GGUF blocks (un-permuted source row),
+// rounds them to bf16 and quantizes its share of the group in registers, so
+// the only HBM traffic is the GGUF bytes in and the packed MLX tensor out.
+//
+// Bit-exactness: the element decode (gguf_decode.hpp) and the group
+// quantization (affine_group.hpp) are the ones of mlxq_gguf_dequantize and
+// mlxq_quantize; this file is compiled with -ffp-contract=off.
+#include <hip/hip_runtime.h>
+
+#include <string>
+
+#include "affine_group.hpp"
+#include "common.hpp"
+#include "gguf_decode.hpp"
+
+namespace mlxq {
+namespace {
+
+constexpr int kThreads = 256;
+
+// Element e of a float-typed GGUF tensor (F32 = 0, F16 = 1, BF16 = 30).
+template <int TAG>
+__device__ __forceinline__ float float_elem(const uint8_t* d, int64_t e) {
+  if constexpr (TAG == 0) {
+    return __uint_as_float(rd_u32(d + 4 * e));
+  } else if constexpr (TAG == 1) {
+    return f16_bits_to_f32(static_cast<uint32_t>(d[2 * e]) | (static_cast<uint32_t>(d[2 * e + 1]) << 8));
+  } else {
+    return bf16_bits_to_f32(static_cast<uint32_t>(d[2 * e]) | (static_cast<uint32_t>(d[2 * e + 1]) << 8));
+  }
+}
+
+template <int TAG>
+constexpr bool is_float_tag() {
+  return TAG == 0 || TAG == 1 || TAG == 30;
+}
+
+// lane = 8 consecutive output elements of row r = lane / (K / 8).
+// perm_hd > 0: source row of output row r within head h = r / perm_hd is
+// h * perm_hd + 2 * (rr % half) + rr / half with rr = r % perm_hd, half =
+// perm_hd / 2 (the inverse of llama.cpp's interleave).
+template <int TAG, int BITS, int LPG>
+__global__ __launch_bounds__(kThreads) void gguf_requant_kernel(const uint8_t* __restrict__ data, int64_t n_lanes,
+                                                                 int K, int perm_hd, uint32_t* __restrict__ wq,
+                                                                 uint16_t* __restrict__ scales,
+                                                                 uint16_t* __restrict__ biases) {
+  const int64_t lane = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  const bool active = lane < n_lanes;
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) v[i] = 0.f;
+  if (active) {
+    const int lpr = K / 8;  // lanes per row
+    const int64_t r = lane / lpr;
+    const int c = static_cast<int>(lane - r * lpr) * 8;
+    int64_t sr = r;
+    if (perm_hd > 0) {
+      const int64_t h = r / perm_hd;
+      const int rr = static_cast<int>(r - h * perm_hd), half = perm_hd / 2;
+      sr = h * perm_hd + 2 * (rr % half) + rr / half;
+    }
+    const int64_t e = sr * K + c;
+    if constexpr (is_float_tag<TAG>()) {
+#pragma unroll
+      for (int i = 0; i < 8; i++) v[i] = float_elem<TAG>(data, e + i);
+    } else {
+      constexpr int E = Geo<TAG>::E, B = Geo<TAG>::B;
+      const int64_t blk = e / E;
+      const int j0 = static_cast<int>(e - blk * E);  // 8 elements never straddle a block (E >= 32)
+      const uint8_t* b = data + blk * B;
+#pragma unroll
+      for (int i = 0; i < 8; i++) v[i] = decode<TAG>(b, j0 + i);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = bf16_bits_to_f32(f32_to_bf16_bits(v[i]));  // as_dtype(bf16)
+  }
+  uint32_t codes[8];
+  float scale, bias;
+  quantize_group8<BITS, LPG>(v, codes, scale, bias);  // every lane of the group takes part
+  if (!active) return;
+  store_codes8<BITS>(wq, lane, codes);
+  if ((threadIdx.x & (LPG - 1)) == 0) {
+    const int64_t g = lane / LPG;
+    scales[g] = static_cast<uint16_t>(f32_to_bf16_bits(scale));
+    biases[g] = static_cast<uint16_t>(f32_to_bf16_bits(bias));
+  }
+}
+
+template <int TAG, int BITS>
+int launch_bits(int group_size, int64_t lanes, int K, int perm_hd, const uint8_t* d, uint32_t* wq, uint16_t* s,
+                uint16_t* b, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>(ceil_div(lanes, kThreads)));
+  switch (group_size) {
+    case 32: hipLaunchKernelGGL((gguf_requant_kernel<TAG, BITS, 4>), grid, dim3(kThreads), 0, st, d, lanes, K, perm_hd, wq, s, b); break;
+    case 64: hipLaunchKernelGGL((gguf_requant_kernel<TAG, BITS, 8>), grid, dim3(kThreads), 0, st, d, lanes, K, perm_hd, wq, s, b); break;
+    default: hipLaunchKernelGGL((gguf_requant_kernel<TAG, BITS, 16>), grid, dim3(kThreads), 0, st, d, lanes, K, perm_hd, wq, s, b); break;
+  }
+  return check_launch("gguf_requantize");
+}
+
+template <int TAG>
+int launch_tag(int bits, int group_size, int64_t lanes, int K, int perm_hd, const uint8_t* d, uint32_t* wq,
+               uint16_t* s, uint16_t* b, hipStream_t st) {
+  if (bits == 4) return launch_bits<TAG, 4>(group_size, lanes, K, perm_hd, d, wq, s, b, st);
+  return launch_bits<TAG, 8>(group_size, lanes, K, perm_hd, d, wq, s, b, st);
+}
+
+}  // namespace
+}  // namespace mlxq
+
+using namespace mlxq;
+
+extern "C" int mlxq_gguf_requantize(uint32_t tag, const void* data, int64_t data_len, int64_t rows, int64_t cols,
+                                    int permute_heads, int group_size, int bits, uint32_t* wq, void* scales,
+                                    void* biases, void* stream) {
+  clear_error();
+  if (bits != 4 && bits != 8) return fail(MLXQ_ERR_UNSUPPORTED, "gguf_requantize: bits must be 4 or 8");
+  if (group_size != 32 && group_size != 64 && group_size != 128)
+    return fail(MLXQ_ERR_UNSUPPORTED, "gguf_requantize: group_size must be 32, 64 or 128");
+  if (rows < 0 || cols <= 0 || permute_heads < 0) return fail(MLXQ_ERR_INVALID, "gguf_requantize: bad shape");
+  if (cols % group_size)
+    return fail(MLXQ_ERR_SHAPE, "gguf_requantize: cols=" + std::to_string(cols) + " not divisible by group_size");
+  if (cols > INT32_MAX / 2 || rows > INT32_MAX) return fail(MLXQ_ERR_INVALID, "gguf_requantize: too large");
+  int64_t elems = 0, bbytes = 0;
+  if (int rc = mlxq_gguf_block(tag, &elems, &bbytes)) return rc;
+  const bool device_tag = tag == 0 || tag == 1 || tag == 30 || tag == 2 || tag == 3 || tag == 6 || tag == 7 ||
+                          tag == 8 || tag == 10 || tag == 11 || tag == 12 || tag == 13 || tag == 14 || tag == 20 ||
+                          tag == 23;
+  if (!device_tag) return fail(MLXQ_ERR_UNSUPPORTED, "gguf_requantize: GGUF type " + std::to_string(tag) +
+                                                         " has no device decoder");
+  if (cols % elems) return fail(MLXQ_ERR_SHAPE, "gguf_requantize: rows must hold whole blocks");
+  const int64_t n = rows * cols;
+  const int64_t need = n / elems * bbytes;
+  if (data_len < need)
+    return fail(MLXQ_ERR_SHORT_BUFFER, "gguf_requantize: need " + std::to_string(need) + " bytes of blocks, got " +
+                                           std::to_string(data_len));
+  int perm_hd = 0;
+  if (permute_heads > 0) {
+    if (rows % permute_heads) return fail(MLXQ_ERR_SHAPE, "gguf_requantize: rows not divisible by the head count");
+    perm_hd = static_cast<int>(rows / permute_heads);
+    if (perm_hd % 2) return fail(MLXQ_ERR_SHAPE, "gguf_requantize: odd head_dim");
+  }
+  if (n == 0) return MLXQ_OK;
+  if (!data || !wq || !scales || !biases) return fail(MLXQ_ERR_INVALID, "gguf_requantize: null pointer");
+  if ((reinterpret_cast<uintptr_t>(wq) & 7u)) return fail(MLXQ_ERR_INVALID, "gguf_requantize: wq must be 8-byte aligned");
+  const int64_t lanes = n / 8;
+  const int K = static_cast<int>(cols);
+  const uint8_t* d = static_cast<const uint8_t*>(data);
+  uint16_t* s = static_cast<uint16_t*>(scales);
+  uint16_t* b = static_cast<uint16_t*>(biases);
+  hipStream_t st = as_stream(stream);
+  switch (tag) {
+    case 0: return launch_tag<0>(bits, group_size, lanes, K, perm_hd, d, wq, s, b, st);
+    case 1: return launch_tag<1>(bits, group_size, lanes, K, perm_hd, d, wq, s, b, st);
+    case 30: return launch_tag<30>(bits, group_size, lanes, K, perm_hd, d, wq, s, b, st);
+    case 2: return launch_tag<2>(bits, group_size, lanes, K, perm_hd, d, wq, s, b, st);
+    case 3: return launch_tag<3>(bits, group_size, lanes, K, perm_hd, d, wq, s, b, st);
+    case 6: return launch_tag<6>(bits, group_size, lanes, K, perm_hd, d, wq, s, b, st);
+    case 7: return launch_tag<7>(bits, group_size, lanes, K, perm_hd, d, wq, s, b, st);
+    case 8: return launch_tag<8>(bits, group_size, lanes, K, perm_hd, d, wq, s, b, st);
+    case 10: return launch_tag<10>(bits, group_size, lanes, K, perm_hd, d, wq, s, b, st);
+    case 11: return launch_tag<11>(bits, group_size, lanes, K, perm_hd, d, wq, s, b, st);
+    case 12: return launch_tag<12>(bits, group_size, lanes, K, perm_hd, d, wq, s, b, st);
+    case 13: return launch_tag<13>(bits, group_size, lanes, K, perm_hd, d, wq, s, b, st);
+    case 14: return launch_tag<14>(bits, group_size, lanes, K, perm_hd, d, wq, s, b, st);
+    case 20: return launch_tag<20>(bits, group_size, lanes, K, perm_hd, d, wq, s, b, st);
+    default: return launch_tag<23>(bits, group_size, lanes, K, perm_hd, d, wq, s, b, st);
+  }
+}

@@ -49,6 +49,8 @@ SIGNATURES = {
     "mlxq_silu_mul": (ctypes.c_int, [_vp, _vp, _i64, _vp, _vp]),
     "mlxq_add": (ctypes.c_int, [_vp, _vp, _i64, _vp, _vp]),
     "mlxq_repeat_kv": (ctypes.c_int, [_vp, _i64, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp, _vp]),
+    "mlxq_gguf_requantize": (ctypes.c_int, [_u32, _vp, _i64, _i64, _i64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                            _vp, _vp, _vp, _vp]),
     "mlxq_gguf_block": (ctypes.c_int, [_u32, ctypes.POINTER(_i64), ctypes.POINTER(_i64)]),
     "mlxq_gguf_tensor_byte_len": (ctypes.c_int, [_u32, _i64, ctypes.POINTER(_i64)]),
     "mlxq_gguf_dequantize": (ctypes.c_int, [_u32, _vp, _i64, _i64, ctypes.c_int, _vp, _vp]),
@@ -291,3 +293,15 @@ def gguf_dequantize(tag: int, data, n: int, out_dtype=None, out=None):
     check(lib().mlxq_gguf_dequantize(tag, _ptr(data), data.numel(), n, _dtype_code(out.dtype), _ptr(out),
                                      _stream()))
     return out
+
+
+def gguf_requantize(tag: int, data, rows: int, cols: int, permute_heads: int = 0, group_size: int = 64,
+                    bits: int = 4):
+    """Fused GGUF blocks -> (un-permute) -> bf16 -> MLX affine (wq, scales, biases) on device."""
+    torch = _torch()
+    wq = torch.empty((rows, cols * bits // 32), dtype=torch.int32, device=data.device)
+    s = torch.empty((rows, cols // group_size), dtype=torch.bfloat16, device=data.device)
+    b = torch.empty_like(s)
+    check(lib().mlxq_gguf_requantize(tag, _ptr(data), data.numel(), rows, cols, permute_heads, group_size, bits,
+                                     _ptr(wq), _ptr(s), _ptr(b), _stream()))
+    return wq, s, b

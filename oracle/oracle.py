@@ -241,3 +241,26 @@ def decode_stack(x_bf16, layers, final_norm, lm_head, cfg) -> np.ndarray:
         a = silu_mul(qlinear_bf16(n2, L["gate"], gs, bits), qlinear_bf16(n2, L["up"], gs, bits))
         x = add(h, qlinear_bf16(a, L["down"], gs, bits))
     return qlinear_bf16(rms_norm(x, final_norm, eps), lm_head, gs, bits)
+
+
+def permute_inverse_qk(w: np.ndarray, n_head: int) -> np.ndarray:
+    """src/gguf/convert.rs:232-256: undo llama.cpp's q/k row interleave of a
+    [out, in] weight: HF row r = k*(hd/2) + j of a head comes from GGUF row
+    2*j + k."""
+    out = w.shape[0]
+    hd = out // n_head
+    half = hd // 2
+    r = np.arange(out)
+    h, rr = r // hd, r % hd
+    src = h * hd + 2 * (rr % half) + rr // half
+    return w[src]
+
+
+def gguf_requantize(tag: int, data: np.ndarray, rows: int, cols: int, permute_heads: int = 0,
+                    group_size: int = 64, bits: int = 4):
+    """The reference convert chain for one projection (convert.rs:131-176):
+    dequantize -> q/k un-permute -> bf16 -> MLX affine quantize of the bf16 tensor."""
+    w = gguf_dequantize(tag, data, rows * cols).reshape(rows, cols)
+    if permute_heads:
+        w = permute_inverse_qk(w, permute_heads)
+    return affine_quantize(f32_to_bf16(w), group_size, bits, BF16)

@@ -445,3 +445,23 @@ def test_repeat_kv_reference_known_answer():
     assert y.tolist() == [0.0, 1.0, 0.0, 1.0, 2.0, 3.0, 2.0, 3.0]
     # groups = 1 is the identity (attention.rs:281-285)
     assert np.array_equal(orc.repeat_kv(x, 2, 2, 1), x)
+
+
+def test_permute_inverse_qk_reference_known_answer():
+    # src/gguf/convert.rs:391-423: the llama.cpp forward interleave per head
+    # (reshape(n_head, 2, hd/2).swapaxes(1, 2): GGUF row 2j+k <- HF row k*hd/2+j)
+    # followed by the inverse must give back the HF rows, and is not the identity
+    n_head, hd, in_dim = 2, 4, 3
+    hf = np.arange(n_head * hd * in_dim, dtype=np.float32).reshape(n_head * hd, in_dim)
+    gguf = np.empty_like(hf)
+    half = hd // 2
+    for h in range(n_head):
+        for k in range(2):
+            for j in range(half):
+                gguf[h * hd + 2 * j + k] = hf[h * hd + k * half + j]
+    assert not np.array_equal(gguf, hf)
+    assert np.array_equal(orc.permute_inverse_qk(gguf, n_head), hf)
+    # Llama-3 k_proj geometry: 8 heads x 128 rows, a permutation of the rows
+    w = np.arange(1024, dtype=np.float32).reshape(1024, 1)
+    p = orc.permute_inverse_qk(w, 8).ravel()
+    assert sorted(p.tolist()) == w.ravel().tolist() and p[1] == 2.0 and p[64] == 1.0
