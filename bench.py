@@ -293,6 +293,19 @@ def bench_gguf(torch, mlxq, iters=10):
             us = e0.elapsed_time(e1) * 1e3 / iters
             gbs = (raw.numel() + n * ob) / (us * 1e-6) / 1e9
             entry[oname] = {"us": round(us, 1), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 3)}
+        # config 4's tail: the fused convert straight to MLX Q4 g64 (dequant ->
+        # bf16 -> requant in one pass; bytes = GGUF in + codes/scales/biases out)
+        rq = mlxq.gguf_requantize(tag, raw, 14336, 4096, 0, 64, 4)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(iters):
+            mlxq.gguf_requantize(tag, raw, 14336, 4096, 0, 64, 4, out=rq)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / iters
+        gbs = (raw.numel() + n // 2 + 2 * 2 * (n // 64)) / (us * 1e-6) / 1e9
+        entry["requant_q4g64"] = {"us": round(us, 1), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 3)}
         res[tname] = entry
         del raw
     return res

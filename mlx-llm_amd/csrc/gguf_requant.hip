@@ -16,6 +16,7 @@
 // mlxq_quantize; this file is compiled with -ffp-contract=off.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <string>
 
 #include "affine_group.hpp"
@@ -44,74 +45,105 @@ constexpr bool is_float_tag() {
   return TAG == 0 || TAG == 1 || TAG == 30;
 }
 
-// lane = 8 consecutive output elements of row r = lane / (K / 8).
-// perm_hd > 0: source row of output row r within head h = r / perm_hd is
-// h * perm_hd + 2 * (rr % half) + rr / half with rr = r % perm_hd, half =
-// perm_hd / 2 (the inverse of llama.cpp's interleave).
-template <int TAG, int BITS, int LPG>
-__global__ __launch_bounds__(kThreads) void gguf_requant_kernel(const uint8_t* __restrict__ data, int64_t n_lanes,
-                                                                 int K, int perm_hd, uint32_t* __restrict__ wq,
+// One workgroup per output row at a time (rows blockIdx.x, + gridDim.x, ...):
+// the source row's GGUF bytes (row sr = the un-permuted source of output row
+// r) are staged in LDS with 16-byte loads when aligned, then every lane
+// decodes 8 consecutive elements from LDS, rounds them to bf16 and
+// quantizes its share of the group.  perm_hd > 0: within head h = r /
+// perm_hd, output row rr = r % perm_hd reads source row h * perm_hd +
+// 2 * (rr % half) + rr / half (half = perm_hd / 2), the inverse of
+// llama.cpp's interleave.
+template <int TAG, int BITS, int LPG, bool ALIGNED16>
+__global__ __launch_bounds__(kThreads) void gguf_requant_kernel(const uint8_t* __restrict__ data, int rows, int K,
+                                                                 int row_bytes, int perm_hd,
+                                                                 uint32_t* __restrict__ wq,
                                                                  uint16_t* __restrict__ scales,
                                                                  uint16_t* __restrict__ biases) {
-  const int64_t lane = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
-  const bool active = lane < n_lanes;
-  float v[8];
-#pragma unroll
-  for (int i = 0; i < 8; i++) v[i] = 0.f;
-  if (active) {
-    const int lpr = K / 8;  // lanes per row
-    const int64_t r = lane / lpr;
-    const int c = static_cast<int>(lane - r * lpr) * 8;
-    int64_t sr = r;
+  extern __shared__ __align__(16) uint8_t lds[];
+  const int lpr = K / 8;  // lanes (8 elements each) per row
+  for (int r = blockIdx.x; r < rows; r += gridDim.x) {
+    int sr = r;
     if (perm_hd > 0) {
-      const int64_t h = r / perm_hd;
-      const int rr = static_cast<int>(r - h * perm_hd), half = perm_hd / 2;
+      const int h = r / perm_hd, rr = r - h * perm_hd, half = perm_hd / 2;
       sr = h * perm_hd + 2 * (rr % half) + rr / half;
     }
-    const int64_t e = sr * K + c;
-    if constexpr (is_float_tag<TAG>()) {
-#pragma unroll
-      for (int i = 0; i < 8; i++) v[i] = float_elem<TAG>(data, e + i);
+    const uint8_t* src = data + static_cast<int64_t>(sr) * row_bytes;
+    if constexpr (ALIGNED16) {
+      for (int i = threadIdx.x; i < row_bytes / 16; i += kThreads)
+        reinterpret_cast<uint4*>(lds)[i] = reinterpret_cast<const uint4*>(src)[i];
     } else {
-      constexpr int E = Geo<TAG>::E, B = Geo<TAG>::B;
-      const int64_t blk = e / E;
-      const int j0 = static_cast<int>(e - blk * E);  // 8 elements never straddle a block (E >= 32)
-      const uint8_t* b = data + blk * B;
-#pragma unroll
-      for (int i = 0; i < 8; i++) v[i] = decode<TAG>(b, j0 + i);
+      for (int i = threadIdx.x; i < row_bytes; i += kThreads) lds[i] = src[i];
     }
+    __syncthreads();
+    // lanes of the row in whole groups per pass (kThreads is a multiple of LPG
+    // and lpr of LPG, so a group's lanes are active together)
+    for (int l0 = 0; l0 < lpr; l0 += kThreads) {
+      const int l = l0 + threadIdx.x;
+      const bool active = l < lpr;
+      float v[8];
 #pragma unroll
-    for (int i = 0; i < 8; i++) v[i] = bf16_bits_to_f32(f32_to_bf16_bits(v[i]));  // as_dtype(bf16)
-  }
-  uint32_t codes[8];
-  float scale, bias;
-  quantize_group8<BITS, LPG>(v, codes, scale, bias);  // every lane of the group takes part
-  if (!active) return;
-  store_codes8<BITS>(wq, lane, codes);
-  if ((threadIdx.x & (LPG - 1)) == 0) {
-    const int64_t g = lane / LPG;
-    scales[g] = static_cast<uint16_t>(f32_to_bf16_bits(scale));
-    biases[g] = static_cast<uint16_t>(f32_to_bf16_bits(bias));
+      for (int i = 0; i < 8; i++) v[i] = 0.f;
+      if (active) {
+        const int e = l * 8;
+        if constexpr (is_float_tag<TAG>()) {
+#pragma unroll
+          for (int i = 0; i < 8; i++) v[i] = float_elem<TAG>(lds, e + i);
+        } else {
+          constexpr int E = Geo<TAG>::E, B = Geo<TAG>::B;
+          const int blk = e / E;
+          const uint8_t* b = lds + blk * B;
+#pragma unroll
+          for (int i = 0; i < 8; i++) v[i] = decode<TAG>(b, e - blk * E + i);  // 8 never straddle a block
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = bf16_bits_to_f32(f32_to_bf16_bits(v[i]));  // as_dtype(bf16)
+      }
+      uint32_t codes[8];
+      float scale, bias;
+      quantize_group8<BITS, LPG>(v, codes, scale, bias);  // every lane of the group takes part
+      if (active) {
+        const int64_t lane = static_cast<int64_t>(r) * lpr + l;
+        store_codes8<BITS>(wq, lane, codes);
+        if ((l & (LPG - 1)) == 0) {
+          const int64_t g = lane / LPG;
+          scales[g] = static_cast<uint16_t>(f32_to_bf16_bits(scale));
+          biases[g] = static_cast<uint16_t>(f32_to_bf16_bits(bias));
+        }
+      }
+    }
+    __syncthreads();  // the row's bytes are read before the next row is staged
   }
 }
 
-template <int TAG, int BITS>
-int launch_bits(int group_size, int64_t lanes, int K, int perm_hd, const uint8_t* d, uint32_t* wq, uint16_t* s,
-                uint16_t* b, hipStream_t st) {
-  const dim3 grid(static_cast<unsigned>(ceil_div(lanes, kThreads)));
-  switch (group_size) {
-    case 32: hipLaunchKernelGGL((gguf_requant_kernel<TAG, BITS, 4>), grid, dim3(kThreads), 0, st, d, lanes, K, perm_hd, wq, s, b); break;
-    case 64: hipLaunchKernelGGL((gguf_requant_kernel<TAG, BITS, 8>), grid, dim3(kThreads), 0, st, d, lanes, K, perm_hd, wq, s, b); break;
-    default: hipLaunchKernelGGL((gguf_requant_kernel<TAG, BITS, 16>), grid, dim3(kThreads), 0, st, d, lanes, K, perm_hd, wq, s, b); break;
+template <int TAG, int BITS, int LPG>
+int launch_lpg(int rows, int K, int row_bytes, int perm_hd, const uint8_t* d, uint32_t* wq, uint16_t* s,
+               uint16_t* b, hipStream_t st) {
+  const bool al = (reinterpret_cast<uintptr_t>(d) & 15u) == 0 && row_bytes % 16 == 0;
+  const size_t lds = (static_cast<size_t>(row_bytes) + 15) / 16 * 16;
+  const dim3 grid(static_cast<unsigned>(std::min(rows, 8192)));
+  auto kern = al ? gguf_requant_kernel<TAG, BITS, LPG, true> : gguf_requant_kernel<TAG, BITS, LPG, false>;
+  if (lds > 64 * 1024) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    if (e != hipSuccess) return fail(MLXQ_ERR_DEVICE, std::string("gguf_requantize: LDS size: ") + hipGetErrorString(e));
   }
+  hipLaunchKernelGGL(kern, grid, dim3(kThreads), lds, st, d, rows, K, row_bytes, perm_hd, wq, s, b);
   return check_launch("gguf_requantize");
 }
 
+template <int TAG, int BITS>
+int launch_bits(int group_size, int rows, int K, int row_bytes, int perm_hd, const uint8_t* d, uint32_t* wq,
+                uint16_t* s, uint16_t* b, hipStream_t st) {
+  if (group_size == 32) return launch_lpg<TAG, BITS, 4>(rows, K, row_bytes, perm_hd, d, wq, s, b, st);
+  if (group_size == 64) return launch_lpg<TAG, BITS, 8>(rows, K, row_bytes, perm_hd, d, wq, s, b, st);
+  return launch_lpg<TAG, BITS, 16>(rows, K, row_bytes, perm_hd, d, wq, s, b, st);
+}
+
 template <int TAG>
-int launch_tag(int bits, int group_size, int64_t lanes, int K, int perm_hd, const uint8_t* d, uint32_t* wq,
-               uint16_t* s, uint16_t* b, hipStream_t st) {
-  if (bits == 4) return launch_bits<TAG, 4>(group_size, lanes, K, perm_hd, d, wq, s, b, st);
-  return launch_bits<TAG, 8>(group_size, lanes, K, perm_hd, d, wq, s, b, st);
+int launch_tag(int bits, int group_size, int rows, int K, int row_bytes, int perm_hd, const uint8_t* d,
+               uint32_t* wq, uint16_t* s, uint16_t* b, hipStream_t st) {
+  if (bits == 4) return launch_bits<TAG, 4>(group_size, rows, K, row_bytes, perm_hd, d, wq, s, b, st);
+  return launch_bits<TAG, 8>(group_size, rows, K, row_bytes, perm_hd, d, wq, s, b, st);
 }
 
 }  // namespace
@@ -152,27 +184,28 @@ extern "C" int mlxq_gguf_requantize(uint32_t tag, const void* data, int64_t data
   if (n == 0) return MLXQ_OK;
   if (!data || !wq || !scales || !biases) return fail(MLXQ_ERR_INVALID, "gguf_requantize: null pointer");
   if ((reinterpret_cast<uintptr_t>(wq) & 7u)) return fail(MLXQ_ERR_INVALID, "gguf_requantize: wq must be 8-byte aligned");
-  const int64_t lanes = n / 8;
-  const int K = static_cast<int>(cols);
+  const int64_t row_bytes = cols / elems * bbytes;
+  if (row_bytes > 160 * 1024) return fail(MLXQ_ERR_UNSUPPORTED, "gguf_requantize: row larger than LDS");
+  const int K = static_cast<int>(cols), R = static_cast<int>(rows), RB = static_cast<int>(row_bytes);
   const uint8_t* d = static_cast<const uint8_t*>(data);
   uint16_t* s = static_cast<uint16_t*>(scales);
   uint16_t* b = static_cast<uint16_t*>(biases);
   hipStream_t st = as_stream(stream);
   switch (tag) {
-    case 0: return launch_tag<0>(bits, group_size, lanes, K, perm_hd, d, wq, s, b, st);
-    case 1: return launch_tag<1>(bits, group_size, lanes, K, perm_hd, d, wq, s, b, st);
-    case 30: return launch_tag<30>(bits, group_size, lanes, K, perm_hd, d, wq, s, b, st);
-    case 2: return launch_tag<2>(bits, group_size, lanes, K, perm_hd, d, wq, s, b, st);
-    case 3: return launch_tag<3>(bits, group_size, lanes, K, perm_hd, d, wq, s, b, st);
-    case 6: return launch_tag<6>(bits, group_size, lanes, K, perm_hd, d, wq, s, b, st);
-    case 7: return launch_tag<7>(bits, group_size, lanes, K, perm_hd, d, wq, s, b, st);
-    case 8: return launch_tag<8>(bits, group_size, lanes, K, perm_hd, d, wq, s, b, st);
-    case 10: return launch_tag<10>(bits, group_size, lanes, K, perm_hd, d, wq, s, b, st);
-    case 11: return launch_tag<11>(bits, group_size, lanes, K, perm_hd, d, wq, s, b, st);
-    case 12: return launch_tag<12>(bits, group_size, lanes, K, perm_hd, d, wq, s, b, st);
-    case 13: return launch_tag<13>(bits, group_size, lanes, K, perm_hd, d, wq, s, b, st);
-    case 14: return launch_tag<14>(bits, group_size, lanes, K, perm_hd, d, wq, s, b, st);
-    case 20: return launch_tag<20>(bits, group_size, lanes, K, perm_hd, d, wq, s, b, st);
-    default: return launch_tag<23>(bits, group_size, lanes, K, perm_hd, d, wq, s, b, st);
+    case 0: return launch_tag<0>(bits, group_size, R, K, RB, perm_hd, d, wq, s, b, st);
+    case 1: return launch_tag<1>(bits, group_size, R, K, RB, perm_hd, d, wq, s, b, st);
+    case 30: return launch_tag<30>(bits, group_size, R, K, RB, perm_hd, d, wq, s, b, st);
+    case 2: return launch_tag<2>(bits, group_size, R, K, RB, perm_hd, d, wq, s, b, st);
+    case 3: return launch_tag<3>(bits, group_size, R, K, RB, perm_hd, d, wq, s, b, st);
+    case 6: return launch_tag<6>(bits, group_size, R, K, RB, perm_hd, d, wq, s, b, st);
+    case 7: return launch_tag<7>(bits, group_size, R, K, RB, perm_hd, d, wq, s, b, st);
+    case 8: return launch_tag<8>(bits, group_size, R, K, RB, perm_hd, d, wq, s, b, st);
+    case 10: return launch_tag<10>(bits, group_size, R, K, RB, perm_hd, d, wq, s, b, st);
+    case 11: return launch_tag<11>(bits, group_size, R, K, RB, perm_hd, d, wq, s, b, st);
+    case 12: return launch_tag<12>(bits, group_size, R, K, RB, perm_hd, d, wq, s, b, st);
+    case 13: return launch_tag<13>(bits, group_size, R, K, RB, perm_hd, d, wq, s, b, st);
+    case 14: return launch_tag<14>(bits, group_size, R, K, RB, perm_hd, d, wq, s, b, st);
+    case 20: return launch_tag<20>(bits, group_size, R, K, RB, perm_hd, d, wq, s, b, st);
+    default: return launch_tag<23>(bits, group_size, R, K, RB, perm_hd, d, wq, s, b, st);
   }
 }

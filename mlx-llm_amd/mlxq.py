@@ -296,12 +296,16 @@ def gguf_dequantize(tag: int, data, n: int, out_dtype=None, out=None):
 
 
 def gguf_requantize(tag: int, data, rows: int, cols: int, permute_heads: int = 0, group_size: int = 64,
-                    bits: int = 4):
-    """Fused GGUF blocks -> (un-permute) -> bf16 -> MLX affine (wq, scales, biases) on device."""
+                    bits: int = 4, out=None):
+    """Fused GGUF blocks -> (un-permute) -> bf16 -> MLX affine (wq, scales, biases) on device.
+    out: optional preallocated (wq, scales, biases)."""
     torch = _torch()
-    wq = torch.empty((rows, cols * bits // 32), dtype=torch.int32, device=data.device)
-    s = torch.empty((rows, cols // group_size), dtype=torch.bfloat16, device=data.device)
-    b = torch.empty_like(s)
+    if out is None:
+        wq = torch.empty((rows, cols * bits // 32), dtype=torch.int32, device=data.device)
+        s = torch.empty((rows, cols // group_size), dtype=torch.bfloat16, device=data.device)
+        b = torch.empty_like(s)
+    else:
+        wq, s, b = out
     check(lib().mlxq_gguf_requantize(tag, _ptr(data), data.numel(), rows, cols, permute_heads, group_size, bits,
                                      _ptr(wq), _ptr(s), _ptr(b), _stream()))
     return wq, s, b
