@@ -64,11 +64,15 @@ __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
 }
 
 // One K step of global data held in registers by one thread.
-template <typename Gm>
+template <typename Gm, int NSG>
 struct Stage {
-  uint4 a[Gm::AU4];
-  uint4 b[Gm::BU4];
-  float s[2], z[2];  // scale/bias of the thread's codes (two groups only for g32 with 64 codes)
+  u32x4 a[Gm::AU4];  // native vectors (not uint4 structs) so the stage stays in registers
+  u32x4 b[Gm::BU4];
+  // scale/bias bits of the thread's codes (two groups only for g32 with 64
+  // codes).  Kept as loaded: converting at load time would make the
+  // compiler wait for these loads -- and, since loads retire in order, for
+  // the whole step's loads -- right after issuing them.
+  uint32_t s[NSG], z[NSG];
 };
 
 template <int BITS, int GS, int BM, int BN, int WM, int WN>
@@ -79,7 +83,9 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void qmm_kernel(const uint16_t* __
                                                                const uint16_t* __restrict__ bias_vec, int N, int K,
                                                                uint16_t* __restrict__ y) {
   using Gm = QmmGeom<BM, BN, WM, WN, BITS>;
-  using St = Stage<Gm>;
+  // scale/bias groups per thread per step: two only for g32 with 64 codes
+  constexpr int NSG = (GS == 32 && Gm::CPT == 64) ? 2 : 1;
+  using St = Stage<Gm, NSG>;
   constexpr int T = Gm::THREADS;
   extern __shared__ __align__(16) uint16_t lds[];
   const int tid = threadIdx.x;
@@ -92,18 +98,18 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void qmm_kernel(const uint16_t* __
 
   // activation loader: 8 threads per row (16 B each), rows tid/8 + (T/8) i
   const int a_chunk = tid & 7, a_row0 = tid >> 3;
-  const uint4* a_src = reinterpret_cast<const uint4*>(x) + a_chunk;
+  const u32x4* a_src = reinterpret_cast<const u32x4*>(x) + a_chunk;
   int a_off[Gm::AU4];  // uint4 offset of each row (rows past M repeat row M-1; results dropped)
 #pragma unroll
   for (int i = 0; i < Gm::AU4; i++) a_off[i] = min(m0 + a_row0 + (T / 8) * i, M - 1) * (K / 8);
   // weight loader: PARTS threads per row, each CPT consecutive codes
   const int b_row = tid / Gm::PARTS, b_part = tid % Gm::PARTS;
   const int b_n = min(n0 + b_row, N - 1);
-  const uint4* b_src = reinterpret_cast<const uint4*>(wq + b_n * row_words) + b_part * Gm::BU4;
+  const u32x4* b_src = reinterpret_cast<const u32x4*>(wq + b_n * row_words) + b_part * Gm::BU4;
   const uint16_t* s_src = scales + static_cast<int64_t>(b_n) * G;
   const uint16_t* z_src = biases + static_cast<int64_t>(b_n) * G;
 
-  auto load = [&](St& r, int kt) {
+  auto load = [&](St& r, int kt) __attribute__((always_inline)) {
     const int k0 = kt * BK;
 #pragma unroll
     for (int i = 0; i < Gm::AU4; i++) r.a[i] = a_src[a_off[i] + k0 / 8];
@@ -111,33 +117,33 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void qmm_kernel(const uint16_t* __
     for (int i = 0; i < Gm::BU4; i++) r.b[i] = b_src[k0 * BITS / 128 + i];
     const int kc = k0 + b_part * Gm::CPT;  // first code of this thread
     if constexpr (GS == 32 && Gm::CPT == 64) {
-      r.s[0] = bf16_bits_to_f32(s_src[kc / 32]);
-      r.s[1] = bf16_bits_to_f32(s_src[kc / 32 + 1]);
-      r.z[0] = bf16_bits_to_f32(z_src[kc / 32]);
-      r.z[1] = bf16_bits_to_f32(z_src[kc / 32 + 1]);
+      r.s[0] = s_src[kc / 32];
+      r.s[1] = s_src[kc / 32 + 1];
+      r.z[0] = z_src[kc / 32];
+      r.z[1] = z_src[kc / 32 + 1];
     } else {
-      r.s[0] = r.s[1] = bf16_bits_to_f32(s_src[kc / GS]);
-      r.z[0] = r.z[1] = bf16_bits_to_f32(z_src[kc / GS]);
+      r.s[0] = s_src[kc / GS];
+      r.z[0] = z_src[kc / GS];
     }
   };
 
-  auto store = [&](const St& r, int stage) {
+  auto store = [&](const St& r, int stage) __attribute__((always_inline)) {
     uint16_t* sa = lds + stage * Gm::STAGE;
     uint16_t* sb = sa + BM * LDR;
 #pragma unroll
     for (int i = 0; i < Gm::AU4; i++)
-      *reinterpret_cast<uint4*>(sa + (a_row0 + (T / 8) * i) * LDR + a_chunk * 8) = r.a[i];
+      *reinterpret_cast<u32x4*>(sa + (a_row0 + (T / 8) * i) * LDR + a_chunk * 8) = r.a[i];
     constexpr int NW = Gm::BU4 * 4;  // code words
     uint32_t w[NW];
 #pragma unroll
     for (int i = 0; i < Gm::BU4; i++) {
-      w[4 * i] = r.b[i].x; w[4 * i + 1] = r.b[i].y; w[4 * i + 2] = r.b[i].z; w[4 * i + 3] = r.b[i].w;
+      w[4 * i] = r.b[i][0]; w[4 * i + 1] = r.b[i][1]; w[4 * i + 2] = r.b[i][2]; w[4 * i + 3] = r.b[i][3];
     }
     uint32_t packed[Gm::CPT / 2];
     if constexpr (BITS == 4) {
 #pragma unroll
       for (int wi = 0; wi < NW; wi++) {  // word wi: codes 8 wi .. 8 wi + 7
-        const float sc = r.s[wi / 4], zz = r.z[wi / 4];
+        const float sc = bf16_bits_to_f32(r.s[NSG == 2 ? wi / 4 : 0]), zz = bf16_bits_to_f32(r.z[NSG == 2 ? wi / 4 : 0]);
         const uint32_t q = w[wi];
 #pragma unroll
         for (int j = 0; j < 4; j++)
@@ -147,16 +153,16 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void qmm_kernel(const uint16_t* __
     } else {
 #pragma unroll
       for (int wi = 0; wi < NW; wi++) {  // word wi: codes 4 wi .. 4 wi + 3
-        const float sc = r.s[wi / 8], zz = r.z[wi / 8];
+        const float sc = bf16_bits_to_f32(r.s[NSG == 2 ? wi / 8 : 0]), zz = bf16_bits_to_f32(r.z[NSG == 2 ? wi / 8 : 0]);
         const uint32_t q = w[wi];
         packed[2 * wi] = pack_bf16(sc * static_cast<float>(q & 0xFFu) + zz, sc * static_cast<float>((q >> 8) & 0xFFu) + zz);
         packed[2 * wi + 1] = pack_bf16(sc * static_cast<float>((q >> 16) & 0xFFu) + zz, sc * static_cast<float>(q >> 24) + zz);
       }
     }
-    uint4* dst = reinterpret_cast<uint4*>(sb + b_row * LDR + b_part * Gm::CPT);
+    u32x4* dst = reinterpret_cast<u32x4*>(sb + b_row * LDR + b_part * Gm::CPT);
 #pragma unroll
     for (int i = 0; i < Gm::CPT / 8; i++)
-      dst[i] = make_uint4(packed[4 * i], packed[4 * i + 1], packed[4 * i + 2], packed[4 * i + 3]);
+      dst[i] = u32x4{packed[4 * i], packed[4 * i + 1], packed[4 * i + 2], packed[4 * i + 3]};
   };
 
   f32x16 acc[Gm::TM][Gm::TN];
@@ -180,7 +186,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void qmm_kernel(const uint16_t* __
   // One K step: LDS stage kt&1 holds step kt, `ready` holds step kt+1 and
   // `target` receives step kt+2.  Called with (r0, r1) and (r1, r0) in turn
   // so that the register roles are static.
-  auto step = [&](int kt, St& target, St& ready) {
+  auto step = [&](int kt, St& target, St& ready) __attribute__((always_inline)) {
     const int cur = kt & 1;
     if (kt + 2 < KT) load(target, kt + 2);
     __builtin_amdgcn_sched_barrier(0);
