@@ -31,6 +31,8 @@ sys.path.insert(0, str(ROOT / "mlx-llm_amd"))
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, published
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, published
 METRIC = "Q4/Q8 qmatmul GB/s & TFLOP/s (% roofline), Llama-3-8B proj shapes, 1 GPU"
+# measured HBM traffic per launch (bytes) of a dominant-kernel candidate, keyed (bits, M, K, N)
+TRAFFIC_BYTES = {(8, 32, 4096, 14336): 68_990_336}
 
 # (name, K, N): y[M, N] = x[M, K] . W[N, K]^T
 PROJ = [("q", 4096, 4096), ("k", 4096, 1024), ("v", 4096, 1024), ("o", 4096, 4096),
@@ -85,6 +87,10 @@ def main(argv=None) -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--quick", action="store_true", help="skip prefill / gguf / cpu legs")
+    ap.add_argument("--profile-shape", metavar="BITS,M,PROJ",
+                    help="only launch one sweep shape 40 times (for rocprofv3 counter runs), no JSON")
+    ap.add_argument("--profile-copy", action="store_true",
+                    help="only run a 64 MiB device copy 5 times (counter calibration), no JSON")
     a = ap.parse_args(argv)
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (no collectives, no sharding); "
@@ -94,6 +100,28 @@ def main(argv=None) -> int:
     import torch
 
     import mlxq
+
+    if a.profile_copy:
+        src = torch.empty(64 << 20, dtype=torch.uint8, device="cuda")
+        src.fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        return 0
+    if a.profile_shape:
+        bits, m, name = a.profile_shape.split(",")
+        bits, m = int(bits), int(m)
+        k, n = {p[0]: (p[1], p[2]) for p in PROJ}[name]
+        layers = make_layers(torch, mlxq, bits, 8, 0x5EED0000 + 100 * bits)
+        x = torch.randn((m, k), device="cuda").to(torch.bfloat16)
+        y = torch.empty((m, n), device="cuda", dtype=torch.bfloat16)
+        fns = [mlxq.bind_qmatmul(x, *L[name], GS, bits, out=y) for L in layers]
+        for _ in range(5):
+            for f in fns:
+                f()
+        torch.cuda.synchronize()
+        return 0
 
     torch.manual_seed(0)
     assert torch.cuda.is_available(), "bench.py needs a GPU"
@@ -193,9 +221,13 @@ def main(argv=None) -> int:
     avg_us = dt / dc
     achieved = dbytes / (avg_us * 1e-6) / 1e9
     kname = ("qmv_dot_kernel (vector ALU)" if dm <= 4 else "qmv_kernel (MFMA)")
+    # HBM bytes per launch from rocprofv3 FETCH_SIZE / WRITE_SIZE runs (scaled by
+    # a 64 MiB copy's readings), profiles/qmv_q8_m32_gate_traffic.md; known for
+    # that kernel only
+    traffic = TRAFFIC_BYTES.get((dbits, dm, dk, dn))
     roofline = {"kernel": f"{kname}, Q{dbits} g64, M={dm}, K={dk} -> N={dn}", "bound": "hbm",
                 "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                 "avg_launch_us": round(avg_us, 3), "algorithmic_bytes_per_launch": int(dbytes),
                 "share_of_step": round(dt * LAYERS / (ms_per_step * 1e3), 3)}
     # the north-star headline: Q4 g64 decode GEMV (M=1) at each projection shape
