@@ -40,6 +40,8 @@ extern "C" int mlxq_qmatmul_workspace_size(int64_t M, int64_t N, int64_t K, int 
   if (rc) return rc;
   if (!bytes) return fail(MLXQ_ERR_INVALID, "qmatmul: null output pointer");
   *bytes = qmv_plan_for(M, N, K, group_size, bits).workspace_bytes();
+  if (M > kQmvDotMaxM && M <= kQmvMaxM && qmv_tile_eligible(M, N, K, group_size, bits))
+    *bytes = qmv_tile_workspace_bytes(M, N);  // split-K partials and counters
   return MLXQ_OK;
 }
 
@@ -71,6 +73,20 @@ extern "C" int mlxq_qmatmul_algo(const void* x, int64_t M, const uint32_t* wq, c
   // decode rows on the vector ALUs (MLXQ_QMV_MFMA=1 forces the MFMA kernel)
   if (M <= kQmvDotMaxM && qmv_dot_eligible(M, N, K, group_size, bits) && !getenv("MLXQ_QMV_MFMA"))
     return launch_qmv_dot(xp, M, wq, sp, bp, bias, N, K, group_size, bits, yp, st);
+
+  // batched decode of the large projections: activations shared through
+  // LDS, K split across workgroups.  Measured faster than the block kernel
+  // below for N*K >= 2^25 from M = 8 (Q4), and for Q8 at M = 32 or with
+  // K > N from M = 16; the split's cross-workgroup hand-off costs more than
+  // it saves on smaller matrices.  MLXQ_QMV_TILE_ALL=1 takes it for every
+  // eligible shape, MLXQ_QMV_LEGACY=1 never.
+  const bool tile_pref =
+      N * K >= (int64_t(1) << 25) && (bits == 4 ? M >= 8 : (M >= 32 || (M >= 16 && K > N)));
+  if (M <= kQmvMaxM && qmv_tile_eligible(M, N, K, group_size, bits) && (tile_pref || getenv("MLXQ_QMV_TILE_ALL")) &&
+      !getenv("MLXQ_QMV_LEGACY") && !getenv("MLXQ_QMV_STREAM")) {
+    rc = launch_qmv_tile(xp, M, wq, sp, bp, bias, N, K, group_size, bits, yp, workspace, workspace_bytes, st);
+    if (rc != MLXQ_ERR_UNSUPPORTED) return rc;  // else: no split fits the workspace, use the block kernel
+  }
 
   // MLXQ_QMV_STREAM=1: the streaming matrix-core kernel (the fused entry
   // point's M > 4 form) for plain calls too; measured at parity or slower

@@ -64,6 +64,17 @@ int launch_qmv_dot_fused(const QmvFused& f, hipStream_t st);
 bool qmv_mfma_eligible(int64_t M, int64_t K, int group_size, int bits);
 int launch_qmv_mfma(const QmvFused& f, hipStream_t st);
 
+// qmv_tile: matrix-core GEMV for batched decode (M <= kQmvMaxM) with the
+// activations shared through LDS and an optional split of K across
+// workgroups (partials and arrival counters in the caller's workspace).
+// Returns MLXQ_ERR_UNSUPPORTED, without launching or setting an error, when
+// the shape would need a split the workspace cannot hold.
+bool qmv_tile_eligible(int64_t M, int64_t N, int64_t K, int group_size, int bits);
+size_t qmv_tile_workspace_bytes(int64_t M, int64_t N);
+int launch_qmv_tile(const uint16_t* x, int64_t M, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
+                    const uint16_t* bias, int64_t N, int64_t K, int group_size, int bits, uint16_t* y,
+                    void* workspace, size_t workspace_bytes, hipStream_t st);
+
 // qmm: LDS-dequant bf16 MFMA GEMM, any M, K % 64 == 0.  No workspace.
 int launch_qmm(const uint16_t* x, int64_t M, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
                const uint16_t* bias, int64_t N, int64_t K, int group_size, int bits, uint16_t* y, hipStream_t st);

@@ -1,0 +1,418 @@
+// Batched-decode quantized GEMV on the matrix cores (gfx950): 5..32
+// activation rows, the activations shared through LDS.
+//
+// Reference: QuantizedLinear::forward (src/primitives/quant.rs:56-70) ->
+// mlx_rs::ops::quantized_matmul at batched-decode shapes (MLX's qmv / small
+// qmm kernels).
+//
+// A wave that streams 16 weight rows and reads its own activations moves
+// 4M/16 bytes of activations per byte of Q4 codes (8x at M = 32): the
+// activation reads, not the weights, then fill the memory pipeline.  Here:
+//  * A workgroup of 4 waves covers 64 * SUB weight rows (each wave 16 * SUB
+//    of them) and walks its K range in rounds of two 64-byte chunks per row,
+//    all waves on the same round.  The round's activations (16 * MT rows x
+//    256 (Q4) / 128 (Q8) k) are loaded once by the workgroup, 16 bytes per
+//    load, and written to one of two LDS stages (rows padded by 16 bytes, so
+//    the 16 rows of an MFMA operand read hit distinct banks); every wave
+//    reads its MFMA A operands from there.  One barrier per round.
+//  * Codes, group parameters and activations of rounds r + 1 and r + 2 are
+//    in flight (three register slots) while round r is computed; a barrier
+//    does not wait for them (it waits only for the LDS writes).
+//  * Math per chunk as in the streaming GEMV: lane (r16, gq) loads 16 bytes
+//    of weight row r16; a 4 x 4 dword transpose across the lane rows gives
+//    group-pure MFMA blocks; P = sum x (OFF + q), S = sum x (MFMA against
+//    ones), acc += s P + (b - OFF s) S per group in f32.
+//  * Split K: when the row tiles alone cannot fill the CUs, blockIdx.y picks
+//    one of `splits` contiguous K ranges.  Each workgroup writes its f32
+//    partial tile to the caller's workspace and counts itself in; the last
+//    one to arrive adds the partials in split order (deterministic), adds
+//    the bias, stores bf16 y and resets the counter to zero.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstdlib>
+#include <string>
+#include <type_traits>
+
+#include "common.hpp"
+#include "mfma_blocks.hpp"
+#include "qmatmul.hpp"
+#include "qmv_dot_kernel.hpp"
+
+namespace mlxq {
+namespace tile {
+
+using dot::DotGeom;
+using dot::load_param_words;
+using mfma::Blk;
+using mfma::decode_q8;
+using mfma::f32x4;
+using mfma::mma;
+using mfma::transpose_rows;
+using mfma::u32x4;
+
+struct TileParams {
+  const uint16_t* x;
+  const uint32_t* wq;
+  const uint16_t* s;
+  const uint16_t* b;
+  const uint16_t* bias;
+  uint16_t* y;
+  float* part;      // [splits][M][N] partial sums (splits > 1)
+  uint32_t* count;  // [tiles] arrival counters, zero between calls
+  int M, N, K;
+  int splits;
+};
+
+constexpr int kMaxSplitsK = 16;  // most K splits of one call
+
+// Q4 codes of one dword (k0..k7, LSB first) -> bf16 (128 + k) pairs
+// (k0,k2),(k4,k6),(k1,k3),(k5,k7): two masks pick the even / odd nibbles
+// into bytes, then v_perm interleaves them with 0x43 bytes (0x43nn is the
+// bf16 of 128 + nn).  7 operations per dword.
+__device__ __forceinline__ void decode_q4_bytes(uint32_t q, uint32_t* b) {
+  const uint32_t lo = q & 0x0F0F0F0Fu, hi = (q >> 4) & 0x0F0F0F0Fu, c = 0x43434343u;
+  b[0] = __builtin_amdgcn_perm(lo, c, 0x00050004u);
+  b[1] = __builtin_amdgcn_perm(lo, c, 0x00070006u);
+  b[2] = __builtin_amdgcn_perm(hi, c, 0x00050004u);
+  b[3] = __builtin_amdgcn_perm(hi, c, 0x00070006u);
+}
+
+// 8 activations x0..x7 (4 dwords as loaded) -> the order of decode_q4_bytes:
+// (x0,x2),(x4,x6),(x1,x3),(x5,x7)
+__device__ __forceinline__ void act_order_q4_bytes(const uint32_t* x, uint32_t* a) {
+  a[0] = __builtin_amdgcn_perm(x[1], x[0], 0x05040100u);
+  a[1] = __builtin_amdgcn_perm(x[3], x[2], 0x05040100u);
+  a[2] = __builtin_amdgcn_perm(x[1], x[0], 0x07060302u);
+  a[3] = __builtin_amdgcn_perm(x[3], x[2], 0x07060302u);
+}
+
+template <int BITS, int GS, int MT, int WV, int NCH>
+struct TileGeom {
+  using Bk = Blk<BITS, GS>;
+  static constexpr int T = 64 * WV;                  // threads
+  static constexpr int MR = 16 * MT;                 // activation rows staged (padded)
+  static constexpr int KS = NCH * Bk::KC;            // k per slice
+  static constexpr int ROW16 = KS / 8 + 1;           // 16-byte slots per staged row (one of padding)
+  static constexpr int XP = MR * (KS / 8) / T;       // 16-byte activation pieces per thread
+  static constexpr int NG = KS / GS;                 // groups per slice
+  static constexpr int NGW = NG / 2;                 // parameter words per row and slice
+  static_assert(XP >= 1 && MR * (KS / 8) % T == 0, "activation pieces must divide over the threads");
+  static_assert(NG % 2 == 0 && (NGW == 2 || NGW % 4 == 0), "parameters load as whole vectors");
+};
+
+template <int BITS, int GS, int MT, int WV, int NCH>
+__global__ __launch_bounds__(64 * WV) void qmv_tile_kernel(const TileParams p) {
+  using Tg = TileGeom<BITS, GS, MT, WV, NCH>;
+  using Bk = typename Tg::Bk;
+  constexpr float OFF = BITS == 4 ? 128.f : 0.f;
+  __shared__ u32x4 xs[Tg::MR * Tg::ROW16];
+  __shared__ uint32_t last;
+
+  const int K = p.K, M = p.M, N = p.N;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, gq = lane >> 4;
+  const int G = K / GS;
+  const int64_t row_u4 = static_cast<int64_t>(K) * BITS / 128;
+  const int tile = blockIdx.x, split = blockIdx.y;
+  const int n0 = tile * 16 * WV + wave * 16;  // this wave's 16 weight rows
+  const int c0 = split * NCH;                 // first chunk of the slice
+  const int n = min(n0 + r16, N - 1);         // rows past N repeat row N-1 (results dropped)
+
+  // 1. activations of the slice (issued first: the LDS staging waits on them)
+  u32x4 xg[Tg::XP];
+  int xdst[Tg::XP];
+#pragma unroll
+  for (int i = 0; i < Tg::XP; i++) {
+    const int q = tid + Tg::T * i;
+    const int row = q / (Tg::KS / 8), col = q % (Tg::KS / 8);
+    // rows past M read row M-1: they only feed output rows >= M
+    xg[i] = *reinterpret_cast<const u32x4*>(p.x + static_cast<int64_t>(min(row, M - 1)) * K +
+                                            static_cast<int64_t>(c0) * Bk::KC + col * 8);
+    xdst[i] = row * Tg::ROW16 + col;
+  }
+  // 2. this lane's row's group parameters over the slice, then 3. its codes,
+  // chunk by chunk (the math on chunk c waits only for chunks <= c)
+  uint32_t sw[Tg::NGW], bw[Tg::NGW];
+  load_param_words<Tg::NGW>(p.s + static_cast<int64_t>(n) * G + c0 * Bk::KC / GS, sw);
+  load_param_words<Tg::NGW>(p.b + static_cast<int64_t>(n) * G + c0 * Bk::KC / GS, bw);
+  u32x4 w[NCH];
+  const u32x4* wrow = reinterpret_cast<const u32x4*>(p.wq) + n * row_u4 + gq;
+#pragma unroll
+  for (int c = 0; c < NCH; c++) w[c] = wrow[static_cast<int64_t>(c0 + c) * 4];
+  __builtin_amdgcn_sched_barrier(0);  // every load is issued before the first wait
+
+  // staged in the order of the Q4 decode (pairs (x0,x2),(x4,x6),...): the
+  // permutation is done once here instead of by every wave per block
+#pragma unroll
+  for (int i = 0; i < Tg::XP; i++) {
+    if constexpr (BITS == 4) {
+      const uint32_t xv[4] = {xg[i][0], xg[i][1], xg[i][2], xg[i][3]};
+      uint32_t a[4];
+      act_order_q4_bytes(xv, a);
+      xs[xdst[i]] = u32x4{a[0], a[1], a[2], a[3]};
+    } else {
+      xs[xdst[i]] = xg[i];
+    }
+  }
+  __syncthreads();
+
+  f32x4 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; mt++) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  uint32_t ones[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) ones[i] = 0x3F803F80u;  // bf16 1.0 pairs
+
+#pragma unroll
+  for (int c = 0; c < NCH; c++) {
+    uint32_t d[4] = {w[c][0], w[c][1], w[c][2], w[c][3]};
+    if constexpr (!Bk::NAT) transpose_rows(d);
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    f32x4 P[MT], SX[MT];
+#pragma unroll
+    for (int j = 0; j < Bk::NB; j++) {
+      const bool first = j % Bk::BPG == 0;
+      uint32_t bq[4];
+      if constexpr (BITS == 4) {
+        decode_q4_bytes(d[j], bq);
+      } else if constexpr (Bk::NAT) {
+        decode_q8(d[2 * j], bq);
+        decode_q8(d[2 * j + 1], bq + 2);
+      } else {
+        decode_q8(d[j], bq);
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; mt++) {
+        // A operand: activation row 16 mt + r16, this lane's slice of block j
+        const u32x4* rowp = xs + (16 * mt + r16) * Tg::ROW16;
+        const int e = c * Bk::KC + Bk::xoff(j, gq);
+        uint32_t a[4];
+        if constexpr (Bk::XW == 4) {
+          const u32x4 v = rowp[e / 8];
+          a[0] = v[0]; a[1] = v[1]; a[2] = v[2]; a[3] = v[3];
+        } else {
+          const uint2 v = reinterpret_cast<const uint2*>(rowp)[e / 4];
+          a[0] = v.x; a[1] = v.y;
+        }
+        SX[mt] = mma<Bk::X32>(a, ones, first ? zero : SX[mt]);
+        P[mt] = mma<Bk::X32>(a, bq, first ? zero : P[mt]);
+      }
+      if (j % Bk::BPG == Bk::BPG - 1) {
+        const int g = (c * Bk::KC + Bk::code0(j)) / GS;  // group within the slice (compile-time)
+        const float sc = __uint_as_float((g & 1) ? (sw[g >> 1] & 0xFFFF0000u) : (sw[g >> 1] << 16));
+        const float bb = __uint_as_float((g & 1) ? (bw[g >> 1] & 0xFFFF0000u) : (bw[g >> 1] << 16));
+        const float cf = bb - OFF * sc;
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+          for (int v = 0; v < 4; v++) acc[mt][v] = fmaf(sc, P[mt][v], fmaf(cf, SX[mt][v], acc[mt][v]));
+      }
+    }
+  }
+
+  // C layout of a 16x16 MFMA tile: lane holds column (weight row) r16 and
+  // activation rows 4 gq + v of the M-tile.
+  const int nn = n0 + r16;
+  if (p.splits == 1) {
+    if (nn < N) {
+      const float bb = p.bias ? bf16_bits_to_f32(p.bias[nn]) : 0.f;
+#pragma unroll
+      for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+          const int m = 16 * mt + 4 * gq + v;
+          if (m < M) p.y[static_cast<int64_t>(m) * N + nn] = static_cast<uint16_t>(f32_to_bf16_bits(acc[mt][v] + bb));
+        }
+    }
+    return;
+  }
+
+  // Split K: publish this workgroup's partials, count in; the last arrival
+  // reduces in split order.  The partials are written and read with
+  // device-coherent (agent-scope) accesses, which go past the per-XCD L2, so
+  // no cache-wide write-back or invalidate is needed: the stores only have
+  // to be complete (memory counter at zero) before the count is raised.
+  if (nn < N) {
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+      for (int v = 0; v < 4; v++) {
+        const int m = 16 * mt + 4 * gq + v;
+        if (m < M)
+          __hip_atomic_store(p.part + (static_cast<int64_t>(split) * M + m) * N + nn, acc[mt][v], __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+      }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_s_waitcnt(0);  // every partial store of this wave has completed
+  __syncthreads();
+  if (tid == 0)
+    last = __hip_atomic_fetch_add(&p.count[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                   static_cast<uint32_t>(p.splits - 1)
+               ? 1u
+               : 0u;
+  __syncthreads();
+  if (!last) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  if (nn < N) {
+    const float bb = p.bias ? bf16_bits_to_f32(p.bias[nn]) : 0.f;
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+      for (int v = 0; v < 4; v++) {
+        const int m = 16 * mt + 4 * gq + v;
+        if (m >= M) continue;
+        // all partials requested at once (unrolled over the maximum, the
+        // index clamped), then added in split order; absent splits add +0
+        float pv[kMaxSplitsK];
+#pragma unroll
+        for (int sp = 0; sp < kMaxSplitsK; sp++)
+          pv[sp] = __hip_atomic_load(p.part + (static_cast<int64_t>(min(sp, p.splits - 1)) * M + m) * N + nn,
+                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        float sum = 0.f;
+#pragma unroll
+        for (int sp = 0; sp < kMaxSplitsK; sp++) sum += sp < p.splits ? (sp == split ? acc[mt][v] : pv[sp]) : 0.f;
+        p.y[static_cast<int64_t>(m) * N + nn] = static_cast<uint16_t>(f32_to_bf16_bits(sum + bb));
+      }
+  }
+  if (tid == 0) __hip_atomic_store(&p.count[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------- launch
+
+constexpr int kMaxSplits = kMaxSplitsK;
+// Arrival counters sit at the start of the workspace in a region of fixed
+// size, whatever the shape, so that calls of different shapes sharing one
+// workspace never write partials over another shape's counters.
+constexpr int64_t kMaxCounters = 8192;
+constexpr size_t kCounterBytes = kMaxCounters * 4;
+
+struct Cfg {
+  int mt = 1, wv = 4, nch = 8;
+};
+
+template <int BITS, int MT, int WV, int NCH>
+int run(const TileParams& a, int tiles, hipStream_t st, int* query) {
+  auto kern = qmv_tile_kernel<BITS, 64, MT, WV, NCH>;
+  if (query) {
+    static int cached = -1;
+    if (cached < 0) {
+      int nb = 0;
+      hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void*>(kern), 64 * WV, 0);
+      if (e != hipSuccess) return fail(MLXQ_ERR_DEVICE, std::string("qmv_tile: occupancy: ") + hipGetErrorString(e));
+      cached = nb;
+    }
+    *query = cached;
+    return MLXQ_OK;
+  }
+  hipLaunchKernelGGL(kern, dim3(tiles, a.splits), dim3(64 * WV), 0, st, a);
+  return check_launch("qmv_tile");
+}
+
+// (waves, chunks per slice): slices of 16 chunks only with 8 waves, which
+// keeps the activation staging at <= 16 pieces per thread
+template <int BITS, int MT>
+int run_wn(const Cfg& c, const TileParams& a, int tiles, hipStream_t st, int* q) {
+  if (c.wv == 4) return c.nch == 4 ? run<BITS, MT, 4, 4>(a, tiles, st, q) : run<BITS, MT, 4, 8>(a, tiles, st, q);
+  if (c.nch == 4) return run<BITS, MT, 8, 4>(a, tiles, st, q);
+  return c.nch == 8 ? run<BITS, MT, 8, 8>(a, tiles, st, q) : run<BITS, MT, 8, 16>(a, tiles, st, q);
+}
+
+int dispatch(int bits, const Cfg& c, const TileParams& a, int tiles, hipStream_t st, int* q) {
+  if (bits == 4) return c.mt == 1 ? run_wn<4, 1>(c, a, tiles, st, q) : run_wn<4, 2>(c, a, tiles, st, q);
+  return c.mt == 1 ? run_wn<8, 1>(c, a, tiles, st, q) : run_wn<8, 2>(c, a, tiles, st, q);
+}
+
+int cu_count() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) return 256;
+  return cus;
+}
+
+int64_t chunks_of(int64_t K, int bits) { return K * bits / 8 / 64; }
+
+}  // namespace tile
+
+using namespace tile;
+
+bool qmv_tile_eligible(int64_t M, int64_t N, int64_t K, int group_size, int bits) {
+  if (M < 1 || M > kQmvMaxM || N < 1 || group_size != 64) return false;
+  if ((K * bits / 8) % 64) return false;
+  const int64_t ch = chunks_of(K, bits);
+  if (ch % 4 || ch > 16 * kMaxSplits) return false;  // whole slices of 4, 8 or 16 chunks, <= 16 slices
+  return static_cast<int64_t>(kMaxSplits) * M * N < (int64_t(1) << 31);
+}
+
+size_t qmv_tile_workspace_bytes(int64_t M, int64_t N) {
+  return kCounterBytes + static_cast<size_t>(kMaxSplits) * M * N * 4;
+}
+
+int launch_qmv_tile(const uint16_t* x, int64_t M, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
+                    const uint16_t* bias, int64_t N, int64_t K, int group_size, int bits, uint16_t* y,
+                    void* workspace, size_t workspace_bytes, hipStream_t st) {
+  if (!qmv_tile_eligible(M, N, K, group_size, bits))
+    return fail(MLXQ_ERR_UNSUPPORTED, "qmv_tile: shape not supported");
+  TileParams a{};
+  a.x = x;
+  a.wq = wq;
+  a.s = s;
+  a.b = b;
+  a.bias = bias;
+  a.y = y;
+  a.M = static_cast<int>(M);
+  a.N = static_cast<int>(N);
+  a.K = static_cast<int>(K);
+  const int64_t ch = chunks_of(K, bits);
+  const bool ws_ok = workspace && !(reinterpret_cast<uintptr_t>(workspace) & 255u) &&
+                     workspace_bytes >= kCounterBytes + static_cast<size_t>(M * N * 4) * 2;
+  const int64_t fit = ws_ok ? static_cast<int64_t>((workspace_bytes - kCounterBytes) / (M * N * 4)) : 1;
+
+  // Slices of 4, 8 or 16 chunks (every load of a slice in flight at once),
+  // workgroups of 4 or 8 waves (64 or 128 weight rows).  Prefer the choice
+  // whose grid is resident in one pass, then the one with more workgroups
+  // resident (more loads in flight), then fewer splits (less partial traffic).
+  static const int cus = cu_count();
+  Cfg best;
+  int64_t best_pass = -1, best_res = 0, best_split = 0, best_tiles = 0;
+  int fwv = 0, fnch = 0;
+  if (const char* e = getenv("MLXQ_QMV_TILE")) sscanf(e, "%d,%d", &fwv, &fnch);
+  for (int wv = 4; wv <= 8; wv += 4)
+    for (int nch = 4; nch <= 16; nch *= 2) {
+      if ((fwv && wv != fwv) || (fnch && nch != fnch) || ch % nch || (nch == 16 && wv != 8)) continue;
+      const int64_t splits = ch / nch;
+      if (splits > kMaxSplits || (splits > 1 && splits > fit)) continue;
+      Cfg c;
+      c.mt = M <= 16 ? 1 : 2;
+      c.wv = wv;
+      c.nch = nch;
+      const int64_t tiles = ceil_div(N, 16 * wv);
+      int nb = 0;
+      if (int rc = dispatch(bits, c, a, 1, st, &nb)) return rc;
+      const int64_t slots = std::max<int64_t>(1, static_cast<int64_t>(nb) * cus);
+      const int64_t wgs = tiles * splits;
+      const int64_t pass = ceil_div(wgs, slots);
+      const int64_t res = std::min(wgs, slots) * wv;  // resident waves
+      if (best_pass < 0 || pass < best_pass || (pass == best_pass && res > best_res) ||
+          (pass == best_pass && res == best_res && splits < best_split)) {
+        best = c;
+        best_pass = pass;
+        best_res = res;
+        best_split = splits;
+        best_tiles = tiles;
+      }
+    }
+  if (best_pass < 0) return MLXQ_ERR_UNSUPPORTED;  // no slicing fits the workspace: the caller picks another kernel
+  a.splits = static_cast<int>(best_split);
+  if (a.splits > 1) {
+    if (best_tiles > kMaxCounters) return fail(MLXQ_ERR_UNSUPPORTED, "qmv_tile: too many row tiles to split");
+    a.count = static_cast<uint32_t*>(workspace);
+    a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
+  }
+  return dispatch(bits, best, a, static_cast<int>(best_tiles), st, nullptr);
+}
+
+}  // namespace mlxq

@@ -161,14 +161,20 @@ def workspace_size(m: int, n: int, k: int, group_size: int = 64, bits: int = 4) 
 
 
 _ws = {}
+_ws_retired = []
 
 
 def workspace(nbytes: int, device):
-    """A zero-filled per-device workspace, grown on demand (kernels leave it zeroed)."""
+    """A per-device qmatmul workspace, zero-filled when allocated and grown on
+    demand.  The kernels leave its counter region at zero (the rest holds
+    scratch partial sums).  A workspace that is outgrown is kept alive, not
+    freed: work already queued or captured in a HIP graph may still use it."""
     torch = _torch()
     key = str(device)
     cur = _ws.get(key)
     if cur is None or cur.numel() < nbytes:
+        if cur is not None:
+            _ws_retired.append(cur)
         cur = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         _ws[key] = cur
     return cur

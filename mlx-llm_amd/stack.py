@@ -131,6 +131,13 @@ class DecodeStack:
         self.g, self.u, self.a = e(cfg.intermediate), e(cfg.intermediate), e(cfg.intermediate)
         self.d = e(cfg.hidden)
         self.logits = e(cfg.vocab)
+        # the qmatmul workspace for the largest projection call of any batch
+        # <= batch, reserved now so that no call grows it inside a capture
+        shapes = [(p.n, p.k) for p in [*self.layers[0].proj.values(), self.lm_head]]
+        need = max(mlxq.workspace_size(b, n, k, cfg.group_size, cfg.bits)
+                   for b in range(1, batch + 1) for n, k in shapes)
+        if need:
+            mlxq.workspace(need, self.device)
 
     def weight_bytes(self) -> int:
         """Packed weight bytes one decode step streams (codes + scales + biases)."""
