@@ -91,11 +91,10 @@ int mlxq_dequantize(const uint32_t* wq, const void* scales, const void* biases,
 /* ------------------------------------------------------------------ */
 
 /* Bytes of device workspace mlxq_qmatmul may use for this shape: nonzero
- * for batched decode (5 <= M <= 32, group size 64), where the large
- * projections split K across workgroups and hand partial sums over through
- * the workspace (a 32 KiB region of arrival counters, then partials).  The
- * workspace must be 256-byte aligned and zero-filled before its first use;
- * every call leaves the counter region at zero.  With no or too small a
+ * for batched decode (5 <= M <= 32, group size 64), where the projections
+ * may split K across workgroups and add the f32 partial sums in a second
+ * kernel.  The workspace must be 256-byte aligned; its contents need no
+ * initialisation and are scratch after a call.  With no or too small a
  * workspace the call still succeeds on an unsplit kernel. */
 int mlxq_qmatmul_workspace_size(int64_t M, int64_t N, int64_t K,
                                 int group_size, int bits, size_t* bytes);

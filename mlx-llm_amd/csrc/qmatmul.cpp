@@ -74,16 +74,13 @@ extern "C" int mlxq_qmatmul_algo(const void* x, int64_t M, const uint32_t* wq, c
   if (M <= kQmvDotMaxM && qmv_dot_eligible(M, N, K, group_size, bits) && !getenv("MLXQ_QMV_MFMA"))
     return launch_qmv_dot(xp, M, wq, sp, bp, bias, N, K, group_size, bits, yp, st);
 
-  // batched decode of the large projections: activations shared through
-  // LDS, K split across workgroups.  Measured faster than the block kernel
-  // below for N*K >= 2^25 from M = 8 (Q4), and for Q8 at M = 32 or with
-  // K > N from M = 16; the split's cross-workgroup hand-off costs more than
-  // it saves on smaller matrices.  MLXQ_QMV_TILE_ALL=1 takes it for every
-  // eligible shape, MLXQ_QMV_LEGACY=1 never.
-  const bool tile_pref =
-      N * K >= (int64_t(1) << 25) && (bits == 4 ? M >= 8 : (M >= 32 || (M >= 16 && K > N)));
-  if (M <= kQmvMaxM && qmv_tile_eligible(M, N, K, group_size, bits) && (tile_pref || getenv("MLXQ_QMV_TILE_ALL")) &&
-      !getenv("MLXQ_QMV_LEGACY") && !getenv("MLXQ_QMV_STREAM")) {
+  // batched decode: activations shared through LDS, K split across
+  // workgroups (qmv_tile.hip), where measured faster than the block kernel
+  // below.  MLXQ_QMV_TILE_ALL=1 takes it for every eligible shape,
+  // MLXQ_QMV_LEGACY=1 never.
+  if (M <= kQmvMaxM && qmv_tile_eligible(M, N, K, group_size, bits) &&
+      (qmv_tile_preferred(M, N, K, bits) || getenv("MLXQ_QMV_TILE_ALL")) && !getenv("MLXQ_QMV_LEGACY") &&
+      !getenv("MLXQ_QMV_STREAM")) {
     rc = launch_qmv_tile(xp, M, wq, sp, bp, bias, N, K, group_size, bits, yp, workspace, workspace_bytes, st);
     if (rc != MLXQ_ERR_UNSUPPORTED) return rc;  // else: no split fits the workspace, use the block kernel
   }

@@ -66,11 +66,13 @@ int launch_qmv_mfma(const QmvFused& f, hipStream_t st);
 
 // qmv_tile: matrix-core GEMV for batched decode (M <= kQmvMaxM) with the
 // activations shared through LDS and an optional split of K across
-// workgroups (partials and arrival counters in the caller's workspace).
+// workgroups (f32 partials in the caller's workspace, added by a second
+// kernel).
 // Returns MLXQ_ERR_UNSUPPORTED, without launching or setting an error, when
 // the shape would need a split the workspace cannot hold.
 bool qmv_tile_eligible(int64_t M, int64_t N, int64_t K, int group_size, int bits);
 size_t qmv_tile_workspace_bytes(int64_t M, int64_t N);
+bool qmv_tile_preferred(int64_t M, int64_t N, int64_t K, int bits);
 int launch_qmv_tile(const uint16_t* x, int64_t M, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
                     const uint16_t* bias, int64_t N, int64_t K, int group_size, int bits, uint16_t* y,
                     void* workspace, size_t workspace_bytes, hipStream_t st);

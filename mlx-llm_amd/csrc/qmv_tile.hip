@@ -8,25 +8,25 @@
 // A wave that streams 16 weight rows and reads its own activations moves
 // 4M/16 bytes of activations per byte of Q4 codes (8x at M = 32): the
 // activation reads, not the weights, then fill the memory pipeline.  Here:
-//  * A workgroup of 4 waves covers 64 * SUB weight rows (each wave 16 * SUB
-//    of them) and walks its K range in rounds of two 64-byte chunks per row,
-//    all waves on the same round.  The round's activations (16 * MT rows x
-//    256 (Q4) / 128 (Q8) k) are loaded once by the workgroup, 16 bytes per
-//    load, and written to one of two LDS stages (rows padded by 16 bytes, so
-//    the 16 rows of an MFMA operand read hit distinct banks); every wave
-//    reads its MFMA A operands from there.  One barrier per round.
-//  * Codes, group parameters and activations of rounds r + 1 and r + 2 are
-//    in flight (three register slots) while round r is computed; a barrier
-//    does not wait for them (it waits only for the LDS writes).
-//  * Math per chunk as in the streaming GEMV: lane (r16, gq) loads 16 bytes
-//    of weight row r16; a 4 x 4 dword transpose across the lane rows gives
-//    group-pure MFMA blocks; P = sum x (OFF + q), S = sum x (MFMA against
-//    ones), acc += s P + (b - OFF s) S per group in f32.
-//  * Split K: when the row tiles alone cannot fill the CUs, blockIdx.y picks
-//    one of `splits` contiguous K ranges.  Each workgroup writes its f32
-//    partial tile to the caller's workspace and counts itself in; the last
-//    one to arrive adds the partials in split order (deterministic), adds
-//    the bias, stores bf16 y and resets the counter to zero.
+//  * A workgroup of 4 or 8 waves covers 64 or 128 weight rows (16 per wave)
+//    over one slice of K (4, 8 or 16 64-byte chunks per row).  The slice's
+//    activations (16 * MT rows) are loaded once by the workgroup and staged
+//    in LDS (rows padded by 16 bytes, so the 16 rows of an MFMA operand read
+//    hit distinct banks; Q4 pairs pre-permuted to the code order), and every
+//    wave reads its MFMA A operands from there.
+//  * Every load of the slice is issued up front (activations, group
+//    parameters, then the codes chunk by chunk): one memory round trip, and
+//    the math on chunk c waits only for chunks <= c.
+//  * Math per chunk: lane (r16, gq) holds 16 bytes of weight row r16; a
+//    4 x 4 dword transpose across the lane rows gives group-pure MFMA
+//    blocks; P = sum x (OFF + q), S = sum x (MFMA against ones),
+//    acc += s P + (b - OFF s) S per group in f32.
+//  * Split K: blockIdx.y picks the slice.  With more than one slice the
+//    workgroups store f32 partial tiles in the caller's workspace and a
+//    second, elementwise kernel adds them in slice order (deterministic),
+//    adds the bias and stores bf16 y.  A hand-off inside the first kernel
+//    (last-arriving workgroup reduces) was measured slower: its device-scope
+//    stores, counter atomic and loads are three serial trips past the L2.
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
@@ -58,8 +58,7 @@ struct TileParams {
   const uint16_t* b;
   const uint16_t* bias;
   uint16_t* y;
-  float* part;      // [splits][M][N] partial sums (splits > 1)
-  uint32_t* count;  // [tiles] arrival counters, zero between calls
+  float* part;  // [splits][M][N] partial sums (splits > 1)
   int M, N, K;
   int splits;
 };
@@ -107,7 +106,6 @@ __global__ __launch_bounds__(64 * WV) void qmv_tile_kernel(const TileParams p) {
   using Bk = typename Tg::Bk;
   constexpr float OFF = BITS == 4 ? 128.f : 0.f;
   __shared__ u32x4 xs[Tg::MR * Tg::ROW16];
-  __shared__ uint32_t last;
 
   const int K = p.K, M = p.M, N = p.N;
   const int tid = threadIdx.x;
@@ -230,65 +228,34 @@ __global__ __launch_bounds__(64 * WV) void qmv_tile_kernel(const TileParams p) {
     return;
   }
 
-  // Split K: publish this workgroup's partials, count in; the last arrival
-  // reduces in split order.  The partials are written and read with
-  // device-coherent (agent-scope) accesses, which go past the per-XCD L2, so
-  // no cache-wide write-back or invalidate is needed: the stores only have
-  // to be complete (memory counter at zero) before the count is raised.
+  // partial tile of this slice; qmv_tile_reduce_kernel adds the slices
   if (nn < N) {
 #pragma unroll
     for (int mt = 0; mt < MT; mt++)
 #pragma unroll
       for (int v = 0; v < 4; v++) {
         const int m = 16 * mt + 4 * gq + v;
-        if (m < M)
-          __hip_atomic_store(p.part + (static_cast<int64_t>(split) * M + m) * N + nn, acc[mt][v], __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
+        if (m < M) p.part[(static_cast<int64_t>(split) * M + m) * N + nn] = acc[mt][v];
       }
   }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-  __builtin_amdgcn_s_waitcnt(0);  // every partial store of this wave has completed
-  __syncthreads();
-  if (tid == 0)
-    last = __hip_atomic_fetch_add(&p.count[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                   static_cast<uint32_t>(p.splits - 1)
-               ? 1u
-               : 0u;
-  __syncthreads();
-  if (!last) return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-  if (nn < N) {
-    const float bb = p.bias ? bf16_bits_to_f32(p.bias[nn]) : 0.f;
-#pragma unroll
-    for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-      for (int v = 0; v < 4; v++) {
-        const int m = 16 * mt + 4 * gq + v;
-        if (m >= M) continue;
-        // all partials requested at once (unrolled over the maximum, the
-        // index clamped), then added in split order; absent splits add +0
-        float pv[kMaxSplitsK];
-#pragma unroll
-        for (int sp = 0; sp < kMaxSplitsK; sp++)
-          pv[sp] = __hip_atomic_load(p.part + (static_cast<int64_t>(min(sp, p.splits - 1)) * M + m) * N + nn,
-                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        float sum = 0.f;
-#pragma unroll
-        for (int sp = 0; sp < kMaxSplitsK; sp++) sum += sp < p.splits ? (sp == split ? acc[mt][v] : pv[sp]) : 0.f;
-        p.y[static_cast<int64_t>(m) * N + nn] = static_cast<uint16_t>(f32_to_bf16_bits(sum + bb));
-      }
-  }
-  if (tid == 0) __hip_atomic_store(&p.count[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// y[m, n] = bf16(sum over splits of part[s, m, n] (in split order) + bias[n])
+__global__ __launch_bounds__(256) void qmv_tile_reduce_kernel(const float* __restrict__ part,
+                                                              const uint16_t* __restrict__ bias,
+                                                              uint16_t* __restrict__ y, int64_t MN, int N,
+                                                              int splits) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= MN) return;
+  float sum = 0.f;
+  for (int sp = 0; sp < splits; sp++) sum += part[sp * MN + i];
+  if (bias) sum += bf16_bits_to_f32(bias[i % N]);
+  y[i] = static_cast<uint16_t>(f32_to_bf16_bits(sum));
 }
 
 // ---------------------------------------------------------------- launch
 
 constexpr int kMaxSplits = kMaxSplitsK;
-// Arrival counters sit at the start of the workspace in a region of fixed
-// size, whatever the shape, so that calls of different shapes sharing one
-// workspace never write partials over another shape's counters.
-constexpr int64_t kMaxCounters = 8192;
-constexpr size_t kCounterBytes = kMaxCounters * 4;
 
 struct Cfg {
   int mt = 1, wv = 4, nch = 8;
@@ -347,8 +314,15 @@ bool qmv_tile_eligible(int64_t M, int64_t N, int64_t K, int group_size, int bits
   return static_cast<int64_t>(kMaxSplits) * M * N < (int64_t(1) << 31);
 }
 
-size_t qmv_tile_workspace_bytes(int64_t M, int64_t N) {
-  return kCounterBytes + static_cast<size_t>(kMaxSplits) * M * N * 4;
+size_t qmv_tile_workspace_bytes(int64_t M, int64_t N) { return static_cast<size_t>(kMaxSplits) * M * N * 4; }
+
+bool qmv_tile_preferred(int64_t M, int64_t N, int64_t K, int bits) {
+  // Measured against the block kernel (qmv.hip) at the Llama-3-8B projection
+  // shapes: the tile kernel wins on the large projections from M = 8 (Q4) /
+  // 16 (Q8; Q8 gate/up only at 32) and on the small ones from M = 24 (Q4)
+  // / 32 (Q8).
+  if (N * K >= (int64_t(1) << 25)) return bits == 4 ? M >= 8 : (M >= 32 || (M >= 16 && K > N));
+  return M >= (bits == 4 ? 24 : 32);
 }
 
 int launch_qmv_tile(const uint16_t* x, int64_t M, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
@@ -367,52 +341,50 @@ int launch_qmv_tile(const uint16_t* x, int64_t M, const uint32_t* wq, const uint
   a.N = static_cast<int>(N);
   a.K = static_cast<int>(K);
   const int64_t ch = chunks_of(K, bits);
-  const bool ws_ok = workspace && !(reinterpret_cast<uintptr_t>(workspace) & 255u) &&
-                     workspace_bytes >= kCounterBytes + static_cast<size_t>(M * N * 4) * 2;
-  const int64_t fit = ws_ok ? static_cast<int64_t>((workspace_bytes - kCounterBytes) / (M * N * 4)) : 1;
+  const bool ws_ok = workspace && !(reinterpret_cast<uintptr_t>(workspace) & 255u);
+  const int64_t fit = ws_ok ? static_cast<int64_t>(workspace_bytes / (M * N * 4)) : 1;  // slices that fit
 
-  // Slices of 4, 8 or 16 chunks (every load of a slice in flight at once),
-  // workgroups of 4 or 8 waves (64 or 128 weight rows).  Prefer the choice
-  // whose grid is resident in one pass, then the one with more workgroups
-  // resident (more loads in flight), then fewer splits (less partial traffic).
-  static const int cus = cu_count();
-  Cfg best;
-  int64_t best_pass = -1, best_res = 0, best_split = 0, best_tiles = 0;
+  // (waves, chunks per slice).  Measured best at the Llama-3-8B shapes
+  // (M = 8..32): large N*K with K >= 2N (down): 8 waves, 16-chunk slices;
+  // other large N*K: Q4 8 waves / 8 chunks, Q8 4 waves / 8 chunks; small
+  // N*K: 4 waves, 8 chunks (4 for Q4 with N < 2048).  Taken when it divides
+  // K into at most 16 slices that fit the workspace, else the first such of
+  // the others.
+  const bool large = N * K >= (int64_t(1) << 25);
+  Cfg pref;
+  pref.mt = M <= 16 ? 1 : 2;
+  if (large && K >= 2 * N) {
+    pref.wv = 8; pref.nch = 16;
+  } else if (large) {
+    pref.wv = bits == 4 ? 8 : 4; pref.nch = 8;
+  } else {
+    pref.wv = 4; pref.nch = bits == 4 && N < 2048 ? 4 : 8;
+  }
   int fwv = 0, fnch = 0;
   if (const char* e = getenv("MLXQ_QMV_TILE")) sscanf(e, "%d,%d", &fwv, &fnch);
-  for (int wv = 4; wv <= 8; wv += 4)
-    for (int nch = 4; nch <= 16; nch *= 2) {
-      if ((fwv && wv != fwv) || (fnch && nch != fnch) || ch % nch || (nch == 16 && wv != 8)) continue;
-      const int64_t splits = ch / nch;
-      if (splits > kMaxSplits || (splits > 1 && splits > fit)) continue;
-      Cfg c;
-      c.mt = M <= 16 ? 1 : 2;
-      c.wv = wv;
-      c.nch = nch;
-      const int64_t tiles = ceil_div(N, 16 * wv);
-      int nb = 0;
-      if (int rc = dispatch(bits, c, a, 1, st, &nb)) return rc;
-      const int64_t slots = std::max<int64_t>(1, static_cast<int64_t>(nb) * cus);
-      const int64_t wgs = tiles * splits;
-      const int64_t pass = ceil_div(wgs, slots);
-      const int64_t res = std::min(wgs, slots) * wv;  // resident waves
-      if (best_pass < 0 || pass < best_pass || (pass == best_pass && res > best_res) ||
-          (pass == best_pass && res == best_res && splits < best_split)) {
-        best = c;
-        best_pass = pass;
-        best_res = res;
-        best_split = splits;
-        best_tiles = tiles;
-      }
-    }
-  if (best_pass < 0) return MLXQ_ERR_UNSUPPORTED;  // no slicing fits the workspace: the caller picks another kernel
-  a.splits = static_cast<int>(best_split);
-  if (a.splits > 1) {
-    if (best_tiles > kMaxCounters) return fail(MLXQ_ERR_UNSUPPORTED, "qmv_tile: too many row tiles to split");
-    a.count = static_cast<uint32_t*>(workspace);
-    a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
+  if (fwv) pref.wv = fwv;
+  if (fnch) pref.nch = fnch;
+  const Cfg order[] = {pref, {pref.mt, 8, 16}, {pref.mt, 8, 8}, {pref.mt, 4, 8}, {pref.mt, 4, 4}, {pref.mt, 8, 4}};
+  const Cfg* pick = nullptr;
+  for (const Cfg& c : order) {
+    if ((c.wv != 4 && c.wv != 8) || (c.nch != 4 && c.nch != 8 && c.nch != 16) || (c.nch == 16 && c.wv != 8))
+      continue;
+    if (ch % c.nch) continue;
+    const int64_t splits = ch / c.nch;
+    if (splits > kMaxSplits || (splits > 1 && splits > fit)) continue;
+    pick = &c;
+    break;
   }
-  return dispatch(bits, best, a, static_cast<int>(best_tiles), st, nullptr);
+  if (!pick) return MLXQ_ERR_UNSUPPORTED;  // no slicing fits the workspace: the caller picks another kernel
+  a.splits = static_cast<int>(ch / pick->nch);
+  a.part = a.splits > 1 ? static_cast<float*>(workspace) : nullptr;
+  const int64_t tiles = ceil_div(N, 16 * pick->wv);
+  if (int rc = dispatch(bits, *pick, a, static_cast<int>(tiles), st, nullptr)) return rc;
+  if (a.splits == 1) return MLXQ_OK;
+  const int64_t mn = M * N;
+  hipLaunchKernelGGL(qmv_tile_reduce_kernel, dim3(static_cast<unsigned>(ceil_div(mn, 256))), dim3(256), 0, st, a.part,
+                     bias, y, mn, a.N, a.splits);
+  return check_launch("qmv_tile_reduce");
 }
 
 }  // namespace mlxq

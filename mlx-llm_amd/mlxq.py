@@ -165,10 +165,9 @@ _ws_retired = []
 
 
 def workspace(nbytes: int, device):
-    """A per-device qmatmul workspace, zero-filled when allocated and grown on
-    demand.  The kernels leave its counter region at zero (the rest holds
-    scratch partial sums).  A workspace that is outgrown is kept alive, not
-    freed: work already queued or captured in a HIP graph may still use it."""
+    """A per-device qmatmul workspace (scratch for split-K partial sums),
+    grown on demand.  A workspace that is outgrown is kept alive, not freed:
+    work already queued or captured in a HIP graph may still use it."""
     torch = _torch()
     key = str(device)
     cur = _ws.get(key)

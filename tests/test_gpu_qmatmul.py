@@ -72,7 +72,7 @@ def test_qmv_config1_single_decode(torch_gpu):
 
 
 def test_qmv_repeat_reuses_workspace(torch_gpu):
-    """Split-K tickets are left at zero: back-to-back calls agree bit-for-bit."""
+    """Back-to-back calls sharing the split-K scratch agree bit-for-bit."""
     wq, s, b = make_layer(5, 4096, 4096, 64, 4)
     x = bf16_acts(6, 4, 4096)
     y1 = run(x, wq, s, b, 64, 4)
