@@ -32,7 +32,7 @@ HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, published
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, published
 METRIC = "Q4/Q8 qmatmul GB/s & TFLOP/s (% roofline), Llama-3-8B proj shapes, 1 GPU"
 # measured HBM traffic per launch (bytes) of a dominant-kernel candidate, keyed (bits, M, K, N)
-TRAFFIC_BYTES = {(8, 32, 4096, 14336): 68_990_336}
+TRAFFIC_BYTES = {(8, 32, 4096, 14336): 95_480_765}
 
 # (name, K, N): y[M, N] = x[M, K] . W[N, K]^T
 PROJ = [("q", 4096, 4096), ("k", 4096, 1024), ("v", 4096, 1024), ("o", 4096, 4096),
@@ -220,10 +220,17 @@ def main(argv=None) -> int:
     (dbits, dm, (dk, dn)), (dt, dc, dbytes) = max(shapes.items(), key=lambda kv: kv[1][0])
     avg_us = dt / dc
     achieved = dbytes / (avg_us * 1e-6) / 1e9
-    kname = ("qmv_dot_kernel (vector ALU)" if dm <= 4 else "qmv_kernel (MFMA)")
-    # HBM bytes per launch from rocprofv3 FETCH_SIZE / WRITE_SIZE runs (scaled by
-    # a 64 MiB copy's readings), profiles/qmv_q8_m32_gate_traffic.md; known for
-    # that kernel only
+    # which kernels serve the call (the dispatch rule of qmatmul.cpp /
+    # qmv_tile.hip, restated here for the label only)
+    if dm <= 4:
+        kname = "qmv_dot_kernel (vector ALU)"
+    elif tile_preferred(dm, dn, dk, dbits):
+        kname = "qmv_tile_kernel + qmv_tile_reduce_kernel (MFMA, split K; one call = both launches)"
+    else:
+        kname = "qmv_kernel (MFMA)"
+    # HBM bytes per call (both kernels) from rocprofv3 FETCH_SIZE / WRITE_SIZE
+    # runs (scaled by a 64 MiB copy's readings), profiles/qmv_tile_q8_m32_gate_traffic.md;
+    # known for that call only
     traffic = TRAFFIC_BYTES.get((dbits, dm, dk, dn))
     roofline = {"kernel": f"{kname}, Q{dbits} g64, M={dm}, K={dk} -> N={dn}", "bound": "hbm",
                 "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -341,6 +348,13 @@ def bench_gguf(torch, mlxq, iters=10):
         res[tname] = entry
         del raw
     return res
+
+
+def tile_preferred(m, n, k, bits):
+    """The batched-decode kernel choice of qmv_tile.hip (qmv_tile_preferred)."""
+    if n * k >= 1 << 25:
+        return m >= 8 if bits == 4 else (m >= 32 or (m >= 16 and k > n))
+    return m >= (24 if bits == 4 else 32)
 
 
 def bench_stack(torch, steps=20, batches=(1, 16)):
