@@ -222,7 +222,7 @@ def main(argv=None) -> int:
     achieved = dbytes / (avg_us * 1e-6) / 1e9
     # which kernels serve the call (the dispatch rule of qmatmul.cpp /
     # qmv_tile.hip, restated here for the label only)
-    if dm <= 4:
+    if dot_preferred(dm, dn, dk, dbits):
         kname = "qmv_dot_kernel (vector ALU)"
     elif tile_preferred(dm, dn, dk, dbits):
         kname = "qmv_tile_kernel + qmv_tile_reduce_kernel (MFMA, split K; one call = both launches)"
@@ -351,10 +351,18 @@ def bench_gguf(torch, mlxq, iters=10):
 
 
 def tile_preferred(m, n, k, bits):
-    """The batched-decode kernel choice of qmv_tile.hip (qmv_tile_preferred)."""
-    if n * k >= 1 << 25:
+    """The decode kernel choice of qmv_tile.hip (qmv_tile_preferred), for labels."""
+    large = n * k >= 1 << 25
+    if m <= 4:
+        return large and k < n and bits == 4 and m >= 3
+    if large:
         return m >= 8 if bits == 4 else (m >= 32 or (m >= 16 and k > n))
     return m >= (24 if bits == 4 else 32)
+
+
+def dot_preferred(m, n, k, bits):
+    """qmv_dot_preferred of qmv_tile.hip, for labels."""
+    return m == 1 or (m == 2 and n * k >= 1 << 25 and k < n)
 
 
 def bench_stack(torch, steps=20, batches=(1, 16)):

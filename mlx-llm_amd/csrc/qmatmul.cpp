@@ -40,7 +40,7 @@ extern "C" int mlxq_qmatmul_workspace_size(int64_t M, int64_t N, int64_t K, int 
   if (rc) return rc;
   if (!bytes) return fail(MLXQ_ERR_INVALID, "qmatmul: null output pointer");
   *bytes = qmv_plan_for(M, N, K, group_size, bits).workspace_bytes();
-  if (M > kQmvDotMaxM && M <= kQmvMaxM && qmv_tile_eligible(M, N, K, group_size, bits))
+  if (M <= kQmvMaxM && qmv_tile_eligible(M, N, K, group_size, bits))
     *bytes = qmv_tile_workspace_bytes(M, N);  // split-K partials and counters
   return MLXQ_OK;
 }
@@ -70,8 +70,13 @@ extern "C" int mlxq_qmatmul_algo(const void* x, int64_t M, const uint32_t* wq, c
 
   if (algo == MLXQ_ALGO_QMM) return launch_qmm(xp, M, wq, sp, bp, bias, N, K, group_size, bits, yp, st);
 
-  // decode rows on the vector ALUs (MLXQ_QMV_MFMA=1 forces the MFMA kernel)
-  if (M <= kQmvDotMaxM && qmv_dot_eligible(M, N, K, group_size, bits) && !getenv("MLXQ_QMV_MFMA"))
+  // Kernel per shape, from measurements at the Llama-3-8B projection shapes:
+  // the vector-ALU kernel at M = 1 (and M = 2 on gate/up), the LDS-shared
+  // tile kernel where qmv_tile_preferred says, the block kernel otherwise.
+  // MLXQ_QMV_MFMA=1 never takes the vector-ALU kernel, MLXQ_QMV_DOT_ALL=1
+  // takes it for every eligible M <= 4.
+  if (M <= kQmvDotMaxM && qmv_dot_eligible(M, N, K, group_size, bits) && !getenv("MLXQ_QMV_MFMA") &&
+      (qmv_dot_preferred(M, N, K, bits) || getenv("MLXQ_QMV_DOT_ALL")))
     return launch_qmv_dot(xp, M, wq, sp, bp, bias, N, K, group_size, bits, yp, st);
 
   // batched decode: activations shared through LDS, K split across

@@ -73,6 +73,7 @@ int launch_qmv_mfma(const QmvFused& f, hipStream_t st);
 bool qmv_tile_eligible(int64_t M, int64_t N, int64_t K, int group_size, int bits);
 size_t qmv_tile_workspace_bytes(int64_t M, int64_t N);
 bool qmv_tile_preferred(int64_t M, int64_t N, int64_t K, int bits);
+bool qmv_dot_preferred(int64_t M, int64_t N, int64_t K, int bits);  // M <= 4: vector-ALU kernel
 int launch_qmv_tile(const uint16_t* x, int64_t M, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
                     const uint16_t* bias, int64_t N, int64_t K, int group_size, int bits, uint16_t* y,
                     void* workspace, size_t workspace_bytes, hipStream_t st);

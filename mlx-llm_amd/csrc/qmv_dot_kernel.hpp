@@ -11,8 +11,8 @@
 //    weight row r16 (the gq-th quarter of a 64-byte chunk), so one wave
 //    instruction reads 16 rows x 64 contiguous bytes -- as fast as a copy.
 //  * Each lane contracts its own 32 (Q4) / 16 (Q8) codes per chunk against
-//    the activations.  Q4 codes become bf16 (128 + q) pairs with one and-or
-//    per pair; Q8 codes are converted exactly through f32.
+//    the activations.  Q4 codes become bf16 (128 + q) pairs with two masks
+//    and four v_perm per 8 codes; Q8 codes are converted exactly through f32.
 //  * The activations are staged once per workgroup in LDS -- already in the
 //    pair order of the Q4 unpack -- together with their sum over every lane
 //    segment, so a segment's result is s * dot + (b - 128 s) * sum(x).  A
@@ -330,12 +330,12 @@ __global__ __launch_bounds__(64 * WV) void qmv_dot_kernel(const Params p) {
   for (int j = 0; j < PT; j++) {
     const int i = tid * PT + j;
     uint4 v = xp[j];
-    if constexpr (BITS == 4) {  // (x0,x1),(x2,x3),(x4,x5),(x6,x7) -> (x0,x4),(x1,x5),(x2,x6),(x3,x7)
+    if constexpr (BITS == 4) {  // (x0,x1),(x2,x3),(x4,x5),(x6,x7) -> (x0,x2),(x4,x6),(x1,x3),(x5,x7)
       uint4 q;
-      q.x = __builtin_amdgcn_perm(v.z, v.x, 0x05040100u);
-      q.y = __builtin_amdgcn_perm(v.z, v.x, 0x07060302u);
-      q.z = __builtin_amdgcn_perm(v.w, v.y, 0x05040100u);
-      q.w = __builtin_amdgcn_perm(v.w, v.y, 0x07060302u);
+      q.x = __builtin_amdgcn_perm(v.y, v.x, 0x05040100u);
+      q.y = __builtin_amdgcn_perm(v.w, v.z, 0x05040100u);
+      q.z = __builtin_amdgcn_perm(v.y, v.x, 0x07060302u);
+      q.w = __builtin_amdgcn_perm(v.w, v.z, 0x07060302u);
       v = q;
     }
     const uint32_t ws[4] = {v.x, v.y, v.z, v.w};
@@ -376,11 +376,15 @@ __global__ __launch_bounds__(64 * WV) void qmv_dot_kernel(const Params p) {
         const uint32_t wv[4] = {w[s].x, w[s].y, w[s].z, w[s].w};
         uint32_t q[4];
         if constexpr (BITS == 4) {
+          // codes k0..k7 -> bf16 (128 + k) pairs (k0,k2),(k4,k6),(k1,k3),(k5,k7):
+          // even / odd nibbles masked into bytes, then interleaved with 0x43
+          // bytes by v_perm (0x43nn is the bf16 of 128 + nn)
           const uint32_t c = wv[t];
-          q[0] = (c & 0x000F000Fu) | 0x43004300u;
-          q[1] = ((c >> 4) & 0x000F000Fu) | 0x43004300u;
-          q[2] = ((c >> 8) & 0x000F000Fu) | 0x43004300u;
-          q[3] = ((c >> 12) & 0x000F000Fu) | 0x43004300u;
+          const uint32_t lo = c & 0x0F0F0F0Fu, hi = (c >> 4) & 0x0F0F0F0Fu, e = 0x43434343u;
+          q[0] = __builtin_amdgcn_perm(lo, e, 0x00050004u);
+          q[1] = __builtin_amdgcn_perm(lo, e, 0x00070006u);
+          q[2] = __builtin_amdgcn_perm(hi, e, 0x00050004u);
+          q[3] = __builtin_amdgcn_perm(hi, e, 0x00070006u);
         } else {
 #pragma unroll
           for (int h = 0; h < 2; h++) {

@@ -317,12 +317,22 @@ bool qmv_tile_eligible(int64_t M, int64_t N, int64_t K, int group_size, int bits
 size_t qmv_tile_workspace_bytes(int64_t M, int64_t N) { return static_cast<size_t>(kMaxSplits) * M * N * 4; }
 
 bool qmv_tile_preferred(int64_t M, int64_t N, int64_t K, int bits) {
-  // Measured against the block kernel (qmv.hip) at the Llama-3-8B projection
-  // shapes: the tile kernel wins on the large projections from M = 8 (Q4) /
-  // 16 (Q8; Q8 gate/up only at 32) and on the small ones from M = 24 (Q4)
-  // / 32 (Q8).
-  if (N * K >= (int64_t(1) << 25)) return bits == 4 ? M >= 8 : (M >= 32 || (M >= 16 && K > N));
+  // Measured against the block kernel (qmv.hip) and the vector-ALU kernel
+  // (qmv_dot) at the Llama-3-8B projection shapes: the tile kernel wins on
+  // the large projections from M = 8 (Q4) / 16 (Q8; Q8 gate/up only at 32),
+  // on Q4 gate/up already from M = 3, and on the small projections from
+  // M = 24 (Q4) / 32 (Q8).
+  const bool large = N * K >= (int64_t(1) << 25);
+  if (M <= 4) return large && K < N && bits == 4 && M >= 3;
+  if (large) return bits == 4 ? M >= 8 : (M >= 32 || (M >= 16 && K > N));
   return M >= (bits == 4 ? 24 : 32);
+}
+
+bool qmv_dot_preferred(int64_t M, int64_t N, int64_t K, int bits) {
+  // M = 1 always; M = 2 on gate/up-like shapes (large N*K, K < N); the block
+  // kernel is faster for the other shapes at M = 2..4.
+  (void)bits;
+  return M == 1 || (M == 2 && N * K >= (int64_t(1) << 25) && K < N);
 }
 
 int launch_qmv_tile(const uint16_t* x, int64_t M, const uint32_t* wq, const uint16_t* s, const uint16_t* b,

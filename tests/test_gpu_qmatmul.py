@@ -237,3 +237,15 @@ def test_qmv_dot_short_rows_every_config(torch_gpu, monkeypatch, bits, cfg, k):
     wq, s, b = make_layer(800 + bits + k, 1000, k, 64, bits)
     x = bf16_acts(801 + k, 2, k)
     assert rel_err(run(x, wq, s, b, 64, bits), orc.qmatmul_f64(x, wq, s, b, 64, bits)) <= TIGHT
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("m", [2, 3, 4])
+@pytest.mark.parametrize("kernel", ["MLXQ_QMV_DOT_ALL", "MLXQ_QMV_MFMA"])
+def test_decode_kernels_forced(torch_gpu, monkeypatch, bits, m, kernel):
+    """M = 2..4 on both decode kernels (the dispatcher picks one per shape)."""
+    monkeypatch.setenv(kernel, "1")
+    n, k = 320, 2048
+    wq, s, b = make_layer(30 + bits + m, n, k, 64, bits)
+    x = bf16_acts(31 + m, m, k)
+    assert rel_err(run(x, wq, s, b, 64, bits), orc.qmatmul_f64(x, wq, s, b, 64, bits)) <= TIGHT
