@@ -40,8 +40,8 @@ extern "C" int mlxq_qmatmul_workspace_size(int64_t M, int64_t N, int64_t K, int 
   if (rc) return rc;
   if (!bytes) return fail(MLXQ_ERR_INVALID, "qmatmul: null output pointer");
   *bytes = qmv_plan_for(M, N, K, group_size, bits).workspace_bytes();
-  if (M <= kQmvMaxM && qmv_tile_eligible(M, N, K, group_size, bits))
-    *bytes = qmv_tile_workspace_bytes(M, N);  // split-K partials and counters
+  if (M >= 2 && M <= kQmvMaxM && qmv_tile_eligible(M, N, K, group_size, bits))
+    *bytes = qmv_tile_workspace_bytes(M, N);  // split-K partials (the M = 1 decode kernel needs none)
   return MLXQ_OK;
 }
 

@@ -75,8 +75,12 @@ def test_quantize_and_qmatmul_argument_errors():
     assert L.mlxq_dequantize(p, p, p, mlxq.BF16, 4, 96, 64, 4, p, None) == mlxq.ERR_SHAPE
     assert L.mlxq_qmatmul(p, 1, p, p, p, None, 64, 100, 64, 4, p, None, 0, None) == mlxq.ERR_SHAPE
     assert L.mlxq_qmatmul(p, 1, p, p, p, None, 64, 128, 64, 2, p, None, 0, None) == mlxq.ERR_UNSUPPORTED
-    # the current kernels need no workspace for any shape
+    # workspace: split-K partials of the batched-decode kernel only (group 64,
+    # 2 <= M <= 32): at most 16 slices of M x N f32
     assert mlxq.workspace_size(1, 4096, 4096, 64, 4) == 0
+    assert mlxq.workspace_size(32, 4096, 4096, 64, 4) == 16 * 32 * 4096 * 4
+    assert mlxq.workspace_size(32, 4096, 4096, 32, 4) == 0
+    assert mlxq.workspace_size(2048, 4096, 4096, 64, 4) == 0
     assert L.mlxq_qmatmul_algo(p, 1, p, p, p, None, 64, 128, 64, 4, p, None, 0, 7, None) == mlxq.ERR_INVALID
     # M = 0 is a no-op
     assert L.mlxq_qmatmul(p, 0, p, p, p, None, 64, 128, 64, 4, p, None, 0, None) == mlxq.OK
