@@ -144,11 +144,16 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void qmm_kernel(const uint16_t* __
 #pragma unroll
       for (int wi = 0; wi < NW; wi++) {  // word wi: codes 8 wi .. 8 wi + 7
         const float sc = bf16_bits_to_f32(r.s[NSG == 2 ? wi / 4 : 0]), zz = bf16_bits_to_f32(r.z[NSG == 2 ? wi / 4 : 0]);
-        const uint32_t q = w[wi];
+        // even codes to the bytes of lo, odd codes to the bytes of hi: each
+        // code is then one v_cvt_f32_ubyte
+        uint32_t lo = w[wi] & 0x0F0F0F0Fu, hi = (w[wi] >> 4) & 0x0F0F0F0Fu;
+        // opaque to the optimizer (an empty asm, no instruction): otherwise
+        // it folds the masks back into one bit-field extract per code
+        asm volatile("" : "+v"(lo), "+v"(hi));
 #pragma unroll
         for (int j = 0; j < 4; j++)
-          packed[4 * wi + j] = pack_bf16(sc * static_cast<float>((q >> (8 * j)) & 0xFu) + zz,
-                                         sc * static_cast<float>((q >> (8 * j + 4)) & 0xFu) + zz);
+          packed[4 * wi + j] = pack_bf16(sc * static_cast<float>((lo >> (8 * j)) & 0xFFu) + zz,
+                                         sc * static_cast<float>((hi >> (8 * j)) & 0xFFu) + zz);
       }
     } else {
 #pragma unroll
