@@ -22,6 +22,7 @@ CSRC = PKG / "csrc"
 HOST = PKG / "host"
 OBJ = PKG / "_build"
 LIB = PKG / "libmlxq.so"
+BIN = PKG / "bin"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
@@ -74,7 +75,25 @@ def build(jobs: int = 8, verbose: bool = False) -> Path:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, LIB)
+    build_host_tests(verbose)
     return LIB
+
+
+def build_host_tests(verbose: bool = False) -> Path:
+    """The C++ restatement of the reference's tests (tests/cpp/host_tests.cpp)
+    against the C++ host API, linked to libmlxq.so (found next to it at run
+    time through the rpath)."""
+    BIN.mkdir(exist_ok=True)
+    out = BIN / "host_tests"
+    cmd = [HIPCC, "-O2", "-std=c++17", f"--offload-arch={ARCH}", "-x", "hip", f"-I{ROOT / 'include'}", f"-I{HOST}",
+           str(ROOT / "tests" / "cpp" / "host_tests.cpp"), "-x", "none", str(LIB), "-Wl,-rpath,$ORIGIN/..",
+           "-o", str(out)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"host tests build failed:\n{r.stdout}\n{r.stderr}")
+    return out
 
 
 def main(argv=None) -> int:

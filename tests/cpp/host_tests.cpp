@@ -1,0 +1,328 @@
+// The reference crate's own tests for the quantized-weight path, restated
+// against the C++ host API (mlx-llm_amd/host/mlxq.hpp), which runs them on
+// the GPU kernels.  Each case names the reference test it mirrors
+// (file:line); the inputs and expected values are the reference's.
+//
+//   host_tests           run every case, print one line per case, exit 1 on any failure
+//   host_tests --list    print the case names only (touches no GPU)
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <string>
+#include <vector>
+
+#include "mlxq.hpp"
+
+using mlxq::Array;
+using mlxq::DType;
+using mlxq::Error;
+using mlxq::Projection;
+using mlxq::QuantizedLinear;
+using mlxq::QuantSpec;
+namespace gguf = mlxq::gguf;
+
+namespace {
+
+struct Failure {
+  std::string msg;
+};
+
+#define EXPECT(cond)                                                                              \
+  do {                                                                                            \
+    if (!(cond)) throw Failure{std::string(__FILE__ ":") + std::to_string(__LINE__) + ": " #cond}; \
+  } while (0)
+
+template <typename F>
+void expect_error(Error::Kind kind, F&& f) {
+  try {
+    f();
+  } catch (const Error& e) {
+    if (e.kind() != kind) throw Failure{std::string("wrong error kind: ") + e.what()};
+    return;
+  }
+  throw Failure{"expected an error"};
+}
+
+// IEEE half of a small set of exactly representable values (the tests' d
+// scales): sign, exponent, mantissa assembled from the float's bits.
+uint16_t f16_bits(float f) {
+  uint32_t u;
+  std::memcpy(&u, &f, 4);
+  const uint32_t s = u >> 31, e = (u >> 23) & 0xFF, m = u & 0x7FFFFF;
+  if (f == 0.0f) return static_cast<uint16_t>(s << 15);
+  return static_cast<uint16_t>((s << 15) | ((e - 127 + 15) << 10) | (m >> 13));
+}
+
+uint16_t bf16_bits(float f) {
+  uint32_t u;
+  std::memcpy(&u, &f, 4);
+  return static_cast<uint16_t>(u >> 16);  // exact for the tests' values
+}
+
+void push16(std::vector<uint8_t>& b, uint16_t v) {
+  b.push_back(static_cast<uint8_t>(v & 0xFF));
+  b.push_back(static_cast<uint8_t>(v >> 8));
+}
+
+// ---------------------------------------------------------------- quant.rs
+
+// quant.rs:91-107 quantize_dequantize_roundtrip_q8
+void quantize_dequantize_roundtrip_q8() {
+  const int n = 2 * 64;
+  std::vector<float> data(n);
+  for (int i = 0; i < n; i++) data[i] = static_cast<float>(i) / n - 0.5f;
+  const Array w = Array::from_f32(data, {2, 64});
+  const QuantizedLinear q = QuantizedLinear::quantize(w, 64, 8);
+  const std::vector<float> back = q.dequantize_weight().to_f32();
+  float max_err = 0.f;
+  for (int i = 0; i < n; i++) max_err = std::fmax(max_err, std::fabs(data[i] - back[i]));
+  EXPECT(max_err < 0.01f);
+}
+
+// quant.rs:109-125 quantized_matmul_approximates_linear_q8
+void quantized_matmul_approximates_linear_q8() {
+  const int n = 4 * 64;
+  std::vector<float> wd(n), xd(64);
+  for (int i = 0; i < n; i++) wd[i] = static_cast<float>(i * 7 % 13) / 13.0f - 0.5f;
+  for (int i = 0; i < 64; i++) xd[i] = static_cast<float>(i) / 64.0f - 0.5f;
+  const Array w = Array::from_f32(wd, {4, 64});
+  const Array x = Array::from_f32(xd, {1, 64});
+  std::vector<double> dense(4, 0.0);  // linear(x, w) = x @ w.T
+  for (int o = 0; o < 4; o++)
+    for (int k = 0; k < 64; k++) dense[o] += static_cast<double>(xd[k]) * wd[o * 64 + k];
+  const QuantizedLinear q = QuantizedLinear::quantize(w, 64, 8);
+  const std::vector<float> quant = q.forward(x).to_f32();
+  EXPECT(quant.size() == 4);
+  for (int o = 0; o < 4; o++) EXPECT(std::fabs(dense[o] - quant[o]) < 0.05);
+}
+
+// ---------------------------------------------------------------- projection.rs
+
+// projection.rs:24-31 (QuantSpec::q4 / q8), :50-71 (load / load_with_bias),
+// :76-90 (from_quantized), :93-103 (forward / is_quantized)
+void projection_load_and_dispatch() {
+  EXPECT((QuantSpec::q4() == QuantSpec{64, 4}));
+  EXPECT((QuantSpec::q8() == QuantSpec{64, 8}));
+  std::vector<float> wd(128 * 256), xd(3 * 256);
+  for (size_t i = 0; i < wd.size(); i++) wd[i] = static_cast<float>((i * 37) % 101) / 101.0f - 0.5f;
+  for (size_t i = 0; i < xd.size(); i++) xd[i] = static_cast<float>((i * 13) % 29) / 29.0f - 0.5f;
+  const Array w = Array::from_f32(wd, {128, 256}, DType::BF16);
+  const Array x = Array::from_f32(xd, {3, 256}, DType::BF16);
+
+  const Projection dense = Projection::load(w, std::nullopt);
+  EXPECT(!dense.is_quantized());
+  expect_error(Error::Kind::Unsupported, [&] { dense.forward(x); });
+
+  const Projection p = Projection::load(w, QuantSpec::q4());
+  EXPECT(p.is_quantized());
+  const std::vector<float> y = p.forward(x).to_f32();
+  EXPECT(y.size() == 3u * 128u);
+  const QuantizedLinear& q = p.quantized();
+  const Projection r = Projection::from_quantized(q.weight, q.scales, q.biases, QuantSpec::q4());
+  EXPECT(r.is_quantized());
+  EXPECT(r.forward(x).to_f32() == y);  // the same parts give the same bits
+
+  // against the dense product of the dequantized weight (f64), the qmatmul bar
+  const std::vector<float> wdq = q.dequantize_weight().to_f32();
+  const std::vector<float> xb = x.to_f32();
+  double max_ref = 0.0, max_err = 0.0;
+  for (int m = 0; m < 3; m++)
+    for (int o = 0; o < 128; o++) {
+      double ref = 0.0;
+      for (int k = 0; k < 256; k++) ref += static_cast<double>(xb[m * 256 + k]) * wdq[o * 256 + k];
+      max_ref = std::fmax(max_ref, std::fabs(ref));
+      max_err = std::fmax(max_err, std::fabs(ref - y[m * 128 + o]));
+    }
+  EXPECT(max_err / max_ref <= 1e-2);
+
+  // with a bias: y_bias - y = bias (up to the bf16 output rounding)
+  std::vector<float> bd(128);
+  for (int o = 0; o < 128; o++) bd[o] = static_cast<float>(o % 7) - 3.0f;
+  const Projection pb = Projection::load_with_bias(w, Array::from_f32(bd, {128}, DType::BF16), QuantSpec::q4());
+  const std::vector<float> yb = pb.forward(x).to_f32();
+  for (int m = 0; m < 3; m++)
+    for (int o = 0; o < 128; o++) EXPECT(std::fabs(yb[m * 128 + o] - (y[m * 128 + o] + bd[o])) <= 0.05);
+}
+
+// ---------------------------------------------------------------- dequant.rs
+
+// dequant.rs:725-747 type_geometry_matches_llama_cpp
+void type_geometry_matches_llama_cpp() {
+  using T = gguf::GgmlType;
+  const std::pair<T, std::pair<size_t, size_t>> cases[] = {
+      {T::Q4_0, {32, 18}},    {T::Q4_1, {32, 20}},    {T::Q5_0, {32, 22}},    {T::Q5_1, {32, 24}},
+      {T::Q8_0, {32, 34}},    {T::Q2K, {256, 84}},    {T::Q3K, {256, 110}},   {T::Q4K, {256, 144}},
+      {T::Q5K, {256, 176}},   {T::Q6K, {256, 210}},   {T::Iq4Nl, {32, 18}},   {T::Iq4Xs, {256, 136}},
+      {T::Iq2Xxs, {256, 66}}, {T::Iq2Xs, {256, 74}},  {T::Iq2S, {256, 82}},   {T::Iq3Xxs, {256, 98}},
+      {T::Iq3S, {256, 110}},  {T::Iq1S, {256, 50}},   {T::Iq1M, {256, 56}},
+  };
+  for (const auto& c : cases) EXPECT(gguf::block(c.first) == c.second);
+}
+
+// dequant.rs:749-767 supported_and_unsupported_types
+void supported_and_unsupported_types() {
+  using T = gguf::GgmlType;
+  EXPECT(gguf::from_tag(20) == T::Iq4Nl);
+  EXPECT(gguf::from_tag(23) == T::Iq4Xs);
+  EXPECT(gguf::from_tag(16) == T::Iq2Xxs);
+  EXPECT(gguf::from_tag(17) == T::Iq2Xs);
+  EXPECT(gguf::from_tag(18) == T::Iq3Xxs);
+  EXPECT(gguf::from_tag(19) == T::Iq1S);
+  EXPECT(gguf::from_tag(21) == T::Iq3S);
+  EXPECT(gguf::from_tag(22) == T::Iq2S);
+  EXPECT(gguf::from_tag(29) == T::Iq1M);
+  EXPECT(gguf::tensor_byte_len(16, 256) == 66);
+  expect_error(Error::Kind::Unsupported, [] { gguf::from_tag(9); });   // Q8_1 (intermediate)
+  expect_error(Error::Kind::Unsupported, [] { gguf::from_tag(15); });  // Q8_K (intermediate)
+  expect_error(Error::Kind::Unsupported, [] { gguf::tensor_byte_len(9, 256); });
+}
+
+// dequant.rs:769-780 iq4_nl_codebook_decode
+void iq4_nl_codebook_decode() {
+  std::vector<uint8_t> b;
+  push16(b, f16_bits(2.0f));
+  b.push_back(0x80);
+  b.resize(2 + 16, 0x00);
+  const std::vector<float> out = gguf::dequantize(20, b.data(), b.size(), 32);
+  EXPECT(out[0] == 2.0f * -127.0f);
+  EXPECT(out[16] == 2.0f * 1.0f);
+  EXPECT(out[1] == 2.0f * -127.0f);
+}
+
+// dequant.rs:782-802 f32_f16_bf16_passthrough
+void f32_f16_bf16_passthrough() {
+  const std::vector<float> vals = {1.0f, -2.5f, 3.25f, 0.0f};
+  std::vector<uint8_t> f32b(16), f16b, bf16b;
+  std::memcpy(f32b.data(), vals.data(), 16);
+  EXPECT(gguf::dequantize(0, f32b.data(), f32b.size(), 4) == vals);
+  for (float v : vals) push16(f16b, f16_bits(v));
+  EXPECT(gguf::dequantize(1, f16b.data(), f16b.size(), 4) == vals);
+  for (float v : vals) push16(bf16b, bf16_bits(v));
+  EXPECT(gguf::dequantize(30, bf16b.data(), bf16b.size(), 4) == vals);
+}
+
+// dequant.rs:805-816 q8_0_block_dequant
+void q8_0_block_dequant() {
+  std::vector<uint8_t> b;
+  push16(b, f16_bits(0.5f));
+  for (int q = 0; q < 32; q++) b.push_back(static_cast<uint8_t>(static_cast<int8_t>(q - 16)));
+  const std::vector<float> out = gguf::dequantize(8, b.data(), b.size(), 32);
+  for (int i = 0; i < 32; i++) EXPECT(std::fabs(out[i] - (i - 16) * 0.5f) < 1e-3f);
+}
+
+// dequant.rs:820-836 q4_0_zero_centered
+void q4_0_zero_centered() {
+  std::vector<uint8_t> b;
+  push16(b, f16_bits(1.0f));
+  b.resize(2 + 16, 0x88);
+  for (float v : gguf::dequantize(2, b.data(), b.size(), 32)) EXPECT(v == 0.0f);
+  std::vector<uint8_t> b2;
+  push16(b2, f16_bits(1.0f));
+  b2.push_back(0x8F);
+  b2.resize(2 + 16, 0x88);
+  const std::vector<float> out2 = gguf::dequantize(2, b2.data(), b2.size(), 32);
+  EXPECT(out2[0] == 7.0f);
+  EXPECT(out2[16] == 0.0f);
+}
+
+// dequant.rs:838-850 q2_k_scale_and_unpack
+void q2_k_scale_and_unpack() {
+  std::vector<uint8_t> b(16, 0x01);
+  b.resize(16 + 64, 0xFF);
+  push16(b, f16_bits(1.0f));
+  push16(b, f16_bits(1.0f));
+  for (float v : gguf::dequantize(10, b.data(), b.size(), 256)) EXPECT(v == 3.0f);
+}
+
+// dequant.rs:854-875 q6_k_centered_is_zero
+void q6_k_centered_is_zero() {
+  std::vector<uint8_t> b(210, 0);
+  for (int i = 128; i < 192; i++) b[i] = 0xAA;
+  for (int i = 192; i < 208; i++) b[i] = 5;
+  const uint16_t d = f16_bits(1.0f);
+  b[208] = static_cast<uint8_t>(d & 0xFF);
+  b[209] = static_cast<uint8_t>(d >> 8);
+  for (float v : gguf::dequantize(14, b.data(), b.size(), 256)) EXPECT(v == 0.0f);
+}
+
+// dequant.rs:159-171: element count not a multiple of the block, short data
+void dequantize_errors() {
+  std::vector<uint8_t> b(18 * 2, 0x88);
+  expect_error(Error::Kind::Msg, [&] { gguf::dequantize(2, b.data(), b.size(), 48); });
+  expect_error(Error::Kind::Msg, [&] { gguf::dequantize(2, b.data(), b.size(), 96); });
+  expect_error(Error::Kind::Msg, [&] { gguf::tensor_byte_len(12, 100); });
+  expect_error(Error::Kind::Unsupported, [&] { gguf::dequantize(9, b.data(), b.size(), 32); });
+}
+
+// ---------------------------------------------------------------- convert.rs
+
+// convert.rs:391-423 qk_permute_inverts_llama_cpp_forward, through the fused
+// convert: GGUF rows in llama.cpp's q/k order come back in HF order.  A
+// Q8_0 tensor whose row r holds the value r everywhere (d = 1): after the
+// convert, HF row r must hold its source value in every column.
+void requantize_projection_undoes_qk_permute() {
+  const int n_head = 2, head_dim = 8, rows = n_head * head_dim, cols = 64;
+  const int half = head_dim / 2;
+  // GGUF row g of head h holds HF row k * half + j where g = 2 j + k
+  std::vector<uint8_t> blocks;
+  std::vector<int> hf_of_gguf(rows);
+  for (int h = 0; h < n_head; h++)
+    for (int k = 0; k < 2; k++)
+      for (int j = 0; j < half; j++) hf_of_gguf[h * head_dim + 2 * j + k] = h * head_dim + k * half + j;
+  for (int g = 0; g < rows; g++)
+    for (int blk = 0; blk < cols / 32; blk++) {
+      push16(blocks, f16_bits(1.0f));
+      for (int i = 0; i < 32; i++) blocks.push_back(static_cast<uint8_t>(static_cast<int8_t>(hf_of_gguf[g] - 8)));
+    }
+  const Array data = Array::from_bytes(blocks.data(), blocks.size(), {static_cast<int64_t>(blocks.size())}, DType::U8);
+  const QuantizedLinear q = gguf::requantize_projection(8, data, rows, cols, n_head, QuantSpec::q8());
+  const std::vector<float> w = q.dequantize_weight().to_f32();
+  for (int r = 0; r < rows; r++)
+    for (int c = 0; c < cols; c++) EXPECT(std::fabs(w[r * cols + c] - static_cast<float>(r - 8)) < 1e-2f);
+  // without the un-permute the rows keep the GGUF order
+  const std::vector<float> w0 = gguf::requantize_projection(8, data, rows, cols, 0, QuantSpec::q8()).dequantize_weight().to_f32();
+  bool differs = false;
+  for (int r = 0; r < rows; r++) differs |= std::fabs(w0[r * cols] - static_cast<float>(hf_of_gguf[r] - 8)) < 1e-2f && hf_of_gguf[r] != r;
+  EXPECT(differs);
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  const std::vector<std::pair<const char*, std::function<void()>>> cases = {
+      {"quantize_dequantize_roundtrip_q8", quantize_dequantize_roundtrip_q8},
+      {"quantized_matmul_approximates_linear_q8", quantized_matmul_approximates_linear_q8},
+      {"projection_load_and_dispatch", projection_load_and_dispatch},
+      {"type_geometry_matches_llama_cpp", type_geometry_matches_llama_cpp},
+      {"supported_and_unsupported_types", supported_and_unsupported_types},
+      {"iq4_nl_codebook_decode", iq4_nl_codebook_decode},
+      {"f32_f16_bf16_passthrough", f32_f16_bf16_passthrough},
+      {"q8_0_block_dequant", q8_0_block_dequant},
+      {"q4_0_zero_centered", q4_0_zero_centered},
+      {"q2_k_scale_and_unpack", q2_k_scale_and_unpack},
+      {"q6_k_centered_is_zero", q6_k_centered_is_zero},
+      {"dequantize_errors", dequantize_errors},
+      {"requantize_projection_undoes_qk_permute", requantize_projection_undoes_qk_permute},
+  };
+  if (argc > 1 && std::strcmp(argv[1], "--list") == 0) {
+    for (const auto& c : cases) std::printf("%s\n", c.first);
+    return 0;
+  }
+  int failed = 0;
+  for (const auto& c : cases) {
+    try {
+      c.second();
+      std::printf("ok %s\n", c.first);
+    } catch (const Failure& f) {
+      failed++;
+      std::printf("FAIL %s: %s\n", c.first, f.msg.c_str());
+    } catch (const std::exception& e) {
+      failed++;
+      std::printf("FAIL %s: exception %s\n", c.first, e.what());
+    }
+    std::fflush(stdout);
+  }
+  std::printf("%zu cases, %d failed\n", cases.size(), failed);
+  return failed ? 1 : 0;
+}
