@@ -8,8 +8,8 @@
 // Design (MFMA-bound):
 //  * Workgroup tile BM x BN, K step 64, WM x WN wavefronts each owning
 //    (BM/WM) x (BN/WN) of the output as tiles of v_mfma_f32_32x32x16_bf16
-//    with f32 accumulators.  Default: 8 wavefronts (2 per SIMD), 256 x 256 or
-//    128 x 256 tiles (chosen from the grid size).
+//    with f32 accumulators.  256 x 256 tiles of 8 wavefronts (2 per SIMD) or
+//    128 x 128 tiles of 4 (two workgroups per CU), chosen from the grid size.
 //  * One or two threads own each weight row of the tile per K step: they load
 //    the row's 64 codes and scale/bias, dequantize them once for the whole
 //    workgroup (codes -> f32 -> scale*q + bias -> bf16, round to nearest
@@ -257,18 +257,27 @@ int launch(const uint16_t* x, int M, const uint32_t* wq, const uint16_t* s, cons
 template <int BITS, int GS>
 int launch_cfg(const uint16_t* x, int M, const uint32_t* wq, const uint16_t* s, const uint16_t* b, const uint16_t* bias,
                int N, int K, uint16_t* y, hipStream_t st) {
-  // 8 wavefronts (2 per SIMD).  256 x 256 tiles (4 x 2 waves of 64 x 128)
-  // when the grid then still has >= 1.5 workgroups per CU, else 128 x 256
-  // (2 x 4 waves of 64 x 64) -- the faster of the measured configurations
-  // at the Llama-3-8B prefill shapes.  MLXQ_QMM_CFG overrides (tuning).
+  // 256 x 256 tiles (8 wavefronts, 4 x 2 of 64 x 128; one workgroup per
+  // CU) when they still give about every CU a tile, else 128 x 128 (4
+  // wavefronts of 64 x 64, two workgroups per CU) -- the faster of the
+  // measured configurations at the Llama-3-8B projection shapes for M from
+  // 256 to 4096.  MLXQ_QMM_CFG overrides (tuning).
+  static const int cus = [] {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      return 256;
+    return n;
+  }();
   const int64_t tiles256 = ceil_div(N, 256) * ceil_div(M, 256);
-  int cfg = tiles256 >= 384 ? 4 : 3;
+  int cfg = tiles256 * 8 >= static_cast<int64_t>(cus) * 7 ? 4 : 6;
   if (const char* e = getenv("MLXQ_QMM_CFG")) cfg = atoi(e);
   switch (cfg) {
     case 1: return launch<BITS, GS, 256, 256, 2, 4>(x, M, wq, s, b, bias, N, K, y, st);
     case 2: return launch<BITS, GS, 256, 128, 2, 2>(x, M, wq, s, b, bias, N, K, y, st);
     case 3: return launch<BITS, GS, 128, 256, 2, 4>(x, M, wq, s, b, bias, N, K, y, st);
     case 4: return launch<BITS, GS, 256, 256, 4, 2>(x, M, wq, s, b, bias, N, K, y, st);
+    case 6: return launch<BITS, GS, 128, 128, 2, 2>(x, M, wq, s, b, bias, N, K, y, st);
     default: return launch<BITS, GS, 128, 256, 2, 2>(x, M, wq, s, b, bias, N, K, y, st);
   }
 }
