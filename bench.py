@@ -373,7 +373,7 @@ def tile_preferred(m, n, k, bits):
     if m <= 4:
         return large and k < n and bits == 4 and m >= 3
     if large:
-        return m >= 8 if bits == 4 else (m >= 32 or (m >= 16 and k > n))
+        return m >= (8 if bits == 4 else 16)
     return m >= (24 if bits == 4 else 32)
 
 

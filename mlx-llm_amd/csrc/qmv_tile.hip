@@ -319,12 +319,12 @@ size_t qmv_tile_workspace_bytes(int64_t M, int64_t N) { return static_cast<size_
 bool qmv_tile_preferred(int64_t M, int64_t N, int64_t K, int bits) {
   // Measured against the block kernel (qmv.hip) and the vector-ALU kernel
   // (qmv_dot) at the Llama-3-8B projection shapes: the tile kernel wins on
-  // the large projections from M = 8 (Q4) / 16 (Q8; Q8 gate/up only at 32),
+  // the large projections from M = 8 (Q4) / 16 (Q8),
   // on Q4 gate/up already from M = 3, and on the small projections from
   // M = 24 (Q4) / 32 (Q8).
   const bool large = N * K >= (int64_t(1) << 25);
   if (M <= 4) return large && K < N && bits == 4 && M >= 3;
-  if (large) return bits == 4 ? M >= 8 : (M >= 32 || (M >= 16 && K > N));
+  if (large) return M >= (bits == 4 ? 8 : 16);
   return M >= (bits == 4 ? 24 : 32);
 }
 
