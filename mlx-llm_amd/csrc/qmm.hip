@@ -72,7 +72,7 @@ struct Stage {
   // codes).  Kept as loaded: converting at load time would make the
   // compiler wait for these loads -- and, since loads retire in order, for
   // the whole step's loads -- right after issuing them.
-  uint32_t s[NSG], z[NSG];
+  uint16_t s[NSG], z[NSG];
 };
 
 template <int BITS, int GS, int BM, int BN, int WM, int WN>
@@ -116,14 +116,10 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void qmm_kernel(const uint16_t* __
 #pragma unroll
     for (int i = 0; i < Gm::BU4; i++) r.b[i] = b_src[k0 * BITS / 128 + i];
     const int kc = k0 + b_part * Gm::CPT;  // first code of this thread
-    if constexpr (GS == 32 && Gm::CPT == 64) {
-      r.s[0] = s_src[kc / 32];
-      r.s[1] = s_src[kc / 32 + 1];
-      r.z[0] = z_src[kc / 32];
-      r.z[1] = z_src[kc / 32 + 1];
-    } else {
-      r.s[0] = s_src[kc / GS];
-      r.z[0] = z_src[kc / GS];
+#pragma unroll
+    for (int g = 0; g < NSG; g++) {
+      r.s[g] = s_src[kc / GS + g];
+      r.z[g] = z_src[kc / GS + g];
     }
   };
 
@@ -143,7 +139,8 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void qmm_kernel(const uint16_t* __
     if constexpr (BITS == 4) {
 #pragma unroll
       for (int wi = 0; wi < NW; wi++) {  // word wi: codes 8 wi .. 8 wi + 7
-        const float sc = bf16_bits_to_f32(r.s[NSG == 2 ? wi / 4 : 0]), zz = bf16_bits_to_f32(r.z[NSG == 2 ? wi / 4 : 0]);
+        const int g = NSG == 2 ? wi / 4 : 0;
+        const float sc = bf16_bits_to_f32(r.s[g]), zz = bf16_bits_to_f32(r.z[g]);
         // even codes to the bytes of lo, odd codes to the bytes of hi: each
         // code is then one v_cvt_f32_ubyte
         uint32_t lo = w[wi] & 0x0F0F0F0Fu, hi = (w[wi] >> 4) & 0x0F0F0F0Fu;
@@ -158,7 +155,8 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void qmm_kernel(const uint16_t* __
     } else {
 #pragma unroll
       for (int wi = 0; wi < NW; wi++) {  // word wi: codes 4 wi .. 4 wi + 3
-        const float sc = bf16_bits_to_f32(r.s[NSG == 2 ? wi / 8 : 0]), zz = bf16_bits_to_f32(r.z[NSG == 2 ? wi / 8 : 0]);
+        const int g = NSG == 2 ? wi / 8 : 0;
+        const float sc = bf16_bits_to_f32(r.s[g]), zz = bf16_bits_to_f32(r.z[g]);
         const uint32_t q = w[wi];
         packed[2 * wi] = pack_bf16(sc * static_cast<float>(q & 0xFFu) + zz, sc * static_cast<float>((q >> 8) & 0xFFu) + zz);
         packed[2 * wi + 1] = pack_bf16(sc * static_cast<float>((q >> 16) & 0xFFu) + zz, sc * static_cast<float>(q >> 24) + zz);
@@ -184,7 +182,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void qmm_kernel(const uint16_t* __
 
   St r0, r1;
   load(r0, 0);
-  if (KT > 1) load(r1, 1);
+  load(r1, min(1, KT - 1));
   __builtin_amdgcn_sched_barrier(0);
   store(r0, 0);
   __syncthreads();
@@ -193,7 +191,10 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void qmm_kernel(const uint16_t* __
   // so that the register roles are static.
   auto step = [&](int kt, St& target, St& ready) __attribute__((always_inline)) {
     const int cur = kt & 1;
-    if (kt + 2 < KT) load(target, kt + 2);
+    // unconditional (past the end: the last step again, its lines are on
+    // chip): a conditional load would make the compiler's memory-counter wait
+    // before `store(ready)` drain every load in flight, this step's included
+    load(target, min(kt + 2, KT - 1));
     __builtin_amdgcn_sched_barrier(0);
     const uint16_t* sa = lds + cur * Gm::STAGE + (wm * WROWS + frag_row) * LDR + frag_k;
     const uint16_t* sb = lds + cur * Gm::STAGE + BM * LDR + (wn * WCOLS + frag_row) * LDR + frag_k;
