@@ -55,7 +55,7 @@ size_t qmv_dot_lds_bytes(int64_t M, int64_t K, int bits, int sub) { return lds_b
 
 bool qmv_dot_eligible(int64_t M, int64_t N, int64_t K, int group_size, int bits) {
   if (M < 1 || M > kQmvDotMaxM) return false;
-  if ((K * bits / 8) % 64) return false;  // whole 64-byte chunks per row
+  if ((K * bits / 8) % 64 || K * bits / 8 < 64 * kRound) return false;  // whole 64-byte chunks, >= one round per row
   const int64_t gb = static_cast<int64_t>(group_size) * bits / 8;
   const int64_t ngr = kRound * (gb >= 64 ? 1 : 64 / gb) / (gb > 64 ? gb / 64 : 1);  // groups per round
   if ((K / group_size) % std::min<int64_t>(ngr, 8)) return false;  // aligned vector loads of round params

@@ -266,7 +266,11 @@ __global__ __launch_bounds__(64 * WV) void qmv_dot_kernel(const Params p) {
       for (int s = 0; s < SUB; s++) T.w[u][s] = wrow[s][static_cast<int64_t>(c0 + u) * 4];
   };
   Rnd cur, nxt;
-  if (cfull > cbeg) fetch(cur, cbeg);
+  // Unconditional: a wave with no full round fetches the row's last round
+  // (unused; the host guarantees a row holds a round).  A conditional fetch
+  // would make the compiler's memory-counter waits in the staging below wait
+  // for these codes too, putting a second memory round trip before the math.
+  fetch(cur, min(cbeg, chunks - RC));
   __builtin_amdgcn_sched_barrier(0);  // the whole first round is in flight before the prologue
 
   // 3a) RMSNorm: sums of x^2 per activation row over the workgroup, then
