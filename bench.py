@@ -32,7 +32,7 @@ HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, published
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, published
 METRIC = "Q4/Q8 qmatmul GB/s & TFLOP/s (% roofline), Llama-3-8B proj shapes, 1 GPU"
 # measured HBM traffic per launch (bytes) of a dominant-kernel candidate, keyed (bits, M, K, N)
-TRAFFIC_BYTES = {(8, 32, 4096, 14336): 95_480_765}
+TRAFFIC_BYTES = {(8, 32, 4096, 14336): 95_506_516}
 
 # (name, K, N): y[M, N] = x[M, K] . W[N, K]^T
 PROJ = [("q", 4096, 4096), ("k", 4096, 1024), ("v", 4096, 1024), ("o", 4096, 4096),
