@@ -9,6 +9,9 @@
 //                              <- gguf::dequant (src/gguf/dequant.rs:31-211)
 //   mlxq::gguf::requantize_projection
 //                              <- the per-projection chain of gguf::convert (src/gguf/convert.rs:131-176)
+//   mlxq::snapshot::write_snapshot, save/load_safetensors, load_projection
+//                              <- snapshot::write_snapshot (src/snapshot.rs:86-148) and the
+//                                 pre-quantized loader branch (src/models/llama.rs:81-95)
 //   mlxq::Error                <- error::Error (src/error.rs:10-45): Device for the
 //                                 MLX-op failures, Unsupported, Msg
 //
@@ -140,4 +143,38 @@ QuantizedLinear requantize_projection(uint32_t tag, const Array& data, int64_t r
                                       int permute_heads, QuantSpec spec);
 
 }  // namespace gguf
+
+// Quantized snapshot I/O (src/snapshot.rs): MLX's on-disk layout of a
+// quantized projection -- `{base}.weight` U32 codes, `{base}.scales` and
+// `{base}.biases` -- in a standard safetensors file, plus the `quantization`
+// block of config.json that marks the snapshot pre-quantized.
+namespace snapshot {
+
+using Tensors = std::vector<std::pair<std::string, Array>>;
+
+// snapshot.rs:41-54
+bool is_projection(const std::string& key);
+
+struct Report {  // snapshot.rs:68-77
+  size_t num_tensors = 0;
+  std::optional<QuantSpec> quantized;
+  std::string out_dir;
+};
+
+// snapshot.rs:86-148: projections (by key) cast to bf16 and re-quantized when
+// `quantize` is set, every other tensor written through; config_json must be
+// a JSON object (the quantization block is added to it); tokenizer files are
+// written verbatim when given.
+Report write_snapshot(const std::string& out_dir, const Tensors& tensors, const std::string& config_json,
+                      std::optional<QuantSpec> quantize, const std::optional<std::string>& tokenizer_json = {},
+                      const std::optional<std::string>& tokenizer_config_json = {});
+
+void save_safetensors(const std::string& path, const Tensors& tensors);
+Tensors load_safetensors(const std::string& path);
+
+// The pre-quantized loader branch (src/models/llama.rs:81-95): a projection
+// from the snapshot's `{base}.weight/.scales/.biases`.
+Projection load_projection(const Tensors& tensors, const std::string& base, QuantSpec spec);
+
+}  // namespace snapshot
 }  // namespace mlxq

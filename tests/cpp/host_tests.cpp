@@ -5,12 +5,19 @@
 //
 //   host_tests           run every case, print one line per case, exit 1 on any failure
 //   host_tests --list    print the case names only (touches no GPU)
+//   host_tests --copy-safetensors IN OUT   load IN, save it as OUT
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
+#include <filesystem>
+#include <fstream>
+#include <sstream>
 #include <functional>
 #include <string>
 #include <vector>
+
+#include <unistd.h>
 
 #include "mlxq.hpp"
 
@@ -287,6 +294,142 @@ void requantize_projection_undoes_qk_permute() {
   EXPECT(differs);
 }
 
+
+// ---------------------------------------------------------------- snapshot.rs
+
+namespace snapshot = mlxq::snapshot;
+
+std::string tmp_dir(const char* label) {
+  const char* t = std::getenv("TMPDIR");
+  return std::string(t ? t : "/tmp") + "/mlxq-snapshot-" + label + "-" + std::to_string(getpid());
+}
+
+std::string read_text(const std::string& path) {
+  std::ifstream f(path, std::ios::binary);
+  std::stringstream ss;
+  ss << f.rdbuf();
+  return ss.str();
+}
+
+// snapshot.rs:223-249 tiny_model: a two-layer tiny Llama tensor set (hidden
+// 64, intermediate 128, q 64, kv 32, vocab 4), values uniform in [-0.2, 0.2)
+// from a fixed xorshift stream.
+snapshot::Tensors tiny_model() {
+  const int64_t h = 64, v = 4, inter = 128, qd = 64, kvd = 32;
+  uint64_t state = 0xABCDEFull;
+  auto randn = [&](int64_t rows, int64_t cols) {
+    std::vector<float> d(rows * cols);
+    for (float& x : d) {
+      state ^= state << 13;
+      state ^= state >> 7;
+      state ^= state << 17;
+      x = (static_cast<float>(state >> 40) / 16777216.0f - 0.5f) * 0.4f;
+    }
+    return Array::from_f32(d, {rows, cols});
+  };
+  auto ones = [&](int64_t n) { return Array::from_f32(std::vector<float>(n, 1.0f), {n}); };
+  snapshot::Tensors t;
+  t.emplace_back("model.embed_tokens.weight", randn(v, h));
+  t.emplace_back("model.norm.weight", ones(h));
+  t.emplace_back("lm_head.weight", randn(v, h));
+  for (int i = 0; i < 2; i++) {
+    const std::string p = "model.layers." + std::to_string(i) + ".";
+    t.emplace_back(p + "input_layernorm.weight", ones(h));
+    t.emplace_back(p + "post_attention_layernorm.weight", ones(h));
+    t.emplace_back(p + "self_attn.q_proj.weight", randn(qd, h));
+    t.emplace_back(p + "self_attn.k_proj.weight", randn(kvd, h));
+    t.emplace_back(p + "self_attn.v_proj.weight", randn(kvd, h));
+    t.emplace_back(p + "self_attn.o_proj.weight", randn(h, qd));
+    t.emplace_back(p + "mlp.gate_proj.weight", randn(inter, h));
+    t.emplace_back(p + "mlp.up_proj.weight", randn(inter, h));
+    t.emplace_back(p + "mlp.down_proj.weight", randn(h, inter));
+  }
+  return t;
+}
+
+const char* kTinyConfig =
+    "{\"hidden_size\": 64, \"intermediate_size\": 128, \"num_hidden_layers\": 2, \"num_attention_heads\": 2, "
+    "\"num_key_value_heads\": 1, \"vocab_size\": 4, \"rms_norm_eps\": 1e-5, \"rope_theta\": 10000.0, "
+    "\"tie_word_embeddings\": false, \"eos_token_id\": 99}";
+
+const Array* find(const snapshot::Tensors& t, const std::string& k) {
+  for (const auto& e : t)
+    if (e.first == k) return &e.second;
+  return nullptr;
+}
+
+// snapshot.rs:251-270
+void projection_predicate_selects_only_attn_mlp_projections() {
+  for (const char* k : {"model.layers.0.self_attn.q_proj.weight", "model.layers.7.self_attn.o_proj.weight",
+                        "model.layers.3.mlp.down_proj.weight"})
+    EXPECT(snapshot::is_projection(k));
+  for (const char* k : {"model.embed_tokens.weight", "lm_head.weight", "model.norm.weight",
+                        "model.layers.0.input_layernorm.weight", "model.layers.0.self_attn.q_norm.weight"})
+    EXPECT(!snapshot::is_projection(k));
+}
+
+// snapshot.rs:272-296: a dense write reloads every tensor bit-identical and
+// adds no quantization block.
+void dense_write_round_trips_bit_identical() {
+  const std::string dir = tmp_dir("dense");
+  const snapshot::Tensors tensors = tiny_model();
+  const snapshot::Report r = snapshot::write_snapshot(dir, tensors, kTinyConfig, std::nullopt);
+  EXPECT(!r.quantized.has_value());
+  EXPECT(r.num_tensors == tensors.size());
+  const snapshot::Tensors back = snapshot::load_safetensors(dir + "/model.safetensors");
+  EXPECT(back.size() == tensors.size());
+  for (const auto& [k, a] : tensors) {
+    const Array* b = find(back, k);
+    EXPECT(b != nullptr);
+    EXPECT(b->dtype() == a.dtype() && b->shape() == a.shape());
+    EXPECT(b->to_bytes() == a.to_bytes());
+  }
+  EXPECT(read_text(dir + "/config.json").find("quantization") == std::string::npos);
+  std::filesystem::remove_all(dir);
+}
+
+// snapshot.rs:298-325: a quantized write stores each projection as packed
+// weight / scales / biases, leaves embeddings dense, marks config.json, and
+// the stored parts load as a quantized projection whose forward equals the
+// in-memory quantization of the bf16 weight.
+void quantized_write_loads_through_prequantized_branch() {
+  const std::string dir = tmp_dir("q8");
+  const snapshot::Tensors tensors = tiny_model();
+  const QuantSpec spec = QuantSpec::q8();
+  const snapshot::Report r =
+      snapshot::write_snapshot(dir, tensors, kTinyConfig, spec, std::string("{\"model\": {}}"), std::nullopt);
+  EXPECT(r.quantized.has_value() && *r.quantized == spec);
+  EXPECT(r.num_tensors == 3 + 2 * 2 + 2 * 7 * 3);
+  const snapshot::Tensors w = snapshot::load_safetensors(dir + "/model.safetensors");
+  const std::string base = "model.layers.0.self_attn.q_proj";
+  EXPECT(find(w, base + ".weight") && find(w, base + ".scales") && find(w, base + ".biases"));
+  EXPECT(find(w, base + ".weight")->dtype() == DType::U32);
+  EXPECT(find(w, base + ".scales")->dtype() == DType::BF16);
+  EXPECT(!find(w, "model.embed_tokens.scales"));
+  EXPECT(find(w, "model.embed_tokens.weight")->dtype() == DType::F32);
+  const std::string cfg = read_text(dir + "/config.json");
+  EXPECT(cfg.find("\"quantization\": {\"group_size\": 64, \"bits\": 8}") != std::string::npos);
+  EXPECT(cfg.find("\"eos_token_id\": 99") != std::string::npos);
+  EXPECT(read_text(dir + "/tokenizer.json") == "{\"model\": {}}");
+  EXPECT(!std::filesystem::exists(dir + "/tokenizer_config.json"));
+
+  const Projection p = snapshot::load_projection(w, base, spec);
+  EXPECT(p.is_quantized());
+  const Array* dense = find(tensors, base + ".weight");
+  const Array wb = Array::from_f32(dense->to_f32(), dense->shape(), DType::BF16);
+  const QuantizedLinear q = QuantizedLinear::quantize(wb, 64, 8);
+  EXPECT(p.quantized().weight.to_bytes() == q.weight.to_bytes());
+  EXPECT(p.quantized().scales.to_bytes() == q.scales.to_bytes());
+  EXPECT(p.quantized().biases.to_bytes() == q.biases.to_bytes());
+  std::vector<float> xv(3 * 64);
+  for (size_t i = 0; i < xv.size(); i++) xv[i] = std::sin(0.37f * static_cast<float>(i));
+  const Array x = Array::from_f32(xv, {3, 64}, DType::BF16);
+  EXPECT(p.forward(x).to_bytes() == q.forward(x).to_bytes());
+  expect_error(Error::Kind::Msg, [&] { snapshot::load_projection(w, "model.norm", spec); });
+  expect_error(Error::Kind::Msg, [&] { snapshot::write_snapshot(dir, tensors, "[1, 2]", spec); });
+  std::filesystem::remove_all(dir);
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -304,7 +447,16 @@ int main(int argc, char** argv) {
       {"q6_k_centered_is_zero", q6_k_centered_is_zero},
       {"dequantize_errors", dequantize_errors},
       {"requantize_projection_undoes_qk_permute", requantize_projection_undoes_qk_permute},
+      {"projection_predicate_selects_only_attn_mlp_projections", projection_predicate_selects_only_attn_mlp_projections},
+      {"dense_write_round_trips_bit_identical", dense_write_round_trips_bit_identical},
+      {"quantized_write_loads_through_prequantized_branch", quantized_write_loads_through_prequantized_branch},
   };
+  if (argc == 4 && std::strcmp(argv[1], "--copy-safetensors") == 0) {
+    // interop check driven from Python: read a file the safetensors package
+    // wrote, write it back through this library
+    mlxq::snapshot::save_safetensors(argv[3], mlxq::snapshot::load_safetensors(argv[2]));
+    return 0;
+  }
   if (argc > 1 && std::strcmp(argv[1], "--list") == 0) {
     for (const auto& c : cases) std::printf("%s\n", c.first);
     return 0;

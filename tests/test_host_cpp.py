@@ -13,6 +13,8 @@ CASES = [
     "type_geometry_matches_llama_cpp", "supported_and_unsupported_types", "iq4_nl_codebook_decode",
     "f32_f16_bf16_passthrough", "q8_0_block_dequant", "q4_0_zero_centered", "q2_k_scale_and_unpack",
     "q6_k_centered_is_zero", "dequantize_errors", "requantize_projection_undoes_qk_permute",
+    "projection_predicate_selects_only_attn_mlp_projections", "dense_write_round_trips_bit_identical",
+    "quantized_write_loads_through_prequantized_branch",
 ]
 
 
@@ -30,3 +32,32 @@ def test_host_tests_pass_on_gpu():
     assert r.returncode == 0, r.stdout + r.stderr
     for c in CASES:
         assert f"ok {c}" in r.stdout
+
+
+@pytest.mark.gpu
+def test_safetensors_interop(tmp_path):
+    """A file the safetensors package writes (every dtype the snapshot uses,
+    with metadata) loads through the C++ reader, and what the C++ writer
+    saves loads back in the package bit-identical."""
+    import torch
+    from safetensors.torch import load_file, save_file
+
+    g = torch.Generator().manual_seed(7)
+    src = {
+        "a.weight": torch.randint(0, 2**31 - 1, (6, 8), generator=g, dtype=torch.int64).to(torch.uint32),
+        "a.scales": torch.randn(6, 2, generator=g).to(torch.bfloat16),
+        "a.biases": torch.randn(6, 2, generator=g).to(torch.float16),
+        "norm.weight": torch.randn(5, generator=g),
+        "tok": torch.randint(0, 255, (3, 7), generator=g, dtype=torch.uint8),
+        "scalar_row": torch.randn(1, 1, generator=g),
+    }
+    fin, fout = tmp_path / "in.safetensors", tmp_path / "out.safetensors"
+    save_file(src, str(fin), metadata={"format": "pt", "note": "{\\\"x\\\": [1, 2]}"})
+    r = subprocess.run([str(BIN), "--copy-safetensors", str(fin), str(fout)], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
+    back = load_file(str(fout))
+    assert sorted(back) == sorted(src)
+    for k, v in src.items():
+        assert back[k].dtype == v.dtype and back[k].shape == v.shape, k
+        assert torch.equal(back[k].view(torch.uint8), v.view(torch.uint8)), k
