@@ -91,9 +91,11 @@ int mlxq_dequantize(const uint32_t* wq, const void* scales, const void* biases,
 /* ------------------------------------------------------------------ */
 
 /* Bytes of device workspace mlxq_qmatmul may use for this shape: nonzero
- * for batched decode (5 <= M <= 32, group size 64), where the projections
- * may split K across workgroups and add the f32 partial sums in a second
- * kernel.  The workspace must be 256-byte aligned; its contents need no
+ * for batched decode (2 <= M <= 32, group size 64) and for prefill shapes
+ * with too few 256 x 256 output tiles to fill the GPU (e.g. M = 2048,
+ * 14336 -> 4096: 2 x M x N x 4 bytes), where the kernel splits K across
+ * workgroups and a second kernel adds the f32 partial sums in slice order.
+ * The workspace must be 256-byte aligned; its contents need no
  * initialisation and are scratch after a call.  With no or too small a
  * workspace the call still succeeds on an unsplit kernel. */
 int mlxq_qmatmul_workspace_size(int64_t M, int64_t N, int64_t K,

@@ -42,6 +42,7 @@ extern "C" int mlxq_qmatmul_workspace_size(int64_t M, int64_t N, int64_t K, int 
   *bytes = qmv_plan_for(M, N, K, group_size, bits).workspace_bytes();
   if (M >= 2 && M <= kQmvMaxM && qmv_tile_eligible(M, N, K, group_size, bits))
     *bytes = qmv_tile_workspace_bytes(M, N);  // split-K partials (the M = 1 decode kernel needs none)
+  if (M > kQmvMaxM && K % 64 == 0) *bytes = qmm_workspace_bytes(M, N, K);  // prefill split-K partials
   return MLXQ_OK;
 }
 
@@ -68,7 +69,8 @@ extern "C" int mlxq_qmatmul_algo(const void* x, int64_t M, const uint32_t* wq, c
   uint16_t* yp = static_cast<uint16_t*>(y);
   hipStream_t st = as_stream(stream);
 
-  if (algo == MLXQ_ALGO_QMM) return launch_qmm(xp, M, wq, sp, bp, bias, N, K, group_size, bits, yp, st);
+  if (algo == MLXQ_ALGO_QMM)
+    return launch_qmm(xp, M, wq, sp, bp, bias, N, K, group_size, bits, yp, workspace, workspace_bytes, st);
 
   // Kernel per shape, from measurements at the Llama-3-8B projection shapes:
   // the vector-ALU kernel at M = 1 (and M = 2 on gate/up), the LDS-shared

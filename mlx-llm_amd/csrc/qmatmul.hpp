@@ -78,8 +78,20 @@ int launch_qmv_tile(const uint16_t* x, int64_t M, const uint32_t* wq, const uint
                     const uint16_t* bias, int64_t N, int64_t K, int group_size, int bits, uint16_t* y,
                     void* workspace, size_t workspace_bytes, hipStream_t st);
 
-// qmm: LDS-dequant bf16 MFMA GEMM, any M, K % 64 == 0.  No workspace.
+// y = bf16(sum over the splits of part[split][M][N], in split order, + bias):
+// the second kernel of every split-K launch.
+int launch_split_reduce(const float* part, const uint16_t* bias, uint16_t* y, int64_t M, int64_t N, int splits,
+                        hipStream_t st);
+
+// qmm: LDS-dequant bf16 MFMA GEMM, any M, K % 64 == 0.  Shapes whose
+// 256 x 256 tiles leave most CUs idle split K (qmm_split_k slices, f32
+// partials in the workspace); without a large enough workspace the call
+// runs unsplit.
+constexpr int kQmmMaxSplits = 8;
+int qmm_split_k(int64_t M, int64_t N, int64_t K);
+size_t qmm_workspace_bytes(int64_t M, int64_t N, int64_t K);
 int launch_qmm(const uint16_t* x, int64_t M, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
-               const uint16_t* bias, int64_t N, int64_t K, int group_size, int bits, uint16_t* y, hipStream_t st);
+               const uint16_t* bias, int64_t N, int64_t K, int group_size, int bits, uint16_t* y, void* workspace,
+               size_t workspace_bytes, hipStream_t st);
 
 }  // namespace mlxq

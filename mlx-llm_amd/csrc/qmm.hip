@@ -81,7 +81,8 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void qmm_kernel(const uint16_t* __
                                                                const uint16_t* __restrict__ scales,
                                                                const uint16_t* __restrict__ biases,
                                                                const uint16_t* __restrict__ bias_vec, int N, int K,
-                                                               uint16_t* __restrict__ y) {
+                                                               uint16_t* __restrict__ y, float* __restrict__ part,
+                                                               int k_len) {
   using Gm = QmmGeom<BM, BN, WM, WN, BITS>;
   // scale/bias groups per thread per step: two only for g32 with 64 codes
   constexpr int NSG = (GS == 32 && Gm::CPT == 64) ? 2 : 1;
@@ -92,7 +93,9 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void qmm_kernel(const uint16_t* __
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
   const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
-  const int KT = K / BK;
+  // split K: slice blockIdx.z covers k_len codes from k_base (k_len = K unsplit)
+  const int k_base = blockIdx.z * k_len;
+  const int KT = k_len / BK;
   const int G = K / GS;
   const int64_t row_words = static_cast<int64_t>(K) * BITS / 32;
 
@@ -110,7 +113,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void qmm_kernel(const uint16_t* __
   const uint16_t* z_src = biases + static_cast<int64_t>(b_n) * G;
 
   auto load = [&](St& r, int kt) __attribute__((always_inline)) {
-    const int k0 = kt * BK;
+    const int k0 = k_base + kt * BK;
 #pragma unroll
     for (int i = 0; i < Gm::AU4; i++) r.a[i] = a_src[a_off[i] + k0 / 8];
 #pragma unroll
@@ -223,6 +226,22 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void qmm_kernel(const uint16_t* __
 
   // C layout of a 32x32 MFMA tile: lane holds column lane%32 and rows
   // 8*(v/4) + 4*(lane/32) + v%4.
+  if (part) {  // split K: this slice's f32 partial sums, added by the reduce kernel
+    float* dst = part + static_cast<int64_t>(blockIdx.z) * M * N;
+#pragma unroll
+    for (int j = 0; j < Gm::TN; j++) {
+      const int n = n0 + wn * WCOLS + 32 * j + (lane & 31);
+      if (n >= N) continue;
+#pragma unroll
+      for (int i = 0; i < Gm::TM; i++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+          const int m = m0 + wm * WROWS + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+          if (m < M) dst[static_cast<int64_t>(m) * N + n] = acc[i][j][v];
+        }
+    }
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < Gm::TN; j++) {
     const int n = n0 + wn * WCOLS + 32 * j + (lane & 31);
@@ -240,7 +259,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void qmm_kernel(const uint16_t* __
 
 template <int BITS, int GS, int BM, int BN, int WM, int WN>
 int launch(const uint16_t* x, int M, const uint32_t* wq, const uint16_t* s, const uint16_t* b, const uint16_t* bias,
-           int N, int K, uint16_t* y, hipStream_t st) {
+           int N, int K, uint16_t* y, float* part, int splits, hipStream_t st) {
   using Gm = QmmGeom<BM, BN, WM, WN, BITS>;
   auto kern = qmm_kernel<BITS, GS, BM, BN, WM, WN>;
   static bool attr_set = false;  // once per process; the attribute is per function
@@ -250,19 +269,15 @@ int launch(const uint16_t* x, int M, const uint32_t* wq, const uint16_t* s, cons
     if (e != hipSuccess) return fail(MLXQ_ERR_DEVICE, std::string("qmm: set LDS size: ") + hipGetErrorString(e));
     attr_set = true;
   }
-  dim3 grid(ceil_div(N, BN), ceil_div(M, BM));
-  hipLaunchKernelGGL(kern, grid, dim3(Gm::THREADS), Gm::LDS_BYTES, st, x, M, wq, s, b, bias, N, K, y);
-  return check_launch("qmm");
+  dim3 grid(ceil_div(N, BN), ceil_div(M, BM), splits);
+  hipLaunchKernelGGL(kern, grid, dim3(Gm::THREADS), Gm::LDS_BYTES, st, x, M, wq, s, b, bias, N, K, y,
+                     splits > 1 ? part : nullptr, K / splits);
+  if (int rc = check_launch("qmm")) return rc;
+  if (splits == 1) return MLXQ_OK;
+  return launch_split_reduce(part, bias, y, M, N, splits, st);
 }
 
-template <int BITS, int GS>
-int launch_cfg(const uint16_t* x, int M, const uint32_t* wq, const uint16_t* s, const uint16_t* b, const uint16_t* bias,
-               int N, int K, uint16_t* y, hipStream_t st) {
-  // 256 x 256 tiles (8 wavefronts, 4 x 2 of 64 x 128; one workgroup per
-  // CU) when they still give about every CU a tile, else 128 x 128 (4
-  // wavefronts of 64 x 64, two workgroups per CU) -- the faster of the
-  // measured configurations at the Llama-3-8B projection shapes for M from
-  // 256 to 4096.  MLXQ_QMM_CFG overrides (tuning).
+int cu_count() {
   static const int cus = [] {
     int dev = 0, n = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
@@ -270,32 +285,74 @@ int launch_cfg(const uint16_t* x, int M, const uint32_t* wq, const uint16_t* s, 
       return 256;
     return n;
   }();
+  return cus;
+}
+
+template <int BITS, int GS>
+int launch_cfg(const uint16_t* x, int M, const uint32_t* wq, const uint16_t* s, const uint16_t* b, const uint16_t* bias,
+               int N, int K, uint16_t* y, float* part, int splits, hipStream_t st) {
+  // 256 x 256 tiles (8 wavefronts, 4 x 2 of 64 x 128; one workgroup per
+  // CU) when they still give about every CU a tile, else 128 x 128 (4
+  // wavefronts of 64 x 64, two workgroups per CU) -- the faster of the
+  // measured configurations at the Llama-3-8B projection shapes for M from
+  // 256 to 4096.  MLXQ_QMM_CFG overrides (tuning).
   const int64_t tiles256 = ceil_div(N, 256) * ceil_div(M, 256);
-  int cfg = tiles256 * 8 >= static_cast<int64_t>(cus) * 7 ? 4 : 6;
+  int cfg = splits > 1 || tiles256 * 8 >= static_cast<int64_t>(cu_count()) * 7 ? 4 : 6;
   if (const char* e = getenv("MLXQ_QMM_CFG")) cfg = atoi(e);
   switch (cfg) {
-    case 1: return launch<BITS, GS, 256, 256, 2, 4>(x, M, wq, s, b, bias, N, K, y, st);
-    case 2: return launch<BITS, GS, 256, 128, 2, 2>(x, M, wq, s, b, bias, N, K, y, st);
-    case 3: return launch<BITS, GS, 128, 256, 2, 4>(x, M, wq, s, b, bias, N, K, y, st);
-    case 4: return launch<BITS, GS, 256, 256, 4, 2>(x, M, wq, s, b, bias, N, K, y, st);
-    case 6: return launch<BITS, GS, 128, 128, 2, 2>(x, M, wq, s, b, bias, N, K, y, st);
-    default: return launch<BITS, GS, 128, 256, 2, 2>(x, M, wq, s, b, bias, N, K, y, st);
+    case 1: return launch<BITS, GS, 256, 256, 2, 4>(x, M, wq, s, b, bias, N, K, y, part, splits, st);
+    case 2: return launch<BITS, GS, 256, 128, 2, 2>(x, M, wq, s, b, bias, N, K, y, part, splits, st);
+    case 3: return launch<BITS, GS, 128, 256, 2, 4>(x, M, wq, s, b, bias, N, K, y, part, splits, st);
+    case 4: return launch<BITS, GS, 256, 256, 4, 2>(x, M, wq, s, b, bias, N, K, y, part, splits, st);
+    case 6: return launch<BITS, GS, 128, 128, 2, 2>(x, M, wq, s, b, bias, N, K, y, part, splits, st);
+    default: return launch<BITS, GS, 128, 256, 2, 2>(x, M, wq, s, b, bias, N, K, y, part, splits, st);
   }
 }
 
 }  // namespace
 
-int launch_qmm(const uint16_t* x, int64_t M, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
-               const uint16_t* bias, int64_t N, int64_t K, int group_size, int bits, uint16_t* y, hipStream_t st) {
-  const int m = static_cast<int>(M), n = static_cast<int>(N), k = static_cast<int>(K);
-  if (bits == 4) {
-    if (group_size == 32) return launch_cfg<4, 32>(x, m, wq, s, b, bias, n, k, y, st);
-    if (group_size == 64) return launch_cfg<4, 64>(x, m, wq, s, b, bias, n, k, y, st);
-    return launch_cfg<4, 128>(x, m, wq, s, b, bias, n, k, y, st);
+int qmm_split_k(int64_t M, int64_t N, int64_t K) {
+  // 256 x 256 tiles times splits should fill about one round of workgroups
+  // (one per CU) when the unsplit grid leaves most CUs idle; each slice
+  // keeps at least 16 K steps and whole groups (K / splits % 128 == 0).
+  // MLXQ_QMM_SPLIT overrides (tuning).
+  if (const char* e = getenv("MLXQ_QMM_SPLIT")) {
+    const int sp = atoi(e);
+    return sp >= 1 && sp <= kQmmMaxSplits && K % (128 * sp) == 0 ? sp : 1;
   }
-  if (group_size == 32) return launch_cfg<8, 32>(x, m, wq, s, b, bias, n, k, y, st);
-  if (group_size == 64) return launch_cfg<8, 64>(x, m, wq, s, b, bias, n, k, y, st);
-  return launch_cfg<8, 128>(x, m, wq, s, b, bias, n, k, y, st);
+  const int64_t cus = cu_count();
+  const int64_t tiles = ceil_div(N, 256) * ceil_div(M, 256);
+  if (tiles * 8 >= cus * 7) return 1;
+  for (int sp = 2; sp <= kQmmMaxSplits; sp++) {
+    if (tiles * sp > cus) break;
+    if (tiles * sp * 8 >= cus * 7 && K % (128 * sp) == 0 && K / sp >= 16 * 64) return sp;
+  }
+  return 1;
+}
+
+size_t qmm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  const int sp = qmm_split_k(M, N, K);
+  return sp > 1 ? static_cast<size_t>(sp) * M * N * sizeof(float) : 0;
+}
+
+int launch_qmm(const uint16_t* x, int64_t M, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
+               const uint16_t* bias, int64_t N, int64_t K, int group_size, int bits, uint16_t* y, void* workspace,
+               size_t workspace_bytes, hipStream_t st) {
+  const int m = static_cast<int>(M), n = static_cast<int>(N), k = static_cast<int>(K);
+  // split K only when the caller's workspace holds the partials
+  int splits = qmm_split_k(M, N, K);
+  if (splits > 1 && (!workspace || workspace_bytes < static_cast<size_t>(splits) * M * N * sizeof(float) ||
+                     (reinterpret_cast<uintptr_t>(workspace) & 255u)))
+    splits = 1;
+  float* part = static_cast<float*>(workspace);
+  if (bits == 4) {
+    if (group_size == 32) return launch_cfg<4, 32>(x, m, wq, s, b, bias, n, k, y, part, splits, st);
+    if (group_size == 64) return launch_cfg<4, 64>(x, m, wq, s, b, bias, n, k, y, part, splits, st);
+    return launch_cfg<4, 128>(x, m, wq, s, b, bias, n, k, y, part, splits, st);
+  }
+  if (group_size == 32) return launch_cfg<8, 32>(x, m, wq, s, b, bias, n, k, y, part, splits, st);
+  if (group_size == 64) return launch_cfg<8, 64>(x, m, wq, s, b, bias, n, k, y, part, splits, st);
+  return launch_cfg<8, 128>(x, m, wq, s, b, bias, n, k, y, part, splits, st);
 }
 
 }  // namespace mlxq

@@ -75,12 +75,18 @@ def test_quantize_and_qmatmul_argument_errors():
     assert L.mlxq_dequantize(p, p, p, mlxq.BF16, 4, 96, 64, 4, p, None) == mlxq.ERR_SHAPE
     assert L.mlxq_qmatmul(p, 1, p, p, p, None, 64, 100, 64, 4, p, None, 0, None) == mlxq.ERR_SHAPE
     assert L.mlxq_qmatmul(p, 1, p, p, p, None, 64, 128, 64, 2, p, None, 0, None) == mlxq.ERR_UNSUPPORTED
-    # workspace: split-K partials of the batched-decode kernel only (group 64,
-    # 2 <= M <= 32): at most 16 slices of M x N f32
+    # workspace: split-K partials of the batched-decode kernel (group 64,
+    # 2 <= M <= 32: at most 16 slices of M x N f32) and of prefill shapes
+    # whose 256 x 256 tiles fill under 7/8 of the 256 CUs (slices chosen to
+    # fill about one round)
     assert mlxq.workspace_size(1, 4096, 4096, 64, 4) == 0
     assert mlxq.workspace_size(32, 4096, 4096, 64, 4) == 16 * 32 * 4096 * 4
     assert mlxq.workspace_size(32, 4096, 4096, 32, 4) == 0
-    assert mlxq.workspace_size(2048, 4096, 4096, 64, 4) == 0
+    assert mlxq.workspace_size(2048, 4096, 4096, 64, 4) == 2 * 2048 * 4096 * 4    # 128 tiles -> 2 slices
+    assert mlxq.workspace_size(2048, 4096, 14336, 64, 4) == 2 * 2048 * 4096 * 4
+    assert mlxq.workspace_size(1024, 4096, 14336, 64, 8) == 4 * 1024 * 4096 * 4   # 64 tiles -> 4 slices
+    assert mlxq.workspace_size(2048, 14336, 4096, 64, 4) == 0                     # 448 tiles: unsplit
+    assert mlxq.workspace_size(2048, 1024, 4096, 64, 4) == 0                      # 32 tiles: slices too short
     assert L.mlxq_qmatmul_algo(p, 1, p, p, p, None, 64, 128, 64, 4, p, None, 0, 7, None) == mlxq.ERR_INVALID
     # M = 0 is a no-op
     assert L.mlxq_qmatmul(p, 0, p, p, p, None, 64, 128, 64, 4, p, None, 0, None) == mlxq.OK

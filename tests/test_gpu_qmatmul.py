@@ -94,6 +94,24 @@ def test_qmm_small(torch_gpu, bits, gs, m):
     assert rel_err(y, ref) <= TIGHT
 
 
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+@pytest.mark.parametrize("splits", [2, 8])
+@pytest.mark.parametrize("n", [200, 202])
+def test_qmm_split_k(torch_gpu, monkeypatch, bits, gs, splits, n):
+    """qmm with K split across workgroups (f32 partials in the workspace,
+    summed in slice order by the reduce kernel): the 4-wide reduce (N % 4 ==
+    0) and the scalar one, a bias vector, M not a multiple of the tile."""
+    monkeypatch.setenv("MLXQ_QMM_SPLIT", str(splits))
+    m, k = 300, 1024
+    assert mlxq.workspace_size(m, n, k, gs, bits) == splits * m * n * 4
+    wq, s, b = make_layer(90 + bits + gs + n, n, k, gs, bits)
+    x = bf16_acts(91 + splits, m, k)
+    bias = orc.f32_to_bf16(orc.normal(92, n, 0, 1))
+    ref = orc.qmatmul_f64(x, wq, s, b, gs, bits) + orc.bf16_to_f32(bias)[None, :]
+    assert rel_err(run(x, wq, s, b, gs, bits, mlxq.ALGO_QMM, bias=bias), ref) <= TIGHT
+
+
 def test_bias_vector(torch_gpu):
     n, k = 192, 256
     wq, s, b = make_layer(70, n, k)
