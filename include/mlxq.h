@@ -200,8 +200,9 @@ int mlxq_gguf_tensor_byte_len(uint32_t tag, int64_t n, int64_t* bytes);
  * n/elems blocks (data_len >= the blocks' bytes); out: n values in out_dtype
  * (MLXQ_F32: bit-exact with the reference; MLXQ_BF16: that f32 value rounded
  * to nearest-even, as convert.rs:156 does).  Device tags: F32, F16, BF16,
- * Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS.
- * IQ1/IQ2/IQ3 grid types return MLXQ_ERR_UNSUPPORTED. */
+ * Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS,
+ * and the grid types IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_S, IQ1_M
+ * (dequant.rs:505-719): every type the reference decodes. */
 int mlxq_gguf_dequantize(uint32_t tag, const void* data, int64_t data_len,
                          int64_t n, int out_dtype, void* out, void* stream);
 

@@ -1,7 +1,7 @@
 // GGUF block dequantization for gfx950.
 //
 // Reference: src/gguf/dequant.rs:156-211 (dispatcher) and the per-type block
-// decoders it calls (:228-497).  The reference walks blocks one at a time on
+// decoders it calls (:228-719).  The reference walks blocks one at a time on
 // one host thread; here a workgroup stages a chunk of whole blocks into LDS
 // with wide coalesced loads, then every thread decodes VEC consecutive output
 // elements straight from LDS and writes them with one 16-byte store.
@@ -137,6 +137,13 @@ int dispatch(uint32_t tag, const uint8_t* d, int64_t nblocks, int64_t n, void* o
     case 14: launch_blocks<14, BF16OUT>(d, nblocks, out, st); break;
     case 20: launch_blocks<20, BF16OUT>(d, nblocks, out, st); break;
     case 23: launch_blocks<23, BF16OUT>(d, nblocks, out, st); break;
+    case 16: launch_blocks<16, BF16OUT>(d, nblocks, out, st); break;
+    case 17: launch_blocks<17, BF16OUT>(d, nblocks, out, st); break;
+    case 22: launch_blocks<22, BF16OUT>(d, nblocks, out, st); break;
+    case 18: launch_blocks<18, BF16OUT>(d, nblocks, out, st); break;
+    case 21: launch_blocks<21, BF16OUT>(d, nblocks, out, st); break;
+    case 19: launch_blocks<19, BF16OUT>(d, nblocks, out, st); break;
+    case 29: launch_blocks<29, BF16OUT>(d, nblocks, out, st); break;
     default:
       return fail(MLXQ_ERR_UNSUPPORTED,
                   "unsupported: GGUF type tag " + std::to_string(tag) + " has no device dequantizer");

@@ -1,7 +1,7 @@
 // GGUF block decoding shared by the dequantizer (gguf.hip) and the fused
 // dequantize + requantize converter (gguf_requant.hip).
 //
-// Reference: the per-type block decoders of src/gguf/dequant.rs (:228-497),
+// Reference: the per-type block decoders of src/gguf/dequant.rs (:228-719),
 // solved for one element: decode<TAG>(block, j) is element j of a block, with
 // exactly the IEEE f32 operations, operand order and roundings the reference
 // uses for it.  Every file that includes this header is compiled with
@@ -12,6 +12,7 @@
 #include <hip/hip_runtime.h>
 
 #include "common.hpp"
+#include "iq_tables.h"
 
 namespace mlxq {
 namespace {  // internal linkage: each including file has its own copy
@@ -186,6 +187,117 @@ __device__ __forceinline__ float decode<23>(const uint8_t* b, int j) {
   return dl * static_cast<float>(kIq4nl[q]);
 }
 
+// ---- IQ grid types (dequant.rs:505-719).  Codebooks: the format's fixed
+// tables (iq_tables.h).  ksigns_iq2xs is computed: entry i is i with bit 7 =
+// parity of i.
+__constant__ uint64_t kIq2xxs[256] = {MLXQ_IQ2XXS_GRID};
+__constant__ uint64_t kIq2xs[512] = {MLXQ_IQ2XS_GRID};
+__constant__ uint64_t kIq2s[1024] = {MLXQ_IQ2S_GRID};
+__constant__ uint32_t kIq3xxs[256] = {MLXQ_IQ3XXS_GRID};
+__constant__ uint32_t kIq3s[512] = {MLXQ_IQ3S_GRID};
+__constant__ uint64_t kIq1s[2048] = {MLXQ_IQ1S_GRID};
+constexpr float kIq1sDelta = 0.125f;  // dequant.rs:26-27
+
+__device__ __forceinline__ uint32_t ksigns(uint32_t i) {
+  i &= 127u;
+  return i | ((__popc(i) & 1u) << 7);
+}
+// output lane jj's sign: -1 where bit jj of the sign byte is set (dequant.rs:508-516)
+__device__ __forceinline__ float iq_sign(uint32_t s, int jj) { return (s >> jj) & 1u ? -1.0f : 1.0f; }
+__device__ __forceinline__ uint32_t grid_byte(uint64_t g, int jj) {
+  return static_cast<uint32_t>(g >> (8 * jj)) & 0xFFu;
+}
+
+// IQ2_XXS (dequant.rs:521-539): 32-block ib32, 8-lane group l, lane jj
+template <>
+__device__ __forceinline__ float decode<16>(const uint8_t* b, int j) {
+  const int ib32 = j >> 5, l = (j >> 3) & 3, jj = j & 7;
+  const float d = rd_f16(b, 0);
+  const uint8_t* q = b + 2 + 8 * ib32;
+  const uint32_t aux1 = rd_u32(q + 4);
+  const float db = d * (0.5f + static_cast<float>(aux1 >> 28)) * 0.25f;
+  const uint64_t g = kIq2xxs[q[l]];
+  return db * static_cast<float>(grid_byte(g, jj)) * iq_sign(ksigns(aux1 >> (7 * l)), jj);
+}
+// IQ2_XS (dequant.rs:543-564)
+template <>
+__device__ __forceinline__ float decode<17>(const uint8_t* b, int j) {
+  const int ib32 = j >> 5, l = (j >> 3) & 3, jj = j & 7;
+  const float d = rd_f16(b, 0);
+  const uint32_t sc = b[66 + ib32];
+  const float db = d * (0.5f + static_cast<float>(l < 2 ? (sc & 0xFu) : (sc >> 4))) * 0.25f;
+  const int qo = 2 + 2 * (4 * ib32 + l);
+  const uint32_t q = static_cast<uint32_t>(b[qo]) | (static_cast<uint32_t>(b[qo + 1]) << 8);
+  const uint64_t g = kIq2xs[q & 511u];
+  return db * static_cast<float>(grid_byte(g, jj)) * iq_sign(ksigns(q >> 9), jj);
+}
+// IQ2_S (dequant.rs:568-591)
+template <>
+__device__ __forceinline__ float decode<22>(const uint8_t* b, int j) {
+  const int ib32 = j >> 5, l = (j >> 3) & 3, jj = j & 7;
+  const float d = rd_f16(b, 0);
+  const uint32_t sc = b[74 + ib32];
+  const float db = d * (0.5f + static_cast<float>(l < 2 ? (sc & 0xFu) : (sc >> 4))) * 0.25f;
+  const uint32_t idx = b[2 + 4 * ib32 + l] | ((static_cast<uint32_t>(b[66 + ib32]) << (8 - 2 * l)) & 0x300u);
+  const uint64_t g = kIq2s[idx];
+  return db * static_cast<float>(grid_byte(g, jj)) * iq_sign(b[34 + 4 * ib32 + l], jj);
+}
+// IQ3_XXS (dequant.rs:596-615): lanes 0-3 from grid point 2l, 4-7 from 2l+1
+template <>
+__device__ __forceinline__ float decode<18>(const uint8_t* b, int j) {
+  const int ib32 = j >> 5, l = (j >> 3) & 3, jj = j & 7;
+  const float d = rd_f16(b, 0);
+  const uint32_t aux = rd_u32(b + 66 + 4 * ib32);
+  const float db = d * (0.5f + static_cast<float>(aux >> 28)) * 0.5f;
+  const uint32_t g = kIq3xxs[b[2 + 8 * ib32 + 2 * l + (jj >> 2)]];
+  return db * static_cast<float>(grid_byte(g, jj & 3)) * iq_sign(ksigns(aux >> (7 * l)), jj);
+}
+// IQ3_S (dequant.rs:619-651): 64-element pair k, its half, 8-lane group l
+template <>
+__device__ __forceinline__ float decode<21>(const uint8_t* b, int j) {
+  const int k = j >> 6, half = (j >> 5) & 1, l = (j >> 3) & 3, jj = j & 7;
+  const float d = rd_f16(b, 0);
+  const uint32_t sc = b[106 + k];
+  const float db = d * static_cast<float>(1 + 2 * static_cast<int>(half ? (sc >> 4) : (sc & 0xFu)));
+  const uint32_t qhb = b[66 + 2 * k + half];
+  const uint8_t* q = b + 2 + 16 * k + 8 * half;
+  const uint32_t idx = jj < 4 ? (q[2 * l] | ((qhb << (8 - 2 * l)) & 256u))
+                              : (q[2 * l + 1] | ((qhb << (7 - 2 * l)) & 256u));
+  const uint32_t g = kIq3s[idx];
+  return db * static_cast<float>(grid_byte(g, jj & 3)) * iq_sign(b[74 + 8 * k + 4 * half + l], jj);
+}
+// IQ1_S (dequant.rs:655-673): signed grid plus a +-delta offset
+template <>
+__device__ __forceinline__ float decode<19>(const uint8_t* b, int j) {
+  const int ib = j >> 5, l = (j >> 3) & 3, jj = j & 7;
+  const float d = rd_f16(b, 0);
+  const uint32_t h = static_cast<uint32_t>(b[34 + 2 * ib]) | (static_cast<uint32_t>(b[35 + 2 * ib]) << 8);
+  const float dl = d * static_cast<float>(2 * static_cast<int>((h >> 12) & 7u) + 1);
+  const float delta = (h & 0x8000u) ? -kIq1sDelta : kIq1sDelta;
+  const uint32_t idx = b[2 + 4 * ib + l] | (((h >> (3 * l)) & 7u) << 8);
+  const int v = static_cast<int8_t>(grid_byte(kIq1s[idx], jj));
+  return dl * (static_cast<float>(v) + delta);
+}
+// IQ1_M (dequant.rs:678-719): f16 scale from the top nibbles of the four
+// scale words, two 3-bit sub-scales per 32-block
+template <>
+__device__ __forceinline__ float decode<29>(const uint8_t* b, int j) {
+  const int ib = j >> 5, l = (j >> 3) & 3, jj = j & 7;
+  uint32_t sc[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) sc[i] = static_cast<uint32_t>(b[48 + 2 * i]) | (static_cast<uint32_t>(b[49 + 2 * i]) << 8);
+  const uint32_t bits = (sc[0] >> 12) | ((sc[1] >> 8) & 0x00F0u) | ((sc[2] >> 4) & 0x0F00u) | (sc[3] & 0xF000u);
+  const float d = f16_bits_to_f32(bits);
+  const uint32_t w = sc[ib >> 1];
+  const int shift = 6 * (ib & 1) + (l < 2 ? 0 : 3);
+  const float dl = d * static_cast<float>(2 * static_cast<int>((w >> shift) & 7u) + 1);
+  const uint32_t qh = b[32 + 2 * ib + (l >> 1)];
+  const uint32_t idx = b[4 * ib + l] | ((l & 1) ? ((qh << 4) & 0x700u) : ((qh << 8) & 0x700u));
+  const float delta = (qh & ((l & 1) ? 0x80u : 0x08u)) ? -kIq1sDelta : kIq1sDelta;
+  const int v = static_cast<int8_t>(grid_byte(kIq1s[idx], jj));
+  return dl * (static_cast<float>(v) + delta);
+}
+
 template <int TAG> struct Geo;
 template <> struct Geo<2> { static constexpr int E = 32, B = 18; };
 template <> struct Geo<3> { static constexpr int E = 32, B = 20; };
@@ -199,6 +311,13 @@ template <> struct Geo<13> { static constexpr int E = 256, B = 176; };
 template <> struct Geo<14> { static constexpr int E = 256, B = 210; };
 template <> struct Geo<20> { static constexpr int E = 32, B = 18; };
 template <> struct Geo<23> { static constexpr int E = 256, B = 136; };
+template <> struct Geo<16> { static constexpr int E = 256, B = 66; };
+template <> struct Geo<17> { static constexpr int E = 256, B = 74; };
+template <> struct Geo<22> { static constexpr int E = 256, B = 82; };
+template <> struct Geo<18> { static constexpr int E = 256, B = 98; };
+template <> struct Geo<21> { static constexpr int E = 256, B = 110; };
+template <> struct Geo<19> { static constexpr int E = 256, B = 50; };
+template <> struct Geo<29> { static constexpr int E = 256, B = 56; };
 
 }  // namespace
 }  // namespace mlxq

@@ -166,7 +166,8 @@ extern "C" int mlxq_gguf_requantize(uint32_t tag, const void* data, int64_t data
   if (int rc = mlxq_gguf_block(tag, &elems, &bbytes)) return rc;
   const bool device_tag = tag == 0 || tag == 1 || tag == 30 || tag == 2 || tag == 3 || tag == 6 || tag == 7 ||
                           tag == 8 || tag == 10 || tag == 11 || tag == 12 || tag == 13 || tag == 14 || tag == 20 ||
-                          tag == 23;
+                          tag == 23 || tag == 16 || tag == 17 || tag == 22 || tag == 18 || tag == 21 || tag == 19 ||
+                          tag == 29;
   if (!device_tag) return fail(MLXQ_ERR_UNSUPPORTED, "gguf_requantize: GGUF type " + std::to_string(tag) +
                                                          " has no device decoder");
   if (cols % elems) return fail(MLXQ_ERR_SHAPE, "gguf_requantize: rows must hold whole blocks");
@@ -206,6 +207,13 @@ extern "C" int mlxq_gguf_requantize(uint32_t tag, const void* data, int64_t data
     case 13: return launch_tag<13>(bits, group_size, R, K, RB, perm_hd, d, wq, s, b, st);
     case 14: return launch_tag<14>(bits, group_size, R, K, RB, perm_hd, d, wq, s, b, st);
     case 20: return launch_tag<20>(bits, group_size, R, K, RB, perm_hd, d, wq, s, b, st);
+    case 16: return launch_tag<16>(bits, group_size, R, K, RB, perm_hd, d, wq, s, b, st);
+    case 17: return launch_tag<17>(bits, group_size, R, K, RB, perm_hd, d, wq, s, b, st);
+    case 22: return launch_tag<22>(bits, group_size, R, K, RB, perm_hd, d, wq, s, b, st);
+    case 18: return launch_tag<18>(bits, group_size, R, K, RB, perm_hd, d, wq, s, b, st);
+    case 21: return launch_tag<21>(bits, group_size, R, K, RB, perm_hd, d, wq, s, b, st);
+    case 19: return launch_tag<19>(bits, group_size, R, K, RB, perm_hd, d, wq, s, b, st);
+    case 29: return launch_tag<29>(bits, group_size, R, K, RB, perm_hd, d, wq, s, b, st);
     default: return launch_tag<23>(bits, group_size, R, K, RB, perm_hd, d, wq, s, b, st);
   }
 }

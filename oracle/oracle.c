@@ -11,6 +11,8 @@
  */
 #include "oracle.h"
 
+#include "../mlx-llm_amd/csrc/iq_tables.h"
+
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -390,6 +392,177 @@ static void dq_iq4_xs(const uint8_t* b, float* y) { /* dequant.rs:481-497 */
   }
 }
 
+/* IQ grid types -- dequant.rs:505-723.  The codebooks are the format's
+ * fixed tables (mlx-llm_amd/csrc/iq_tables.h, the reference's
+ * src/gguf/iq_grids.rs); the sign table ksigns_iq2xs is its closed form:
+ * entry i is i with bit 7 set to the parity of i (every sign byte has an
+ * even number of set bits). */
+static const uint64_t IQ2XXS[256] = {MLXQ_IQ2XXS_GRID};
+static const uint64_t IQ2XS[512] = {MLXQ_IQ2XS_GRID};
+static const uint64_t IQ2S[1024] = {MLXQ_IQ2S_GRID};
+static const uint32_t IQ3XXS[256] = {MLXQ_IQ3XXS_GRID};
+static const uint32_t IQ3S[512] = {MLXQ_IQ3S_GRID};
+static const uint64_t IQ1S[2048] = {MLXQ_IQ1S_GRID};
+#define IQ1S_DELTA 0.125f /* dequant.rs:26-27 */
+
+uint8_t orc_ksigns_iq2xs(int i) {
+  int p = __builtin_popcount((unsigned)i & 127u) & 1;
+  return (uint8_t)((i & 127) | (p << 7));
+}
+
+int orc_iq_grid(int table, int i, uint64_t* entry) {
+  static const int sizes[6] = {256, 512, 1024, 256, 512, 2048};
+  if (table < 0 || table > 5) return -1;
+  if (!entry) return sizes[table];
+  if (i < 0 || i >= sizes[table]) return -1;
+  switch (table) {
+    case 0: *entry = IQ2XXS[i]; break;
+    case 1: *entry = IQ2XS[i]; break;
+    case 2: *entry = IQ2S[i]; break;
+    case 3: *entry = IQ3XXS[i]; break;
+    case 4: *entry = IQ3S[i]; break;
+    default: *entry = IQ1S[i]; break;
+  }
+  return sizes[table];
+}
+
+/* sign of output lane j for a sign byte: -1 where bit j is set (dequant.rs:508-516) */
+static float iq_sign(uint8_t signs, int j) { return (signs >> j) & 1 ? -1.0f : 1.0f; }
+static uint8_t grid_byte(uint64_t g, int j) { return (uint8_t)(g >> (8 * j)); }
+
+static void dq_iq2_xxs(const uint8_t* b, float* y) { /* dequant.rs:521-539 */
+  float d = rd_f16(b, 0);
+  for (int ib32 = 0; ib32 < 8; ib32++) {
+    const uint8_t* q = b + 2 + 8 * ib32;
+    uint32_t aux0 = rd_u32(q), aux1 = rd_u32(q + 4);
+    float db = d * (0.5f + (float)(aux1 >> 28)) * 0.25f;
+    for (int l = 0; l < 4; l++) {
+      uint64_t g = IQ2XXS[(aux0 >> (8 * l)) & 255];
+      uint8_t signs = orc_ksigns_iq2xs((aux1 >> (7 * l)) & 127);
+      for (int j = 0; j < 8; j++) y[32 * ib32 + 8 * l + j] = db * (float)grid_byte(g, j) * iq_sign(signs, j);
+    }
+  }
+}
+
+static void dq_iq2_xs(const uint8_t* b, float* y) { /* dequant.rs:543-564 */
+  float d = rd_f16(b, 0);
+  for (int ib32 = 0; ib32 < 8; ib32++) {
+    uint8_t sc = b[66 + ib32];
+    float db[2] = {d * (0.5f + (float)(sc & 0xF)) * 0.25f, d * (0.5f + (float)(sc >> 4)) * 0.25f};
+    for (int l = 0; l < 4; l++) {
+      int qo = 2 + 2 * (4 * ib32 + l);
+      uint16_t q = (uint16_t)(b[qo] | (b[qo + 1] << 8));
+      uint64_t g = IQ2XS[q & 511];
+      uint8_t signs = orc_ksigns_iq2xs(q >> 9);
+      for (int j = 0; j < 8; j++) y[32 * ib32 + 8 * l + j] = db[l / 2] * (float)grid_byte(g, j) * iq_sign(signs, j);
+    }
+  }
+}
+
+static void dq_iq2_s(const uint8_t* b, float* y) { /* dequant.rs:568-591 */
+  float d = rd_f16(b, 0);
+  const uint8_t* qs = b + 2;
+  const uint8_t* qh = b + 66;
+  const uint8_t* scales = b + 74;
+  for (int ib32 = 0; ib32 < 8; ib32++) {
+    uint8_t sc = scales[ib32];
+    float db[2] = {d * (0.5f + (float)(sc & 0xF)) * 0.25f, d * (0.5f + (float)(sc >> 4)) * 0.25f};
+    for (int l = 0; l < 4; l++) {
+      int idx = qs[4 * ib32 + l] | (((int)qh[ib32] << (8 - 2 * l)) & 0x300);
+      uint64_t g = IQ2S[idx];
+      uint8_t signs = qs[32 + 4 * ib32 + l];
+      for (int j = 0; j < 8; j++) y[32 * ib32 + 8 * l + j] = db[l / 2] * (float)grid_byte(g, j) * iq_sign(signs, j);
+    }
+  }
+}
+
+static void dq_iq3_xxs(const uint8_t* b, float* y) { /* dequant.rs:596-615 */
+  float d = rd_f16(b, 0);
+  const uint8_t* ss = b + 66;
+  for (int ib32 = 0; ib32 < 8; ib32++) {
+    uint32_t aux = rd_u32(ss + 4 * ib32);
+    float db = d * (0.5f + (float)(aux >> 28)) * 0.5f;
+    const uint8_t* q = b + 2 + 8 * ib32;
+    for (int l = 0; l < 4; l++) {
+      uint32_t g1 = IQ3XXS[q[2 * l]], g2 = IQ3XXS[q[2 * l + 1]];
+      uint8_t signs = orc_ksigns_iq2xs((aux >> (7 * l)) & 127);
+      for (int j = 0; j < 4; j++) {
+        y[32 * ib32 + 8 * l + j] = db * (float)grid_byte(g1, j) * iq_sign(signs, j);
+        y[32 * ib32 + 8 * l + j + 4] = db * (float)grid_byte(g2, j) * iq_sign(signs, j + 4);
+      }
+    }
+  }
+}
+
+static void dq_iq3_s(const uint8_t* b, float* y) { /* dequant.rs:619-651 */
+  float d = rd_f16(b, 0);
+  const uint8_t* qh = b + 66;
+  const uint8_t* signs = b + 74;
+  const uint8_t* scales = b + 106;
+  int yi = 0;
+  for (int k = 0; k < 4; k++) {
+    uint8_t sc = scales[k];
+    float dbs[2] = {d * (float)(1 + 2 * (sc & 0xF)), d * (float)(1 + 2 * (sc >> 4))};
+    for (int half = 0; half < 2; half++) {
+      float db = dbs[half];
+      uint32_t qhb = qh[2 * k + half];
+      const uint8_t* q = b + 2 + 16 * k + 8 * half;
+      const uint8_t* sg = signs + 8 * k + 4 * half;
+      for (int l = 0; l < 4; l++) {
+        int i1 = q[2 * l] | (int)((qhb << (8 - 2 * l)) & 256);
+        int i2 = q[2 * l + 1] | (int)((qhb << (7 - 2 * l)) & 256);
+        uint32_t g1 = IQ3S[i1], g2 = IQ3S[i2];
+        for (int j = 0; j < 4; j++) {
+          y[yi + j] = db * (float)grid_byte(g1, j) * iq_sign(sg[l], j);
+          y[yi + j + 4] = db * (float)grid_byte(g2, j) * iq_sign(sg[l], j + 4);
+        }
+        yi += 8;
+      }
+    }
+  }
+}
+
+static void dq_iq1_s(const uint8_t* b, float* y) { /* dequant.rs:655-673 */
+  float d = rd_f16(b, 0);
+  const uint8_t* qs = b + 2;
+  const uint8_t* qh = b + 34;
+  for (int ib = 0; ib < 8; ib++) {
+    uint16_t h = (uint16_t)(qh[2 * ib] | (qh[2 * ib + 1] << 8));
+    float dl = d * (float)(2 * ((h >> 12) & 7) + 1);
+    float delta = (h & 0x8000) ? -IQ1S_DELTA : IQ1S_DELTA;
+    for (int l = 0; l < 4; l++) {
+      int idx = qs[4 * ib + l] | (((h >> (3 * l)) & 7) << 8);
+      uint64_t g = IQ1S[idx];
+      for (int j = 0; j < 8; j++) y[32 * ib + 8 * l + j] = dl * ((float)(int8_t)grid_byte(g, j) + delta);
+    }
+  }
+}
+
+static void dq_iq1_m(const uint8_t* b, float* y) { /* dequant.rs:678-719 */
+  const uint8_t* qs = b;
+  const uint8_t* qh = b + 32;
+  uint16_t sc[4];
+  for (int i = 0; i < 4; i++) sc[i] = (uint16_t)(b[48 + 2 * i] | (b[49 + 2 * i] << 8));
+  uint16_t bits = (uint16_t)((sc[0] >> 12) | ((sc[1] >> 8) & 0x00F0) | ((sc[2] >> 4) & 0x0F00) | (sc[3] & 0xF000));
+  float d = orc_f16_to_f32(bits);
+  for (int ib = 0; ib < 8; ib++) {
+    uint16_t w = sc[ib / 2];
+    int shift = 6 * (ib % 2);
+    float dl1 = d * (float)(2 * ((w >> shift) & 7) + 1);
+    float dl2 = d * (float)(2 * ((w >> (shift + 3)) & 7) + 1);
+    int qh0 = qh[2 * ib], qh1 = qh[2 * ib + 1];
+    int idx[4] = {qs[4 * ib] | ((qh0 << 8) & 0x700), qs[4 * ib + 1] | ((qh0 << 4) & 0x700),
+                  qs[4 * ib + 2] | ((qh1 << 8) & 0x700), qs[4 * ib + 3] | ((qh1 << 4) & 0x700)};
+    float delta[4] = {(qh0 & 0x08) ? -IQ1S_DELTA : IQ1S_DELTA, (qh0 & 0x80) ? -IQ1S_DELTA : IQ1S_DELTA,
+                      (qh1 & 0x08) ? -IQ1S_DELTA : IQ1S_DELTA, (qh1 & 0x80) ? -IQ1S_DELTA : IQ1S_DELTA};
+    for (int l = 0; l < 4; l++) {
+      float dl = l < 2 ? dl1 : dl2;
+      uint64_t g = IQ1S[idx[l]];
+      for (int j = 0; j < 8; j++) y[32 * ib + 8 * l + j] = dl * ((float)(int8_t)grid_byte(g, j) + delta[l]);
+    }
+  }
+}
+
 typedef void (*dq_fn)(const uint8_t*, float*);
 static dq_fn dq_for(uint32_t tag) {
   switch (tag) {
@@ -405,6 +578,13 @@ static dq_fn dq_for(uint32_t tag) {
     case 14: return dq_q6_k;
     case 20: return dq_iq4_nl;
     case 23: return dq_iq4_xs;
+    case 16: return dq_iq2_xxs;
+    case 17: return dq_iq2_xs;
+    case 22: return dq_iq2_s;
+    case 18: return dq_iq3_xxs;
+    case 21: return dq_iq3_s;
+    case 19: return dq_iq1_s;
+    case 29: return dq_iq1_m;
     default: return NULL;
   }
 }
@@ -429,7 +609,7 @@ static int dequant_impl(uint32_t tag, const uint8_t* data, int64_t data_len,
     return 0;
   }
   dq_fn f = dq_for(tag);
-  if (!f) return 3; /* grid types: not restated in this oracle */
+  if (!f) return 3;
 #ifdef _OPENMP
 #pragma omp parallel for schedule(static) num_threads(threads > 0 ? threads : 1)
 #endif

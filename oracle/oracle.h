@@ -42,11 +42,21 @@ float orc_bf16_to_f32(uint16_t b);
 int orc_gguf_block(uint32_t tag, int64_t* elems, int64_t* bytes);
 int orc_gguf_tensor_byte_len(uint32_t tag, int64_t n, int64_t* bytes);
 /* dequant.rs:156-211: returns 0 ok, 3 unsupported, 2 n not a multiple,
- * 4 data shorter than needed.  Supports every non-grid type: F32, F16, BF16,
- * Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS.
- * IQ1/IQ2/IQ3 grid types return 3 (not restated here). */
+ * 4 data shorter than needed.  Every type the reference decodes: F32, F16,
+ * BF16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ4_NL,
+ * IQ4_XS and the grid types IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_S,
+ * IQ1_M (dequant.rs:505-719).
+ * pinned (grid types): the reference's known answers (dequant.rs:877-955),
+ * the codebooks' structure and closed forms of single-bit changes
+ * (tests/test_oracle_iq.py). */
 int orc_gguf_dequantize(uint32_t tag, const uint8_t* data, int64_t data_len,
                         int64_t n, float* out);
+/* ksigns_iq2xs entry i (i < 128): i with bit 7 = parity of i. */
+uint8_t orc_ksigns_iq2xs(int i);
+/* Codebook `table` (0 IQ2_XXS, 1 IQ2_XS, 2 IQ2_S, 3 IQ3_XXS, 4 IQ3_S,
+ * 5 IQ1_S): entry i into *entry (if non-null); returns the table size, -1
+ * for a bad table or index. */
+int orc_iq_grid(int table, int i, uint64_t* entry);
 
 /* ---- GGUF block producers (NOT in the reference; llama.cpp block layouts
  * restated from the public ggml format so tests have realistic blocks).

@@ -50,6 +50,9 @@ def lib() -> ctypes.CDLL:
         L.orc_gguf_dequantize.argtypes = [ctypes.c_uint32, _P, _i64, _i64, _P]
         L.orc_gguf_dequantize_mt.argtypes = [ctypes.c_uint32, _P, _i64, _i64, _P, ctypes.c_int]
         L.orc_gguf_quantize.argtypes = [ctypes.c_uint32, _P, _i64, _P]
+        L.orc_ksigns_iq2xs.restype = ctypes.c_uint8
+        L.orc_ksigns_iq2xs.argtypes = [ctypes.c_int]
+        L.orc_iq_grid.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_uint64)]
         L.orc_affine_quantize.argtypes = [ctypes.c_int, _P, _i64, _i64, ctypes.c_int, ctypes.c_int, _P, _P, _P]
         L.orc_affine_dequantize.argtypes = [ctypes.c_int, _P, _P, _P, _i64, _i64, ctypes.c_int, ctypes.c_int, _P]
         L.orc_qmatmul_f64.argtypes = [_P, _i64, _P, _P, _P, _i64, _i64, ctypes.c_int, ctypes.c_int, _P]
@@ -125,6 +128,26 @@ def gguf_dequantize(tag: int, data: np.ndarray, n: int, threads: int = 1) -> np.
     else:
         _chk(lib().orc_gguf_dequantize(tag, _p(data), data.size, n, _p(out)))
     return out
+
+
+IQ_GRIDS = {"iq2xxs": 0, "iq2xs": 1, "iq2s": 2, "iq3xxs": 3, "iq3s": 4, "iq1s": 5}
+
+
+def iq_grid(name: str) -> np.ndarray:
+    """A GGUF IQ codebook as stored (uint64 entries; the 4-byte grids in the
+    low 32 bits)."""
+    t = IQ_GRIDS[name]
+    n = lib().orc_iq_grid(t, 0, None)
+    out = np.empty(n, dtype=np.uint64)
+    v = ctypes.c_uint64(0)
+    for i in range(n):
+        assert lib().orc_iq_grid(t, i, ctypes.byref(v)) == n
+        out[i] = v.value
+    return out
+
+
+def ksigns_iq2xs() -> np.ndarray:
+    return np.array([lib().orc_ksigns_iq2xs(i) for i in range(128)], dtype=np.uint8)
 
 
 def gguf_quantize(tag: int, x: np.ndarray) -> np.ndarray:

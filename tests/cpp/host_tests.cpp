@@ -253,6 +253,63 @@ void q6_k_centered_is_zero() {
   for (float v : gguf::dequantize(14, b.data(), b.size(), 256)) EXPECT(v == 0.0f);
 }
 
+// dequant.rs:877-882 iq_block_d1: f16 d = 1, then a zero payload
+std::vector<uint8_t> iq_block_d1(size_t total) {
+  std::vector<uint8_t> b;
+  push16(b, f16_bits(1.0f));
+  b.resize(total, 0);
+  return b;
+}
+
+bool all_equal(const std::vector<float>& v, size_t from, size_t to, float x) {
+  for (size_t i = from; i < to; i++)
+    if (v[i] != x) return false;
+  return true;
+}
+
+// dequant.rs:889-900
+void iq2_xxs_grid_scale_and_offset() {
+  const std::vector<float> out = gguf::dequantize(16, iq_block_d1(66).data(), 66, 256);
+  EXPECT(all_equal(out, 0, 256, 1.0f));
+  std::vector<uint8_t> b2 = iq_block_d1(66);
+  b2[9] = 0x30;
+  const std::vector<float> out2 = gguf::dequantize(16, b2.data(), b2.size(), 256);
+  EXPECT(all_equal(out2, 0, 32, 7.0f));
+  EXPECT(out2[32] == 1.0f);
+}
+
+// dequant.rs:904-910
+void iq2_xs_and_s_grid_zero_decode() {
+  EXPECT(all_equal(gguf::dequantize(17, iq_block_d1(74).data(), 74, 256), 0, 256, 1.0f));
+  EXPECT(all_equal(gguf::dequantize(22, iq_block_d1(82).data(), 82, 256), 0, 256, 1.0f));
+}
+
+// dequant.rs:914-920
+void iq3_xxs_and_s_grid_zero_decode() {
+  EXPECT(all_equal(gguf::dequantize(18, iq_block_d1(98).data(), 98, 256), 0, 256, 1.0f));
+  EXPECT(all_equal(gguf::dequantize(21, iq_block_d1(110).data(), 110, 256), 0, 256, 1.0f));
+}
+
+// dequant.rs:925-937
+void iq1_s_signed_grid_and_scale() {
+  EXPECT(all_equal(gguf::dequantize(19, iq_block_d1(50).data(), 50, 256), 0, 256, -0.875f));
+  std::vector<uint8_t> b = iq_block_d1(50);
+  b[35] = 0x10;
+  const std::vector<float> out2 = gguf::dequantize(19, b.data(), b.size(), 256);
+  EXPECT(all_equal(out2, 0, 32, -2.625f));
+  EXPECT(out2[32] == -0.875f);
+}
+
+// dequant.rs:941-955
+void iq1_m_packed_f16_scale() {
+  std::vector<uint8_t> b(56, 0);
+  b[53] = 0xC0;
+  b[55] = 0x30;
+  EXPECT(all_equal(gguf::dequantize(29, b.data(), b.size(), 256), 0, 256, -0.875f));
+  const std::vector<uint8_t> zero(56, 0);
+  EXPECT(all_equal(gguf::dequantize(29, zero.data(), zero.size(), 256), 0, 256, 0.0f));
+}
+
 // dequant.rs:159-171: element count not a multiple of the block, short data
 void dequantize_errors() {
   std::vector<uint8_t> b(18 * 2, 0x88);
@@ -446,6 +503,11 @@ int main(int argc, char** argv) {
       {"q2_k_scale_and_unpack", q2_k_scale_and_unpack},
       {"q6_k_centered_is_zero", q6_k_centered_is_zero},
       {"dequantize_errors", dequantize_errors},
+      {"iq2_xxs_grid_scale_and_offset", iq2_xxs_grid_scale_and_offset},
+      {"iq2_xs_and_s_grid_zero_decode", iq2_xs_and_s_grid_zero_decode},
+      {"iq3_xxs_and_s_grid_zero_decode", iq3_xxs_and_s_grid_zero_decode},
+      {"iq1_s_signed_grid_and_scale", iq1_s_signed_grid_and_scale},
+      {"iq1_m_packed_f16_scale", iq1_m_packed_f16_scale},
       {"requantize_projection_undoes_qk_permute", requantize_projection_undoes_qk_permute},
       {"projection_predicate_selects_only_attn_mlp_projections", projection_predicate_selects_only_attn_mlp_projections},
       {"dense_write_round_trips_bit_identical", dense_write_round_trips_bit_identical},

@@ -10,6 +10,11 @@ assertions of the reference tests:
   q4_0_zero_centered                src/gguf/dequant.rs:820-836
   q2_k_scale_and_unpack             src/gguf/dequant.rs:841-850
   q6_k_centered_is_zero             src/gguf/dequant.rs:854-875
+  iq2_xxs_grid_scale_and_offset     src/gguf/dequant.rs:884-900
+  iq2_xs_and_s_grid_zero_decode     src/gguf/dequant.rs:902-910
+  iq3_xxs_and_s_grid_zero_decode    src/gguf/dequant.rs:912-920
+  iq1_s_signed_grid_and_scale       src/gguf/dequant.rs:922-937
+  iq1_m_packed_f16_scale            src/gguf/dequant.rs:939-955
 
 and the two Q8 tolerance tests of src/primitives/quant.rs:91-125 (inputs and
 bounds).  Nothing from the reference is imported or run; the byte strings
@@ -68,6 +73,33 @@ def main():
     b[208:210] = le16(f16(1.0))
     cases.append({"name": "q6_k_centered_is_zero", "tag": 14, "n": 256, "hex": bytes(b).hex(),
                   "expect_all": [0.0] * 256})
+
+    # IQ grid types: f16 d = 1 then a zero payload (iq_block_d1, dequant.rs:877-882)
+    def iq_d1(total, **patch):
+        b = bytearray(le16(f16(1.0)) + bytes(total - 2))
+        for k, v in patch.items():
+            b[int(k[1:])] = v
+        return bytes(b)
+
+    cases.append({"name": "iq2_xxs_grid_zero", "tag": 16, "n": 256, "hex": iq_d1(66).hex(),
+                  "expect_all": [1.0] * 256})
+    cases.append({"name": "iq2_xxs_block0_scale3", "tag": 16, "n": 256, "hex": iq_d1(66, b9=0x30).hex(),
+                  "expect_all": [7.0] * 32 + [1.0] * 224})
+    cases.append({"name": "iq2_xs_grid_zero", "tag": 17, "n": 256, "hex": iq_d1(74).hex(), "expect_all": [1.0] * 256})
+    cases.append({"name": "iq2_s_grid_zero", "tag": 22, "n": 256, "hex": iq_d1(82).hex(), "expect_all": [1.0] * 256})
+    cases.append({"name": "iq3_xxs_grid_zero", "tag": 18, "n": 256, "hex": iq_d1(98).hex(),
+                  "expect_all": [1.0] * 256})
+    cases.append({"name": "iq3_s_grid_zero", "tag": 21, "n": 256, "hex": iq_d1(110).hex(), "expect_all": [1.0] * 256})
+    cases.append({"name": "iq1_s_signed_grid", "tag": 19, "n": 256, "hex": iq_d1(50).hex(),
+                  "expect_all": [-0.875] * 256})
+    cases.append({"name": "iq1_s_block0_scale3", "tag": 19, "n": 256, "hex": iq_d1(50, b35=0x10).hex(),
+                  "expect_all": [-2.625] * 32 + [-0.875] * 224})
+    b = bytearray(56)
+    b[53] = 0xC0  # sc2 = 0xC000
+    b[55] = 0x30  # sc3 = 0x3000 -> d = f16 0x3C00 = 1.0
+    cases.append({"name": "iq1_m_packed_f16_scale", "tag": 29, "n": 256, "hex": bytes(b).hex(),
+                  "expect_all": [-0.875] * 256})
+    cases.append({"name": "iq1_m_zero_scale", "tag": 29, "n": 256, "hex": bytes(56).hex(), "expect_all": [0.0] * 256})
 
     geometry = {  # dequant.rs:727-746 (tag: [elems, bytes])
         "2": [32, 18], "3": [32, 20], "6": [32, 22], "7": [32, 24], "8": [32, 34], "10": [256, 84],

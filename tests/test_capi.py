@@ -59,7 +59,8 @@ def test_gguf_error_paths():
     assert _gguf(2, 17, 32) == mlxq.ERR_SHORT_BUFFER   # dequant.rs:166-171
     assert b"needs 18 bytes" in mlxq.lib().mlxq_last_error()
     assert _gguf(9, 64, 32) == mlxq.ERR_UNSUPPORTED    # dequant.rs:109-111
-    assert _gguf(16, 66, 256) == mlxq.ERR_UNSUPPORTED  # grid types: no device kernel
+    assert _gguf(15, 292, 256) == mlxq.ERR_UNSUPPORTED  # dequant.rs:763-765 (Q8_K)
+    assert _gguf(16, 65, 256) == mlxq.ERR_SHORT_BUFFER  # IQ2_XXS: 66 bytes per 256
     assert _gguf(2, 18, 32, out_dtype=mlxq.F16) == mlxq.ERR_UNSUPPORTED
     assert _gguf(2, 0, 0) == mlxq.OK                   # empty tensor
 

@@ -12,7 +12,8 @@ from helpers import dev, host
 pytestmark = pytest.mark.gpu
 
 TAGS = {"F32": 0, "F16": 1, "BF16": 30, "Q4_0": 2, "Q4_1": 3, "Q5_0": 6, "Q5_1": 7, "Q8_0": 8, "Q2_K": 10,
-        "Q3_K": 11, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14, "IQ4_NL": 20, "IQ4_XS": 23}
+        "Q3_K": 11, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14, "IQ4_NL": 20, "IQ4_XS": 23, "IQ2_XXS": 16, "IQ2_XS": 17,
+        "IQ2_S": 22, "IQ3_XXS": 18, "IQ3_S": 21, "IQ1_S": 19, "IQ1_M": 29}
 
 
 def blocks(tag, rows, cols, seed):
@@ -28,8 +29,10 @@ def blocks(tag, rows, cols, seed):
     # other types: random block bytes with every f16 scale field finite (|d| < 2)
     e, nb = orc.gguf_block(tag)
     raw = np.random.default_rng(seed).integers(0, 256, size=(rows * cols // e, nb), dtype=np.uint8)
-    for o in {3: [0, 2], 6: [0], 7: [0, 2], 10: [80, 82], 11: [108], 13: [0, 2]}[tag]:
+    for o in {3: [0, 2], 6: [0], 7: [0, 2], 10: [80, 82], 11: [108], 13: [0, 2]}.get(tag, [0] if tag != 29 else []):
         raw[:, o + 1] &= 0x3B
+    if tag == 29:  # IQ1_M: the f16 scale's top nibble is the last scale word's
+        raw[:, 55] &= 0x3F
     return raw.ravel()
 
 
@@ -82,7 +85,7 @@ def test_requantize_errors(torch_gpu):
     d = torch.zeros(18 * 4, dtype=torch.uint8, device="cuda")
     with pytest.raises(mlxq.MlxqError):  # data shorter than the blocks (2 rows x 64 Q4_0 = 4 blocks... x2)
         mlxq.gguf_requantize(2, d, 4, 64, 0, 64, 4)
-    with pytest.raises(mlxq.Unsupported):  # IQ2_XXS has no device decoder
-        mlxq.gguf_requantize(16, d, 1, 256, 0, 64, 4)
+    with pytest.raises(mlxq.Unsupported):  # tag 9 (Q8_1) is not a type the reference decodes
+        mlxq.gguf_requantize(9, d, 1, 32, 0, 32, 4)
     with pytest.raises(mlxq.MlxqError):  # odd head_dim
         mlxq.gguf_requantize(2, torch.zeros(18 * 6, dtype=torch.uint8, device="cuda"), 6, 32, 2, 32, 4)

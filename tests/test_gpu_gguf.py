@@ -12,7 +12,7 @@ from helpers import dev, host
 
 pytestmark = pytest.mark.gpu
 KAT = json.loads((Path(__file__).resolve().parent / "golden" / "gguf_kat.json").read_text())
-DEVICE_TAGS = [2, 3, 6, 7, 8, 10, 11, 12, 13, 14, 20, 23]
+DEVICE_TAGS = [2, 3, 6, 7, 8, 10, 11, 12, 13, 14, 20, 23, 16, 17, 22, 18, 21, 19, 29]
 STAR_TAGS = [2, 8, 12, 14, 20, 23]  # Q4_0 Q8_0 Q4_K Q6_K IQ4_NL IQ4_XS
 rng = np.random.default_rng(77)
 
@@ -33,9 +33,11 @@ def random_blocks(tag, nblk):
     e, b = orc.gguf_block(tag)
     raw = rng.integers(0, 256, size=(nblk, b), dtype=np.uint8)
     d_off = {2: [0], 3: [0, 2], 6: [0], 7: [0, 2], 8: [0], 10: [80, 82], 11: [108], 12: [0, 2], 13: [0, 2],
-             14: [208], 20: [0], 23: [0]}[tag]
+             14: [208], 20: [0], 23: [0], 16: [0], 17: [0], 22: [0], 18: [0], 21: [0], 19: [0]}.get(tag, [])
     for o in d_off:
         raw[:, o + 1] &= 0x3B  # exponent <= 14: finite, below 2
+    if tag == 29:  # IQ1_M: f16 bits 12-15 (sign, exponent top) are the top nibble of the last scale word
+        raw[:, 55] &= 0x3F
     return raw.ravel(), e * nblk
 
 

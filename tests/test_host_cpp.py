@@ -12,7 +12,9 @@ CASES = [
     "quantize_dequantize_roundtrip_q8", "quantized_matmul_approximates_linear_q8", "projection_load_and_dispatch",
     "type_geometry_matches_llama_cpp", "supported_and_unsupported_types", "iq4_nl_codebook_decode",
     "f32_f16_bf16_passthrough", "q8_0_block_dequant", "q4_0_zero_centered", "q2_k_scale_and_unpack",
-    "q6_k_centered_is_zero", "dequantize_errors", "requantize_projection_undoes_qk_permute",
+    "q6_k_centered_is_zero", "dequantize_errors", "iq2_xxs_grid_scale_and_offset", "iq2_xs_and_s_grid_zero_decode",
+    "iq3_xxs_and_s_grid_zero_decode", "iq1_s_signed_grid_and_scale", "iq1_m_packed_f16_scale",
+    "requantize_projection_undoes_qk_permute",
     "projection_predicate_selects_only_attn_mlp_projections", "dense_write_round_trips_bit_identical",
     "quantized_write_loads_through_prequantized_branch",
 ]
