@@ -25,6 +25,7 @@
 #include <stdlib.h>
 
 #include <string>
+#include <type_traits>
 
 #include "common.hpp"
 #include "qmatmul.hpp"
@@ -35,25 +36,37 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int BK = 64;
 constexpr int LDR = BK + 8;  // padded LDS row, bf16 elements
 
-// Tile BM x BN, WM x WN wavefronts (each (BM/WM) x (BN/WN) of the output).
-template <int BM, int BN, int WM, int WN, int BITS>
+// Tile BM x BN, WM x WN wavefronts (each (BM/WM) x (BN/WN) of the output)
+// in MF x MF MFMA tiles (32: v_mfma_f32_32x32x16_bf16, 16:
+// v_mfma_f32_16x16x32_bf16).
+template <int BM, int BN, int WM, int WN, int BITS, int MF>
 struct QmmGeom {
   static constexpr int THREADS = 64 * WM * WN;
-  static constexpr int STAGE = (BM + BN) * LDR;           // bf16 per LDS stage
+  static constexpr int PARTS = THREADS >= 2 * BN ? 2 : 1;  // threads per weight row
+  // rows the weight loader covers: BN, or more when BN does not divide the
+  // threads (the extra rows repeat clamped weights into spare LDS rows, so
+  // no thread branches around its loads)
+  static constexpr int LROWS = THREADS / PARTS;
+  static constexpr int STAGE = (BM + LROWS) * LDR;         // bf16 per LDS stage
   static constexpr int LDS_BYTES = 2 * STAGE * 2;          // two stages
-  static constexpr int TM = BM / WM / 32;                  // 32-row MFMA tiles per wave
-  static constexpr int TN = BN / WN / 32;                  // 32-col MFMA tiles per wave
+  static constexpr int TM = BM / WM / MF;                  // MFMA row tiles per wave
+  static constexpr int TN = BN / WN / MF;                  // MFMA column tiles per wave
+  static constexpr int NV = MF * MF / 64;                  // accumulator floats per lane per tile
+  static constexpr int KS = 512 / MF;                      // k per MFMA
   static constexpr int AU4 = BM * 8 / THREADS;             // activation uint4 per thread per step
-  static constexpr int PARTS = THREADS / BN;               // threads per weight row (1 or 2)
   static constexpr int CPT = BK / PARTS;                   // codes per thread per step
   static constexpr int BU4 = CPT * BITS / 128;             // code uint4 per thread per step
-  static_assert(THREADS % BN == 0 && (PARTS == 1 || PARTS == 2), "weight rows map onto threads");
+  static_assert(MF == 16 || MF == 32, "MFMA shape");
+  static_assert(LROWS >= BN && THREADS % PARTS == 0, "weight rows map onto threads");
+  static_assert((BM / WM) % MF == 0 && (BN / WN) % MF == 0, "wave tiles are whole MFMA tiles");
   static_assert(BM * 8 % THREADS == 0, "activation chunks map onto threads");
+  static_assert(LDS_BYTES <= 160 * 1024, "two stages fit in LDS");
 };
 
 __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
@@ -75,7 +88,7 @@ struct Stage {
   uint16_t s[NSG], z[NSG];
 };
 
-template <int BITS, int GS, int BM, int BN, int WM, int WN>
+template <int BITS, int GS, int BM, int BN, int WM, int WN, int MF>
 __global__ __launch_bounds__(64 * WM * WN, 1) void qmm_kernel(const uint16_t* __restrict__ x, int M,
                                                                const uint32_t* __restrict__ wq,
                                                                const uint16_t* __restrict__ scales,
@@ -83,7 +96,8 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void qmm_kernel(const uint16_t* __
                                                                const uint16_t* __restrict__ bias_vec, int N, int K,
                                                                uint16_t* __restrict__ y, float* __restrict__ part,
                                                                int k_len) {
-  using Gm = QmmGeom<BM, BN, WM, WN, BITS>;
+  using Gm = QmmGeom<BM, BN, WM, WN, BITS, MF>;
+  using AccT = std::conditional_t<MF == 32, f32x16, f32x4>;
   // scale/bias groups per thread per step: two only for g32 with 64 codes
   constexpr int NSG = (GS == 32 && Gm::CPT == 64) ? 2 : 1;
   using St = Stage<Gm, NSG>;
@@ -171,16 +185,18 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void qmm_kernel(const uint16_t* __
       dst[i] = u32x4{packed[4 * i], packed[4 * i + 1], packed[4 * i + 2], packed[4 * i + 3]};
   };
 
-  f32x16 acc[Gm::TM][Gm::TN];
+  AccT acc[Gm::TM][Gm::TN];
 #pragma unroll
   for (int i = 0; i < Gm::TM; i++)
 #pragma unroll
     for (int j = 0; j < Gm::TN; j++)
 #pragma unroll
-      for (int v = 0; v < 16; v++) acc[i][j][v] = 0.f;
+      for (int v = 0; v < Gm::NV; v++) acc[i][j][v] = 0.f;
 
-  const int frag_row = lane & 31;
-  const int frag_k = (lane >> 5) * 8;
+  // A/B fragment of an MF x MF tile: lane holds row lane % MF and 8
+  // consecutive k from (lane / MF) * 8
+  const int frag_row = lane & (MF - 1);
+  const int frag_k = (lane / MF) * 8;
   constexpr int WROWS = BM / WM, WCOLS = BN / WN;
 
   St r0, r1;
@@ -200,21 +216,25 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void qmm_kernel(const uint16_t* __
     load(target, min(kt + 2, KT - 1));
     __builtin_amdgcn_sched_barrier(0);
     const uint16_t* sa = lds + cur * Gm::STAGE + (wm * WROWS + frag_row) * LDR + frag_k;
-    const uint16_t* sb = lds + cur * Gm::STAGE + BM * LDR + (wn * WCOLS + frag_row) * LDR + frag_k;
+    const uint16_t* sb = lds + cur * Gm::STAGE + BM * LDR + (wn * WCOLS + frag_row) * LDR + frag_k;  // weights
 #pragma unroll
-    for (int ks = 0; ks < BK / 16; ks++) {
+    for (int ks = 0; ks < BK / Gm::KS; ks++) {
       bf16x8 a[Gm::TM], b[Gm::TN];
 #pragma unroll
       for (int i = 0; i < Gm::TM; i++)
-        a[i] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(sa + 32 * i * LDR + ks * 16));
+        a[i] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(sa + MF * i * LDR + ks * Gm::KS));
 #pragma unroll
       for (int j = 0; j < Gm::TN; j++)
-        b[j] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(sb + 32 * j * LDR + ks * 16));
+        b[j] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(sb + MF * j * LDR + ks * Gm::KS));
 #pragma unroll
       for (int i = 0; i < Gm::TM; i++)
 #pragma unroll
-        for (int j = 0; j < Gm::TN; j++)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < Gm::TN; j++) {
+          if constexpr (MF == 32)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+          else
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
     }
     if (kt + 1 < KT) store(ready, cur ^ 1);
     __syncthreads();
@@ -224,19 +244,23 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void qmm_kernel(const uint16_t* __
     if (kt + 1 < KT) step(kt + 1, r1, r0);
   }
 
-  // C layout of a 32x32 MFMA tile: lane holds column lane%32 and rows
-  // 8*(v/4) + 4*(lane/32) + v%4.
+  // C layout of an MFMA tile: lane holds column lane % MF and, for 32x32,
+  // rows 8*(v/4) + 4*(lane/32) + v%4; for 16x16, rows 4*(lane/16) + v.
+  auto row_of = [&](int i, int v) {
+    return m0 + wm * WROWS + MF * i +
+           (MF == 32 ? 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3) : 4 * (lane >> 4) + v);
+  };
   if (part) {  // split K: this slice's f32 partial sums, added by the reduce kernel
     float* dst = part + static_cast<int64_t>(blockIdx.z) * M * N;
 #pragma unroll
     for (int j = 0; j < Gm::TN; j++) {
-      const int n = n0 + wn * WCOLS + 32 * j + (lane & 31);
+      const int n = n0 + wn * WCOLS + MF * j + (lane & (MF - 1));
       if (n >= N) continue;
 #pragma unroll
       for (int i = 0; i < Gm::TM; i++)
 #pragma unroll
-        for (int v = 0; v < 16; v++) {
-          const int m = m0 + wm * WROWS + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+        for (int v = 0; v < Gm::NV; v++) {
+          const int m = row_of(i, v);
           if (m < M) dst[static_cast<int64_t>(m) * N + n] = acc[i][j][v];
         }
     }
@@ -244,24 +268,24 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void qmm_kernel(const uint16_t* __
   }
 #pragma unroll
   for (int j = 0; j < Gm::TN; j++) {
-    const int n = n0 + wn * WCOLS + 32 * j + (lane & 31);
+    const int n = n0 + wn * WCOLS + MF * j + (lane & (MF - 1));
     if (n >= N) continue;
     const float bb = bias_vec ? bf16_bits_to_f32(bias_vec[n]) : 0.f;
 #pragma unroll
     for (int i = 0; i < Gm::TM; i++)
 #pragma unroll
-      for (int v = 0; v < 16; v++) {
-        const int m = m0 + wm * WROWS + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+      for (int v = 0; v < Gm::NV; v++) {
+        const int m = row_of(i, v);
         if (m < M) y[static_cast<int64_t>(m) * N + n] = static_cast<uint16_t>(f32_to_bf16_bits(acc[i][j][v] + bb));
       }
   }
 }
 
-template <int BITS, int GS, int BM, int BN, int WM, int WN>
+template <int BITS, int GS, int BM, int BN, int WM, int WN, int MF = 32>
 int launch(const uint16_t* x, int M, const uint32_t* wq, const uint16_t* s, const uint16_t* b, const uint16_t* bias,
            int N, int K, uint16_t* y, float* part, int splits, hipStream_t st) {
-  using Gm = QmmGeom<BM, BN, WM, WN, BITS>;
-  auto kern = qmm_kernel<BITS, GS, BM, BN, WM, WN>;
+  using Gm = QmmGeom<BM, BN, WM, WN, BITS, MF>;
+  auto kern = qmm_kernel<BITS, GS, BM, BN, WM, WN, MF>;
   static bool attr_set = false;  // once per process; the attribute is per function
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -292,12 +316,18 @@ template <int BITS, int GS>
 int launch_cfg(const uint16_t* x, int M, const uint32_t* wq, const uint16_t* s, const uint16_t* b, const uint16_t* bias,
                int N, int K, uint16_t* y, float* part, int splits, hipStream_t st) {
   // 256 x 256 tiles (8 wavefronts, 4 x 2 of 64 x 128; one workgroup per
-  // CU) when they still give about every CU a tile, else 128 x 128 (4
-  // wavefronts of 64 x 64, two workgroups per CU) -- the faster of the
-  // measured configurations at the Llama-3-8B projection shapes for M from
-  // 256 to 4096.  MLXQ_QMM_CFG overrides (tuning).
+  // CU) when they still give about every CU a tile (or K is split), else
+  // 128 x 128 (4 wavefronts of 64 x 64, two workgroups per CU) -- the faster
+  // of the measured configurations at the Llama-3-8B projection shapes for M
+  // from 256 to 4096.  MLXQ_QMM_CFG overrides (tuning).
   const int64_t tiles256 = ceil_div(N, 256) * ceil_div(M, 256);
-  int cfg = splits > 1 || tiles256 * 8 >= static_cast<int64_t>(cu_count()) * 7 ? 4 : 6;
+  const int64_t cus = cu_count();
+  int cfg = splits > 1 || tiles256 * 8 >= cus * 7 ? 4 : 6;
+  // N a multiple of 224 (gate/up: 14336 = 64 x 224): 256 x 224 tiles (4 x 2
+  // waves of 64 x 112 in 16 x 16 MFMA tiles) make whole rounds of the CUs
+  // where 256 x 256 tiles leave a partial one (e.g. 256 vs 224 tiles at
+  // M = 1024: 818 vs 738 TFLOP/s; 2 rounds vs 1.75 at M = 2048: 918 vs 897)
+  if (splits == 1 && N % 224 == 0 && (N / 224) * ceil_div(M, 256) * 8 >= cus * 7) cfg = 7;
   if (const char* e = getenv("MLXQ_QMM_CFG")) cfg = atoi(e);
   switch (cfg) {
     case 1: return launch<BITS, GS, 256, 256, 2, 4>(x, M, wq, s, b, bias, N, K, y, part, splits, st);
@@ -305,6 +335,7 @@ int launch_cfg(const uint16_t* x, int M, const uint32_t* wq, const uint16_t* s, 
     case 3: return launch<BITS, GS, 128, 256, 2, 4>(x, M, wq, s, b, bias, N, K, y, part, splits, st);
     case 4: return launch<BITS, GS, 256, 256, 4, 2>(x, M, wq, s, b, bias, N, K, y, part, splits, st);
     case 6: return launch<BITS, GS, 128, 128, 2, 2>(x, M, wq, s, b, bias, N, K, y, part, splits, st);
+    case 7: return launch<BITS, GS, 256, 224, 4, 2, 16>(x, M, wq, s, b, bias, N, K, y, part, splits, st);
     default: return launch<BITS, GS, 128, 256, 2, 2>(x, M, wq, s, b, bias, N, K, y, part, splits, st);
   }
 }

@@ -112,6 +112,23 @@ def test_qmm_split_k(torch_gpu, monkeypatch, bits, gs, splits, n):
     assert rel_err(run(x, wq, s, b, gs, bits, mlxq.ALGO_QMM, bias=bias), ref) <= TIGHT
 
 
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("cfg", [4, 6, 7])
+@pytest.mark.parametrize("n", [448, 300])
+def test_qmm_tile_configs(torch_gpu, monkeypatch, bits, cfg, n):
+    """Every qmm workgroup tile the dispatcher picks (256x256 / 128x128 in
+    32x32 MFMA tiles, 256x224 in 16x16 ones) with a bias, M and N not
+    multiples of the tile."""
+    monkeypatch.setenv("MLXQ_QMM_CFG", str(cfg))
+    monkeypatch.setenv("MLXQ_QMM_SPLIT", "1")
+    m, k = 300, 512
+    wq, s, b = make_layer(95 + bits + n, n, k, 64, bits)
+    x = bf16_acts(96 + cfg, m, k)
+    bias = orc.f32_to_bf16(orc.normal(97, n, 0, 1))
+    ref = orc.qmatmul_f64(x, wq, s, b, 64, bits) + orc.bf16_to_f32(bias)[None, :]
+    assert rel_err(run(x, wq, s, b, 64, bits, mlxq.ALGO_QMM, bias=bias), ref) <= TIGHT
+
+
 def test_bias_vector(torch_gpu):
     n, k = 192, 256
     wq, s, b = make_layer(70, n, k)
