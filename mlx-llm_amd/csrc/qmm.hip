@@ -88,7 +88,7 @@ struct Stage {
   uint16_t s[NSG], z[NSG];
 };
 
-template <int BITS, int GS, int BM, int BN, int WM, int WN, int MF>
+template <int BITS, int GS, int BM, int BN, int WM, int WN, int MF, int PP>
 __global__ __launch_bounds__(64 * WM * WN, 1) void qmm_kernel(const uint16_t* __restrict__ x, int M,
                                                                const uint32_t* __restrict__ wq,
                                                                const uint16_t* __restrict__ scales,
@@ -98,6 +98,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void qmm_kernel(const uint16_t* __
                                                                int k_len) {
   using Gm = QmmGeom<BM, BN, WM, WN, BITS, MF>;
   using AccT = std::conditional_t<MF == 32, f32x16, f32x4>;
+  static_assert(!PP || (WM == 4 && WN == 2 && BM == 256), "ping-pong: two groups of four waves");
   // scale/bias groups per thread per step: two only for g32 with 64 codes
   constexpr int NSG = (GS == 32 && Gm::CPT == 64) ? 2 : 1;
   using St = Stage<Gm, NSG>;
@@ -113,12 +114,16 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void qmm_kernel(const uint16_t* __
   const int G = K / GS;
   const int64_t row_words = static_cast<int64_t>(K) * BITS / 32;
 
-  // activation loader: 8 threads per row (16 B each), rows tid/8 + (T/8) i
-  const int a_chunk = tid & 7, a_row0 = tid >> 3;
+  // activation loader: 8 threads per row (16 B each), rows tid/8 + (T/8) i;
+  // ping-pong: each half of the threads loads the rows its own waves
+  // multiply (half h: rows 128 h + (tid % 256)/8 + 32 i)
+  const int a_chunk = tid & 7;
+  const int a_row0 = PP != 0 ? (tid >> 8) * (BM / 2) + ((tid & (T / 2 - 1)) >> 3) : (tid >> 3);
+  constexpr int A_STRIDE = PP != 0 ? T / 16 : T / 8;
   const u32x4* a_src = reinterpret_cast<const u32x4*>(x) + a_chunk;
   int a_off[Gm::AU4];  // uint4 offset of each row (rows past M repeat row M-1; results dropped)
 #pragma unroll
-  for (int i = 0; i < Gm::AU4; i++) a_off[i] = min(m0 + a_row0 + (T / 8) * i, M - 1) * (K / 8);
+  for (int i = 0; i < Gm::AU4; i++) a_off[i] = min(m0 + a_row0 + A_STRIDE * i, M - 1) * (K / 8);
   // weight loader: PARTS threads per row, each CPT consecutive codes
   const int b_row = tid / Gm::PARTS, b_part = tid % Gm::PARTS;
   const int b_n = min(n0 + b_row, N - 1);
@@ -126,10 +131,13 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void qmm_kernel(const uint16_t* __
   const uint16_t* s_src = scales + static_cast<int64_t>(b_n) * G;
   const uint16_t* z_src = biases + static_cast<int64_t>(b_n) * G;
 
-  auto load = [&](St& r, int kt) __attribute__((always_inline)) {
+  auto load_a = [&](St& r, int kt) __attribute__((always_inline)) {
     const int k0 = k_base + kt * BK;
 #pragma unroll
     for (int i = 0; i < Gm::AU4; i++) r.a[i] = a_src[a_off[i] + k0 / 8];
+  };
+  auto load_b = [&](St& r, int kt) __attribute__((always_inline)) {
+    const int k0 = k_base + kt * BK;
 #pragma unroll
     for (int i = 0; i < Gm::BU4; i++) r.b[i] = b_src[k0 * BITS / 128 + i];
     const int kc = k0 + b_part * Gm::CPT;  // first code of this thread
@@ -139,13 +147,18 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void qmm_kernel(const uint16_t* __
       r.z[g] = z_src[kc / GS + g];
     }
   };
+  auto load = [&](St& r, int kt) __attribute__((always_inline)) {
+    load_a(r, kt);
+    load_b(r, kt);
+  };
 
-  auto store = [&](const St& r, int stage) __attribute__((always_inline)) {
+  // activations from ra, weights from r (the same stage)
+  auto store2 = [&](const St& ra, const St& r, int stage) __attribute__((always_inline)) {
     uint16_t* sa = lds + stage * Gm::STAGE;
     uint16_t* sb = sa + BM * LDR;
 #pragma unroll
     for (int i = 0; i < Gm::AU4; i++)
-      *reinterpret_cast<u32x4*>(sa + (a_row0 + (T / 8) * i) * LDR + a_chunk * 8) = r.a[i];
+      *reinterpret_cast<u32x4*>(sa + (a_row0 + A_STRIDE * i) * LDR + a_chunk * 8) = ra.a[i];
     constexpr int NW = Gm::BU4 * 4;  // code words
     uint32_t w[NW];
 #pragma unroll
@@ -184,6 +197,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void qmm_kernel(const uint16_t* __
     for (int i = 0; i < Gm::CPT / 8; i++)
       dst[i] = u32x4{packed[4 * i], packed[4 * i + 1], packed[4 * i + 2], packed[4 * i + 3]};
   };
+  auto store = [&](const St& r, int stage) __attribute__((always_inline)) { store2(r, r, stage); };
 
   AccT acc[Gm::TM][Gm::TN];
 #pragma unroll
@@ -204,6 +218,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void qmm_kernel(const uint16_t* __
   load(r1, min(1, KT - 1));
   __builtin_amdgcn_sched_barrier(0);
   store(r0, 0);
+  if constexpr ((PP & 8) != 0) load_b(r0, min(2, KT - 1));  // the weights run one step further ahead
   __syncthreads();
   // One K step: LDS stage kt&1 holds step kt, `ready` holds step kt+1 and
   // `target` receives step kt+2.  Called with (r0, r1) and (r1, r0) in turn
@@ -239,9 +254,106 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void qmm_kernel(const uint16_t* __
     if (kt + 1 < KT) store(ready, cur ^ 1);
     __syncthreads();
   };
-  for (int kt = 0; kt < KT; kt += 2) {
-    step(kt, r0, r1);
-    if (kt + 1 < KT) step(kt + 1, r1, r0);
+  if constexpr (PP != 0) {
+    // Ping-pong: waves 0-3 (group 0, output rows 0-127) and 4-7 (group 1,
+    // rows 128-255) take turns between barriers.  While one group runs its
+    // MFMAs on stage kt, the other writes its half of stage kt+1 (loaded two
+    // phases earlier) and requests its half of stage kt+2; each SIMD (one
+    // wave of each group) so has one wave on the matrix core and one on
+    // the vector ALU and LDS.  Stage (kt+1)&1 was last read in the previous
+    // step, which both groups have left.
+    const int grp = __builtin_amdgcn_readfirstlane((PP & 3) == 1 ? wave >> 2 : wave & 1);
+    auto mma = [&](int kt) __attribute__((always_inline)) {
+      if constexpr ((PP & 4) != 0) __builtin_amdgcn_s_setprio(1);
+      const int cur = kt & 1;
+      const uint16_t* sa = lds + cur * Gm::STAGE + (wm * WROWS + frag_row) * LDR + frag_k;
+      const uint16_t* sb = lds + cur * Gm::STAGE + BM * LDR + (wn * WCOLS + frag_row) * LDR + frag_k;
+#pragma unroll
+      for (int ks = 0; ks < BK / Gm::KS; ks++) {
+        bf16x8 a[Gm::TM], b[Gm::TN];
+#pragma unroll
+        for (int i = 0; i < Gm::TM; i++)
+          a[i] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(sa + MF * i * LDR + ks * Gm::KS));
+#pragma unroll
+        for (int j = 0; j < Gm::TN; j++)
+          b[j] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(sb + MF * j * LDR + ks * Gm::KS));
+#pragma unroll
+        for (int i = 0; i < Gm::TM; i++)
+#pragma unroll
+          for (int j = 0; j < Gm::TN; j++) {
+            if constexpr (MF == 32)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+            else
+              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+          }
+      }
+      if constexpr ((PP & 4) != 0) __builtin_amdgcn_s_setprio(0);
+    };
+    // r1 holds this thread's part of stage 1; past the end a stage nobody
+    // reads is written (unconditional: no branch around the loads)
+    auto fill = [&](int kt) __attribute__((always_inline)) {
+      store(r1, (kt + 1) & 1);
+      load(r1, min(kt + 2, KT - 1));
+    };
+    // deep form (PP & 8, KT even): the weights of stage kt+1 alternate
+    // between r1 and r0 and are requested three steps ahead, the
+    // activations (mostly L2 hits) two
+    auto fill_e = [&](int kt) __attribute__((always_inline)) {
+      store2(r1, r1, (kt + 1) & 1);
+      load_a(r1, min(kt + 2, KT - 1));
+      load_b(r1, min(kt + 3, KT - 1));
+    };
+    auto fill_o = [&](int kt) __attribute__((always_inline)) {
+      store2(r1, r0, (kt + 1) & 1);
+      load_a(r1, min(kt + 2, KT - 1));
+      load_b(r0, min(kt + 3, KT - 1));
+    };
+    // one loop per group (a wave-uniform branch): both run two barriers per
+    // step, so the barriers pair up with the groups half a step apart
+    if constexpr ((PP & 8) != 0) {
+      if (grp == 0) {
+        for (int kt = 0; kt < KT; kt += 2) {
+          mma(kt);
+          __syncthreads();
+          fill_e(kt);
+          __syncthreads();
+          mma(kt + 1);
+          __syncthreads();
+          fill_o(kt + 1);
+          __syncthreads();
+        }
+      } else {
+        for (int kt = 0; kt < KT; kt += 2) {
+          fill_e(kt);
+          __syncthreads();
+          mma(kt);
+          __syncthreads();
+          fill_o(kt + 1);
+          __syncthreads();
+          mma(kt + 1);
+          __syncthreads();
+        }
+      }
+    } else if (grp == 0) {
+      for (int kt = 0; kt < KT; kt++) {
+        mma(kt);
+        __syncthreads();
+        fill(kt);
+        __syncthreads();
+      }
+    } else {
+      for (int kt = 0; kt < KT; kt++) {
+        fill(kt);
+        __syncthreads();
+        mma(kt);
+        __syncthreads();
+      }
+    }
+  } else {
+    for (int kt = 0; kt < KT; kt += 2) {
+      step(kt, r0, r1);
+      if (kt + 1 < KT) step(kt + 1, r1, r0);
+    }
   }
 
   // C layout of an MFMA tile: lane holds column lane % MF and, for 32x32,
@@ -281,11 +393,11 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void qmm_kernel(const uint16_t* __
   }
 }
 
-template <int BITS, int GS, int BM, int BN, int WM, int WN, int MF = 32>
+template <int BITS, int GS, int BM, int BN, int WM, int WN, int MF = 32, int PP = 0>
 int launch(const uint16_t* x, int M, const uint32_t* wq, const uint16_t* s, const uint16_t* b, const uint16_t* bias,
            int N, int K, uint16_t* y, float* part, int splits, hipStream_t st) {
   using Gm = QmmGeom<BM, BN, WM, WN, BITS, MF>;
-  auto kern = qmm_kernel<BITS, GS, BM, BN, WM, WN, MF>;
+  auto kern = qmm_kernel<BITS, GS, BM, BN, WM, WN, MF, PP>;
   static bool attr_set = false;  // once per process; the attribute is per function
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -315,19 +427,21 @@ int cu_count() {
 template <int BITS, int GS>
 int launch_cfg(const uint16_t* x, int M, const uint32_t* wq, const uint16_t* s, const uint16_t* b, const uint16_t* bias,
                int N, int K, uint16_t* y, float* part, int splits, hipStream_t st) {
-  // 256 x 256 tiles (8 wavefronts, 4 x 2 of 64 x 128; one workgroup per
-  // CU) when they still give about every CU a tile (or K is split), else
-  // 128 x 128 (4 wavefronts of 64 x 64, two workgroups per CU) -- the faster
-  // of the measured configurations at the Llama-3-8B projection shapes for M
-  // from 256 to 4096.  MLXQ_QMM_CFG overrides (tuning).
+  // Configurations measured at the Llama-3-8B projection shapes for M from
+  // 256 to 4096; MLXQ_QMM_CFG overrides (tuning).
   const int64_t tiles256 = ceil_div(N, 256) * ceil_div(M, 256);
   const int64_t cus = cu_count();
-  int cfg = splits > 1 || tiles256 * 8 >= cus * 7 ? 4 : 6;
-  // N a multiple of 224 (gate/up: 14336 = 64 x 224): 256 x 224 tiles (4 x 2
-  // waves of 64 x 112 in 16 x 16 MFMA tiles) make whole rounds of the CUs
-  // where 256 x 256 tiles leave a partial one (e.g. 256 vs 224 tiles at
-  // M = 1024: 818 vs 738 TFLOP/s; 2 rounds vs 1.75 at M = 2048: 918 vs 897)
-  if (splits == 1 && N % 224 == 0 && (N / 224) * ceil_div(M, 256) * 8 >= cus * 7) cfg = 7;
+  // Ping-pong 256-row tiles (two groups of four waves take turns on the
+  // matrix cores) when the grid fills the CUs or K is split; the deep form
+  // (weights three K steps ahead) needs an even number of K steps.  For N a
+  // multiple of 224 (gate/up: 14336 = 64 x 224) Q4 takes 256 x 224 tiles,
+  // which make whole rounds of CUs where 256-wide ones leave a partial one.
+  // Grids too small for either: 128 x 128 tiles, two workgroups per CU.
+  const bool even_steps = (K / splits / BK) % 2 == 0;
+  int cfg = 6;
+  if (splits > 1 || tiles256 * 8 >= cus * 7) cfg = even_steps ? 14 : 9;
+  if (BITS == 4 && splits == 1 && N % 224 == 0 && (N / 224) * ceil_div(M, 256) * 8 >= cus * 7)
+    cfg = even_steps ? 15 : 10;
   if (const char* e = getenv("MLXQ_QMM_CFG")) cfg = atoi(e);
   switch (cfg) {
     case 1: return launch<BITS, GS, 256, 256, 2, 4>(x, M, wq, s, b, bias, N, K, y, part, splits, st);
@@ -336,6 +450,10 @@ int launch_cfg(const uint16_t* x, int M, const uint32_t* wq, const uint16_t* s, 
     case 4: return launch<BITS, GS, 256, 256, 4, 2>(x, M, wq, s, b, bias, N, K, y, part, splits, st);
     case 6: return launch<BITS, GS, 128, 128, 2, 2>(x, M, wq, s, b, bias, N, K, y, part, splits, st);
     case 7: return launch<BITS, GS, 256, 224, 4, 2, 16>(x, M, wq, s, b, bias, N, K, y, part, splits, st);
+    case 9: return launch<BITS, GS, 256, 256, 4, 2, 32, 1>(x, M, wq, s, b, bias, N, K, y, part, splits, st);
+    case 10: return launch<BITS, GS, 256, 224, 4, 2, 16, 1>(x, M, wq, s, b, bias, N, K, y, part, splits, st);
+    case 14: return launch<BITS, GS, 256, 256, 4, 2, 32, 9>(x, M, wq, s, b, bias, N, K, y, part, splits, st);
+    case 15: return launch<BITS, GS, 256, 224, 4, 2, 16, 9>(x, M, wq, s, b, bias, N, K, y, part, splits, st);
     default: return launch<BITS, GS, 128, 256, 2, 2>(x, M, wq, s, b, bias, N, K, y, part, splits, st);
   }
 }

@@ -113,12 +113,13 @@ def test_qmm_split_k(torch_gpu, monkeypatch, bits, gs, splits, n):
 
 
 @pytest.mark.parametrize("bits", [4, 8])
-@pytest.mark.parametrize("cfg", [4, 6, 7])
+@pytest.mark.parametrize("cfg", [4, 6, 7, 9, 10, 14, 15])
 @pytest.mark.parametrize("n", [448, 300])
 def test_qmm_tile_configs(torch_gpu, monkeypatch, bits, cfg, n):
     """Every qmm workgroup tile the dispatcher picks (256x256 / 128x128 in
-    32x32 MFMA tiles, 256x224 in 16x16 ones) with a bias, M and N not
-    multiples of the tile."""
+    32x32 MFMA tiles, 256x224 in 16x16 ones; plain, ping-pong and ping-pong
+    with the weights three steps ahead) with a bias, M and N not multiples
+    of the tile (K = 512: 8 K steps, the deep form's even count)."""
     monkeypatch.setenv("MLXQ_QMM_CFG", str(cfg))
     monkeypatch.setenv("MLXQ_QMM_SPLIT", "1")
     m, k = 300, 512
