@@ -156,6 +156,72 @@ int mlxq_qmatmul_fused(const void* x, int64_t M, int64_t K,
                        void* stream);
 
 /* ------------------------------------------------------------------ */
+/* Whole batch-1 decode step in one persistent launch                  */
+/* ------------------------------------------------------------------ */
+
+/* A quantized projection's packed weights (MLX affine layout). */
+typedef struct {
+  const uint32_t* wq;   /* [N, K*bits/32] */
+  const void* scales;   /* [N, K/group_size] bf16 */
+  const void* biases;   /* [N, K/group_size] bf16 */
+} mlxq_qweight;
+
+/* One Llama layer of the decode chain (src/models/llama.rs:689-735). */
+typedef struct {
+  mlxq_qweight q, k, v, o, gate, up, down;
+  const void* ln1;      /* [hidden] bf16, input_layernorm (llama.rs:698)          */
+  const void* ln2;      /* [hidden] bf16, post_attention_layernorm (llama.rs:728) */
+} mlxq_decode_layer;
+
+typedef struct {
+  int32_t layers, hidden, intermediate, heads, kv_heads, head_dim, vocab;
+  int32_t group_size, bits;
+  float eps;
+} mlxq_decode_config;
+
+/* Launch parameters filled by mlxq_decode_plan (host memory, caller-owned). */
+typedef struct {
+  void* workspace;
+  int32_t stages, grid, lds_bytes, max_k, hidden, vocab;
+} mlxq_decode_plan_t;
+
+/* Device workspace bytes for a plan: header, stage table and the per-layer
+ * activations (q, k, v, h, SwiGLU output, layer output). */
+int mlxq_decode_plan_size(const mlxq_decode_config* cfg, size_t* bytes);
+
+/* Replaces, for batch 1, the per-layer chain of CausalLm's decode forward
+ * (src/models/llama.rs:689-735: rms_norm -> q/k/v (:806-812) -> attention
+ * -> o (:829-835) + residual -> rms_norm -> gate/up -> silu*mul -> down
+ * (:1040-1045) + residual; final norm + lm_head :595-603) with attention
+ * taken as the identity on v repeated to the query heads (one cached
+ * position), every projection Q4 g64.  Uploads the stage table into the
+ * workspace (synchronous on `stream`; not for use under graph capture) and
+ * resets its barrier state.  The workspace must stay allocated and the weight
+ * pointers valid while the plan is used.  MLXQ_ERR_UNSUPPORTED: widths not a
+ * multiple of 512 (hidden, intermediate, heads*head_dim), bits != 4 or
+ * group_size != 64; callers then run the per-projection calls. */
+int mlxq_decode_plan(const mlxq_decode_config* cfg,
+                     const mlxq_decode_layer* layers, const void* final_norm,
+                     const mlxq_qweight* lm_head, void* workspace,
+                     size_t workspace_bytes, mlxq_decode_plan_t* plan,
+                     void* stream);
+
+/* One decode step: x [hidden] bf16 (16-byte aligned, read only) ->
+ * logits [vocab] bf16, as the chain of mlxq_rms_norm / mlxq_qmatmul /
+ * mlxq_repeat_kv / mlxq_add / mlxq_silu_mul up to f32 summation order.
+ * One launch with one workgroup per CU, all resident, synchronising through
+ * a grid barrier in the workspace; capturable in a HIP graph.  Calls on one
+ * plan must not overlap (they share its barrier and activations).  A barrier
+ * that waits longer than 0.5 s (workgroups not co-resident) ends the launch;
+ * mlxq_decode_status then reports it and the plan must be made again. */
+int mlxq_decode_step(const mlxq_decode_plan_t* plan, const void* x,
+                     void* logits, void* stream);
+
+/* *timed_out = 1 if a launch on this plan gave up at a grid barrier
+ * (synchronous read of the workspace header). */
+int mlxq_decode_status(const mlxq_decode_plan_t* plan, int* timed_out);
+
+/* ------------------------------------------------------------------ */
 /* Decode layer chain around the projections (bf16, MLX rounding points) */
 /* ------------------------------------------------------------------ */
 

@@ -54,6 +54,10 @@ SIGNATURES = {
     "mlxq_gguf_block": (ctypes.c_int, [_u32, ctypes.POINTER(_i64), ctypes.POINTER(_i64)]),
     "mlxq_gguf_tensor_byte_len": (ctypes.c_int, [_u32, _i64, ctypes.POINTER(_i64)]),
     "mlxq_gguf_dequantize": (ctypes.c_int, [_u32, _vp, _i64, _i64, ctypes.c_int, _vp, _vp]),
+    "mlxq_decode_plan_size": (ctypes.c_int, [_vp, ctypes.POINTER(_sz)]),
+    "mlxq_decode_plan": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _sz, _vp, _vp]),
+    "mlxq_decode_step": (ctypes.c_int, [_vp, _vp, _vp, _vp]),
+    "mlxq_decode_status": (ctypes.c_int, [_vp, ctypes.POINTER(ctypes.c_int)]),
 }
 
 
@@ -61,6 +65,28 @@ class Projection(ctypes.Structure):
     """mlxq_projection (include/mlxq.h)."""
     _fields_ = [("wq", _vp), ("scales", _vp), ("biases", _vp), ("bias", _vp), ("residual", _vp), ("y", _vp),
                 ("N", _i64)]
+
+
+class QWeight(ctypes.Structure):
+    """mlxq_qweight (include/mlxq.h)."""
+    _fields_ = [("wq", _vp), ("scales", _vp), ("biases", _vp)]
+
+
+class DecodeLayer(ctypes.Structure):
+    """mlxq_decode_layer (include/mlxq.h)."""
+    _fields_ = [(n, QWeight) for n in ("q", "k", "v", "o", "gate", "up", "down")] + [("ln1", _vp), ("ln2", _vp)]
+
+
+class DecodeConfig(ctypes.Structure):
+    """mlxq_decode_config (include/mlxq.h)."""
+    _fields_ = [(n, ctypes.c_int32) for n in ("layers", "hidden", "intermediate", "heads", "kv_heads", "head_dim",
+                                              "vocab", "group_size", "bits")] + [("eps", ctypes.c_float)]
+
+
+class DecodePlanT(ctypes.Structure):
+    """mlxq_decode_plan_t (include/mlxq.h)."""
+    _fields_ = [("workspace", _vp)] + [(n, ctypes.c_int32) for n in ("stages", "grid", "lds_bytes", "max_k",
+                                                                      "hidden", "vocab")]
 
 
 class MlxqError(RuntimeError):
@@ -314,3 +340,40 @@ def gguf_requantize(tag: int, data, rows: int, cols: int, permute_heads: int = 0
     check(lib().mlxq_gguf_requantize(tag, _ptr(data), data.numel(), rows, cols, permute_heads, group_size, bits,
                                      _ptr(wq), _ptr(s), _ptr(b), _stream()))
     return wq, s, b
+
+
+class DecodePlan:
+    """A persistent batch-1 decode step over a stack's quantized weights
+    (mlxq_decode_plan / mlxq_decode_step).  cfg: dict with layers, hidden,
+    intermediate, heads, kv_heads, head_dim, vocab, group_size, bits, eps;
+    layers: list of dicts {q,k,v,o,gate,up,down: (wq, scales, biases),
+    ln1, ln2}; lm_head: (wq, scales, biases).  Raises Unsupported for widths
+    the persistent kernel does not cover.  The plan keeps its workspace and
+    the tensors it points at alive."""
+
+    def __init__(self, cfg: dict, layers, final_norm, lm_head, device):
+        torch = _torch()
+        self.cfg = DecodeConfig(**{k: cfg[k] for k, _ in DecodeConfig._fields_})
+        size = ctypes.c_size_t(0)
+        check(lib().mlxq_decode_plan_size(ctypes.byref(self.cfg), ctypes.byref(size)))
+        self.workspace = torch.zeros(size.value, dtype=torch.uint8, device=device)
+        qw = lambda t: QWeight(_ptr(t[0]), _ptr(t[1]), _ptr(t[2]))  # noqa: E731
+        arr = (DecodeLayer * len(layers))()
+        for i, L in enumerate(layers):
+            arr[i] = DecodeLayer(*(qw(L[p]) for p in ("q", "k", "v", "o", "gate", "up", "down")), _ptr(L["ln1"]),
+                                 _ptr(L["ln2"]))
+        self._keep = (layers, final_norm, lm_head)
+        self._lm = qw(lm_head)
+        self.plan = DecodePlanT()
+        check(lib().mlxq_decode_plan(ctypes.byref(self.cfg), arr, _ptr(final_norm), ctypes.byref(self._lm),
+                                     _ptr(self.workspace), size.value, ctypes.byref(self.plan), _stream()))
+
+    def step(self, x, logits):
+        """One decode step on the current stream: x [hidden] bf16 -> logits [vocab] bf16."""
+        check(lib().mlxq_decode_step(ctypes.byref(self.plan), _ptr(x), _ptr(logits), _stream()))
+        return logits
+
+    def timed_out(self) -> bool:
+        r = ctypes.c_int(0)
+        check(lib().mlxq_decode_status(ctypes.byref(self.plan), ctypes.byref(r)))
+        return bool(r.value)

@@ -56,3 +56,57 @@ def test_llama3_8b_width_two_layers(torch_gpu, batch):
     got, want = _run(StackConfig(layers=2), batch, graph=True)
     print("rel_err", rel_err(orc.bf16_to_f32(got), orc.bf16_to_f32(want).astype(np.float64)))
     assert rel_err(orc.bf16_to_f32(got), orc.bf16_to_f32(want).astype(np.float64)) <= TOL
+
+
+# ---- persistent single-launch decode step (mlxq_decode_plan / mlxq_decode_step)
+
+def _persistent(cfg: StackConfig, seeds, graph: bool):
+    """Logits of the persistent step and of the oracle chain for each input
+    seed, on one plan (and one graph when graph=True): later calls must see
+    the new input, not activations left by an earlier call."""
+    st = DecodeStack(cfg, batch=1, seed=11, norm_noise=0.1)
+    layers, norm, lm = st.host_weights()
+    g = None
+    out = []
+    for sd in seeds:
+        x = orc.f32_to_bf16(orc.normal(sd, cfg.hidden, 0.0, 1.0)).reshape(1, cfg.hidden)
+        st.x.copy_(dev(x, True))
+        if graph:
+            if g is None:
+                g = st.capture(1, persistent=True)
+            g.replay()
+        else:
+            st.forward(1, persistent=True)
+        got = host(st.logits).copy()
+        want = orc.decode_stack(x, layers, norm, lm, cfg.as_dict())
+        out.append((got, want))
+    assert not st.persistent_plan().timed_out()
+    return st, out
+
+
+@pytest.mark.parametrize("graph", [False, True])
+def test_persistent_small(torch_gpu, graph):
+    _, res = _persistent(StackConfig(**SMALL), [501, 502, 503], graph)
+    for got, want in res:
+        assert rel_err(orc.bf16_to_f32(got), orc.bf16_to_f32(want).astype(np.float64)) <= TOL
+
+
+def test_persistent_llama3_8b_width_two_layers(torch_gpu):
+    """Config-5 widths, two layers, three inputs through one captured graph;
+    also against the fused multi-launch chain on the same weights."""
+    st, res = _persistent(StackConfig(layers=2), [601, 602, 603], graph=True)
+    for got, want in res:
+        e = rel_err(orc.bf16_to_f32(got), orc.bf16_to_f32(want).astype(np.float64))
+        print("rel_err", e)
+        assert e <= TOL
+    pers = orc.bf16_to_f32(res[-1][0]).astype(np.float64)
+    st.forward(1, fused=True)
+    fused = orc.bf16_to_f32(host(st.logits))
+    assert rel_err(pers, fused.astype(np.float64)) <= TOL
+
+
+def test_persistent_unsupported(torch_gpu):
+    import mlxq
+    st = DecodeStack(StackConfig(bits=8, **SMALL), batch=1, seed=3)
+    with pytest.raises(mlxq.Unsupported):
+        st.persistent_plan()
