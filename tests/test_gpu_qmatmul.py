@@ -285,3 +285,39 @@ def test_decode_kernels_forced(torch_gpu, monkeypatch, bits, m, kernel):
     wq, s, b = make_layer(30 + bits + m, n, k, 64, bits)
     x = bf16_acts(31 + m, m, k)
     assert rel_err(run(x, wq, s, b, 64, bits), orc.qmatmul_f64(x, wq, s, b, 64, bits)) <= TIGHT
+
+
+ROW_K = {4: [2048, 4096, 8192], 8: [1024, 2048, 4096, 7168, 8192, 14336, 16384]}
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+@pytest.mark.parametrize("geom", ["auto", "1,4", "2,4", "4,4", "1,8", "1,16"])
+def test_qmv_row_batch1(torch_gpu, monkeypatch, bits, gs, geom):
+    """Batch-1 whole-row kernel (qmv_row.hip) at every row length it is
+    built for (1..16 KB of codes), every forced (rows per wave, waves per
+    workgroup), group sizes 32/64/128, N not a multiple of the rows per
+    workgroup (203) and smaller than one workgroup (8), with a bias vector."""
+    if geom != "auto":
+        r, w = geom.split(",")
+        monkeypatch.setenv("MLXQ_QMV_ROW_R", r)
+        monkeypatch.setenv("MLXQ_QMV_ROW_W", w)
+    for k in ROW_K[bits]:
+        for n in (203, 8):
+            wq, s, b = make_layer(0x60 + bits + gs + k + n, n, k, gs, bits)
+            x = bf16_acts(0x61 + k, 1, k)
+            bias = orc.f32_to_bf16(np.linspace(-1, 1, n, dtype=np.float32))
+            ref = orc.qmatmul_f64(x, wq, s, b, gs, bits) + orc.bf16_to_f32(bias).astype(np.float64)
+            y = run(x, wq, s, b, gs, bits, bias=bias)
+            assert rel_err(y, ref) <= TIGHT, (k, n)
+
+
+def test_qmv_row_skipped_kernel_agrees(torch_gpu, monkeypatch):
+    """MLXQ_QMV_NO_ROW=1 (the previous batch-1 kernel) and the row kernel
+    agree to bf16 rounding on a Llama shape."""
+    wq, s, b = make_layer(0x62, 4096, 4096, 64, 4)
+    x = bf16_acts(0x63, 1, 4096)
+    a = run(x, wq, s, b, 64, 4)
+    monkeypatch.setenv("MLXQ_QMV_NO_ROW", "1")
+    c = run(x, wq, s, b, 64, 4)
+    assert rel_err(a, c.astype(np.float64)) <= TIGHT
