@@ -77,11 +77,14 @@ extern "C" int mlxq_qmatmul_algo(const void* x, int64_t M, const uint32_t* wq, c
   // tile kernel where qmv_tile_preferred says, the block kernel otherwise.
   // MLXQ_QMV_MFMA=1 never takes the vector-ALU kernel, MLXQ_QMV_DOT_ALL=1
   // takes it for every eligible M <= 4.
-  // batch 1: whole rows per wave (qmv_row.hip) where K*bits/8 is a whole
-  // number of 1 KB load instructions; MLXQ_QMV_NO_ROW=1 skips it
-  if (M == 1 && qmv_row_eligible(M, N, K, group_size, bits) && !getenv("MLXQ_QMV_NO_ROW") &&
-      !getenv("MLXQ_QMV_MFMA"))
-    return launch_qmv_row(xp, wq, sp, bp, bias, N, K, group_size, bits, yp, st);
+  // whole rows per wave (qmv_row.hip) where K*bits/8 is a whole number of
+  // 1 KB load instructions: at M = 1, and at M = 2..4 for short matrices (N
+  // <= 2048: k/v 6.1 -> 5.6 us Q4, 6.9 -> 5.1 Q8 at M = 4; on taller ones
+  // its per-row decode and LDS reads make it slower than the kernels below).
+  // MLXQ_QMV_NO_ROW=1 skips it, MLXQ_QMV_ROW_ALL=1 takes it for every M <= 4.
+  if (qmv_row_eligible(M, N, K, group_size, bits) && (M == 1 || N <= 2048 || getenv("MLXQ_QMV_ROW_ALL")) &&
+      !getenv("MLXQ_QMV_NO_ROW") && !getenv("MLXQ_QMV_MFMA"))
+    return launch_qmv_row(xp, M, wq, sp, bp, bias, N, K, group_size, bits, yp, st);
   if (M <= kQmvDotMaxM && qmv_dot_eligible(M, N, K, group_size, bits) && !getenv("MLXQ_QMV_MFMA") &&
       (qmv_dot_preferred(M, N, K, bits) || getenv("MLXQ_QMV_DOT_ALL")))
     return launch_qmv_dot(xp, M, wq, sp, bp, bias, N, K, group_size, bits, yp, st);

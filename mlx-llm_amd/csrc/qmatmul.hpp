@@ -25,9 +25,9 @@ int launch_qmv(const QmvPlan& p, const uint16_t* x, int64_t M, const uint32_t* w
                const uint16_t* b, const uint16_t* bias, int64_t N, int64_t K, int group_size, int bits, uint16_t* y,
                hipStream_t st);
 
-// qmv_row: batch-1 GEMV, whole rows per wave, 1 KB loads (qmv_row.hip).
+// qmv_row: decode GEMV (M <= 4), whole rows per wave, 1 KB loads (qmv_row.hip).
 bool qmv_row_eligible(int64_t M, int64_t N, int64_t K, int group_size, int bits);
-int launch_qmv_row(const uint16_t* x, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
+int launch_qmv_row(const uint16_t* x, int64_t M, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
                    const uint16_t* bias, int64_t N, int64_t K, int group_size, int bits, uint16_t* y,
                    hipStream_t st);
 

@@ -47,8 +47,10 @@ __device__ __forceinline__ void decode_q8(uint32_t q, uint32_t& b0, uint32_t& b1
   b1 = __builtin_amdgcn_perm(__float_as_uint(f3), __float_as_uint(f2), 0x07060302u);
 }
 
-// BITS: 4 or 8; NI: 1 KB load instructions per row; R: rows per wave; W: waves per workgroup
-template <int BITS, int NI, int R, int W>
+// BITS: 4 or 8; NI: 1 KB load instructions per row; R: rows per wave; W:
+// waves per workgroup; MM: activation rows (1..4; each code is decoded once
+// and dotted with every activation row)
+template <int BITS, int NI, int R, int W, int MM = 1>
 __global__ __launch_bounds__(64 * W) void qmv_row_kernel(const uint16_t* __restrict__ x,
                                                          const uint32_t* __restrict__ wq,
                                                          const uint16_t* __restrict__ sc,
@@ -59,11 +61,11 @@ __global__ __launch_bounds__(64 * W) void qmv_row_kernel(const uint16_t* __restr
   constexpr int K = NI * 8192 / BITS;   // elements per row
   constexpr int CPL = 128 / BITS;       // codes per lane per load (one chunk)
   constexpr int NP = K / 8;             // 16-byte pieces of x
-  constexpr int XPT = (NP + T - 1) / T; // pieces per thread
+  constexpr int XPT = (MM * NP + T - 1) / T; // pieces per thread (all activation rows)
   constexpr float OFF = BITS == 4 ? 128.f : 0.f;
   static_assert(NP % 4 == 0, "whole chunks of x");
-  __shared__ uint4 xp[NP];
-  __shared__ float xs[K / CPL];
+  __shared__ uint4 xp[MM * NP];
+  __shared__ float xs[MM * (K / CPL)];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -75,7 +77,7 @@ __global__ __launch_bounds__(64 * W) void qmv_row_kernel(const uint16_t* __restr
 #pragma unroll
   for (int i = 0; i < XPT; i++) {
     const int q = tid + i * T;
-    xv[i] = q < NP ? reinterpret_cast<const uint4*>(x)[q] : make_uint4(0, 0, 0, 0);
+    xv[i] = q < MM * NP ? reinterpret_cast<const uint4*>(x)[q] : make_uint4(0, 0, 0, 0);
   }
   // 2. the wave's rows: codes (1 KB per instruction), then the lanes' scale/bias
   uint4 cw[R][NI];
@@ -101,7 +103,7 @@ __global__ __launch_bounds__(64 * W) void qmv_row_kernel(const uint16_t* __restr
 #pragma unroll
   for (int i = 0; i < XPT; i++) {
     const int q = tid + i * T;
-    if (i * T + T > NP && q >= NP) continue;  // whole 4-lane groups drop out together (NP % 4 == 0)
+    if (i * T + T > MM * NP && q >= MM * NP) continue;  // whole 4-lane groups drop out together (NP % 4 == 0)
     const uint32_t a[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
     float f[8];
 #pragma unroll
@@ -127,72 +129,75 @@ __global__ __launch_bounds__(64 * W) void qmv_row_kernel(const uint16_t* __restr
   __syncthreads();
 
   // 4. dot products: chunk ch = t*64 + lane of every row shares its x
-  float acc[R];
+  float acc[R][MM];
 #pragma unroll
-  for (int r = 0; r < R; r++) acc[r] = 0.f;
+  for (int r = 0; r < R; r++)
+#pragma unroll
+    for (int m = 0; m < MM; m++) acc[r][m] = 0.f;
 #pragma unroll
   for (int t = 0; t < NI; t++) {
     const int ch = t * 64 + lane;
-    const float xsum = xs[ch];
-    if (BITS == 4) {
-      const uint4* xq = xp + ch * 4;
-      uint4 X[4];
 #pragma unroll
-      for (int k = 0; k < 4; k++) X[k] = xq[k];
+    for (int r = 0; r < R; r++) {
+      const uint32_t wd[4] = {cw[r][t].x, cw[r][t].y, cw[r][t].z, cw[r][t].w};
+      uint32_t p[8];  // decoded bf16 pairs of the 16 bytes
 #pragma unroll
-      for (int r = 0; r < R; r++) {
-        const uint32_t wd[4] = {cw[r][t].x, cw[r][t].y, cw[r][t].z, cw[r][t].w};
-        float d = 0.f;
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-          const uint32_t w = wd[k];
-          d = dot2((w & 0x000F000Fu) | 0x43004300u, X[k].x, d);
-          d = dot2(((w >> 4) & 0x000F000Fu) | 0x43004300u, X[k].y, d);
-          d = dot2(((w >> 8) & 0x000F000Fu) | 0x43004300u, X[k].z, d);
-          d = dot2(((w >> 12) & 0x000F000Fu) | 0x43004300u, X[k].w, d);
+      for (int k = 0; k < 4; k++) {
+        if (BITS == 4) {
+          p[2 * k] = wd[k];  // decoded per use below (one and-or each)
+        } else {
+          decode_q8(wd[k], p[2 * k], p[2 * k + 1]);
         }
-        const float s = bf16_bits_to_f32(sv[r][t]), b = bf16_bits_to_f32(bv[r][t]);
-        acc[r] += s * d + (b - OFF * s) * xsum;
       }
-    } else {
-      const uint4* xq = xp + ch * 2;
-      const uint4 X0 = xq[0], X1 = xq[1];
-      const uint32_t xd[8] = {X0.x, X0.y, X0.z, X0.w, X1.x, X1.y, X1.z, X1.w};
+      const float s = bf16_bits_to_f32(sv[r][t]), b = bf16_bits_to_f32(bv[r][t]);
 #pragma unroll
-      for (int r = 0; r < R; r++) {
-        const uint32_t wd[4] = {cw[r][t].x, cw[r][t].y, cw[r][t].z, cw[r][t].w};
+      for (int m = 0; m < MM; m++) {
+        const float xsum = xs[m * (K / CPL) + ch];
         float d = 0.f;
+        if (BITS == 4) {
+          const uint4* xq = xp + m * NP + ch * 4;
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-          uint32_t p0, p1;
-          decode_q8(wd[k], p0, p1);
-          d = dot2(p0, xd[2 * k], d);
-          d = dot2(p1, xd[2 * k + 1], d);
+          for (int k = 0; k < 4; k++) {
+            const uint4 X = xq[k];
+            const uint32_t w = p[2 * k];
+            d = dot2((w & 0x000F000Fu) | 0x43004300u, X.x, d);
+            d = dot2(((w >> 4) & 0x000F000Fu) | 0x43004300u, X.y, d);
+            d = dot2(((w >> 8) & 0x000F000Fu) | 0x43004300u, X.z, d);
+            d = dot2(((w >> 12) & 0x000F000Fu) | 0x43004300u, X.w, d);
+          }
+        } else {
+          const uint4* xq = xp + m * NP + ch * 2;
+          const uint4 X0 = xq[0], X1 = xq[1];
+          const uint32_t xd[8] = {X0.x, X0.y, X0.z, X0.w, X1.x, X1.y, X1.z, X1.w};
+#pragma unroll
+          for (int k = 0; k < 8; k++) d = dot2(p[k], xd[k], d);
         }
-        const float s = bf16_bits_to_f32(sv[r][t]), b = bf16_bits_to_f32(bv[r][t]);
-        acc[r] += s * d + b * xsum;
+        acc[r][m] += s * d + (b - OFF * s) * xsum;
       }
     }
   }
   // 5. row sums across the 64 lanes
 #pragma unroll
   for (int r = 0; r < R; r++) {
-    float v = acc[r];
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
-    const int n = row0 + r;
-    if (lane == 0 && n < N) {
-      if (bias) v += bf16_bits_to_f32(bias[n]);
-      y[n] = static_cast<uint16_t>(f32_to_bf16_bits(v));
+    for (int m = 0; m < MM; m++) {
+      float v = acc[r][m];
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+      const int n = row0 + r;
+      if (lane == 0 && n < N) {
+        if (bias) v += bf16_bits_to_f32(bias[n]);
+        y[static_cast<int64_t>(m) * N + n] = static_cast<uint16_t>(f32_to_bf16_bits(v));
+      }
     }
   }
 }
 
-template <int BITS, int NI, int R, int W>
+template <int BITS, int NI, int R, int W, int MM = 1>
 int launch_rw(const uint16_t* x, const uint32_t* wq, const uint16_t* s, const uint16_t* b, const uint16_t* bias,
               int64_t N, int gs, uint16_t* y, hipStream_t st) {
   const unsigned grid = static_cast<unsigned>((N + R * W - 1) / (R * W));
-  hipLaunchKernelGGL((qmv_row_kernel<BITS, NI, R, W>), dim3(grid), dim3(64 * W), 0, st, x, wq, s, b, bias, y,
+  hipLaunchKernelGGL((qmv_row_kernel<BITS, NI, R, W, MM>), dim3(grid), dim3(64 * W), 0, st, x, wq, s, b, bias, y,
                      static_cast<int>(N), gs);
   return check_launch("qmv_row");
 }
@@ -201,8 +206,14 @@ int launch_rw(const uint16_t* x, const uint32_t* wq, const uint16_t* s, const ui
 // rows take several rows per wave, long rows one (registers), with more
 // waves per workgroup to share the activation staging.
 template <int BITS, int NI>
-int launch_ni(const uint16_t* x, const uint32_t* wq, const uint16_t* s, const uint16_t* b, const uint16_t* bias,
-              int64_t N, int gs, uint16_t* y, int R, int W, hipStream_t st) {
+int launch_ni(const uint16_t* x, int64_t M, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
+              const uint16_t* bias, int64_t N, int gs, uint16_t* y, int R, int W, hipStream_t st) {
+  if constexpr (NI * 8192 / BITS <= 4096) {  // several activation rows: K <= 4096 (LDS)
+    if (M == 2) return launch_rw<BITS, NI, 1, 4, 2>(x, wq, s, b, bias, N, gs, y, st);
+    if (M == 3) return launch_rw<BITS, NI, 1, 4, 3>(x, wq, s, b, bias, N, gs, y, st);
+    if (M == 4) return launch_rw<BITS, NI, 1, 4, 4>(x, wq, s, b, bias, N, gs, y, st);
+  }
+  if (M != 1) return fail(MLXQ_ERR_UNSUPPORTED, "qmv_row: M > 1 needs K <= 4096");
   if constexpr (NI <= 2) {
     if (R >= 4) return launch_rw<BITS, NI, 4, 4>(x, wq, s, b, bias, N, gs, y, st);
     if (R == 2) return launch_rw<BITS, NI, 2, 4>(x, wq, s, b, bias, N, gs, y, st);
@@ -220,7 +231,8 @@ int launch_ni(const uint16_t* x, const uint32_t* wq, const uint16_t* s, const ui
 }  // namespace row
 
 bool qmv_row_eligible(int64_t M, int64_t N, int64_t K, int group_size, int bits) {
-  if (M != 1 || N < 1 || (bits != 4 && bits != 8) || group_size < 128 / bits) return false;
+  if (M < 1 || M > 4 || N < 1 || (bits != 4 && bits != 8) || group_size < 128 / bits) return false;
+  if (M > 1 && K > 4096) return false;  // the activation rows share the workgroup's LDS
   if ((K * bits / 8) % 1024) return false;
   const int64_t ni = K * bits / 8 / 1024;
   // Q4 with 7 KB rows (the down projection, K = 14336) measured faster on
@@ -240,7 +252,7 @@ void qmv_row_geometry(int64_t N, int64_t K, int bits, int& R, int& W) {
   if (const char* e = getenv("MLXQ_QMV_ROW_W")) W = atoi(e);
 }
 
-int launch_qmv_row(const uint16_t* x, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
+int launch_qmv_row(const uint16_t* x, int64_t M, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
                    const uint16_t* bias, int64_t N, int64_t K, int group_size, int bits, uint16_t* y,
                    hipStream_t st) {
   using namespace row;
@@ -249,8 +261,8 @@ int launch_qmv_row(const uint16_t* x, const uint32_t* wq, const uint16_t* s, con
   const int64_t ni = K * bits / 8 / 1024;
 #define MLXQ_ROW_CASE(NIV)                                                                       \
   case NIV:                                                                                      \
-    return bits == 4 ? launch_ni<4, NIV>(x, wq, s, b, bias, N, group_size, y, R, W, st)             \
-                     : launch_ni<8, NIV>(x, wq, s, b, bias, N, group_size, y, R, W, st);
+    return bits == 4 ? launch_ni<4, NIV>(x, M, wq, s, b, bias, N, group_size, y, R, W, st)             \
+                     : launch_ni<8, NIV>(x, M, wq, s, b, bias, N, group_size, y, R, W, st);
   switch (ni) {
     MLXQ_ROW_CASE(1)
     MLXQ_ROW_CASE(2)

@@ -321,3 +321,18 @@ def test_qmv_row_skipped_kernel_agrees(torch_gpu, monkeypatch):
     monkeypatch.setenv("MLXQ_QMV_NO_ROW", "1")
     c = run(x, wq, s, b, 64, 4)
     assert rel_err(a, c.astype(np.float64)) <= TIGHT
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("m", [2, 3, 4])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+def test_qmv_row_several_rows(torch_gpu, monkeypatch, bits, m, gs):
+    """The whole-row kernel with 2..4 activation rows (K <= 4096), forced on
+    a tall ragged matrix and taken by default on a short one, with a bias."""
+    monkeypatch.setenv("MLXQ_QMV_ROW_ALL", "1")
+    for n, k in ((203, 4096), (1024, 2048), (8, 1024 * 8 // bits)):
+        wq, s, b = make_layer(0x70 + bits + m + gs + n, n, k, gs, bits)
+        x = bf16_acts(0x71 + m, m, k)
+        bias = orc.f32_to_bf16(np.linspace(-1, 1, n, dtype=np.float32))
+        ref = orc.qmatmul_f64(x, wq, s, b, gs, bits) + orc.bf16_to_f32(bias).astype(np.float64)[None, :]
+        assert rel_err(run(x, wq, s, b, gs, bits, bias=bias), ref) <= TIGHT, (n, k)
