@@ -225,7 +225,7 @@ def main(argv=None) -> int:
     if dot_preferred(dm, dn, dk, dbits):
         kname = "qmv_dot_kernel (vector ALU)"
     elif tile_preferred(dm, dn, dk, dbits):
-        kname = "qmv_tile_kernel + qmv_tile_reduce_kernel (MFMA, split K; one call = both launches)"
+        kname = "qmv_tile_kernel + split_reduce4_kernel (MFMA, split K; one call = both launches)"
     else:
         kname = "qmv_kernel (MFMA)"
     # HBM bytes per call (both kernels) from rocprofv3 FETCH_SIZE / WRITE_SIZE
