@@ -183,6 +183,8 @@ typedef struct {
 typedef struct {
   void* workspace;
   int32_t stages, grid, lds_bytes, max_k, hidden, vocab;
+  int32_t trace;  /* nonzero: the launch records per-stage wall-clock stamps
+                     in the workspace (set from MLXQ_DECODE_TRACE at plan time) */
 } mlxq_decode_plan_t;
 
 /* Device workspace bytes for a plan: header, stage table and the per-layer

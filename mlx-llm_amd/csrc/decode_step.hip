@@ -43,6 +43,7 @@
 
 #include <algorithm>
 #include <cstddef>
+#include <cstdlib>
 #include <string>
 #include <vector>
 
@@ -181,7 +182,7 @@ template <int D>
 __global__ __launch_bounds__(kThreads, 1) void decode_step_kernel(const DStage* st_g, int NS,
                                                                   const uint16_t* __restrict__ x_arg,
                                                                   uint16_t* __restrict__ logits, DHeader* hdr,
-                                                                  int max_kin, int max_k, int hidden) {
+                                                                  int max_kin, int max_k, int hidden, int trace_on) {
   extern __shared__ __align__(16) unsigned char smem[];
   const Lds L = lds_layout(max_kin, max_k, hidden, NS);
   uint16_t* raw = reinterpret_cast<uint16_t*>(smem + L.raw);
@@ -209,7 +210,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_step_kernel(const DStage* 
     // ------------------------------ stager ------------------------------
     unsigned long long* trace = reinterpret_cast<unsigned long long*>(hdr + 1);
     auto stamp = [&](int s, int k) {
-      if (lane == 0 && g < kTraceWgs) trace[(static_cast<size_t>(s) * kTraceWgs + g) * 4 + k] = wall_clock64();
+      if (trace_on && lane == 0 && g < kTraceWgs) trace[(static_cast<size_t>(s) * kTraceWgs + g) * 4 + k] = wall_clock64();
     };
     for (int s = 0; s < NS; s++) {
       const int kind = st[s].kind, flags = st[s].flags;
@@ -510,9 +511,10 @@ __global__ __launch_bounds__(kThreads, 1) void decode_step_kernel(const DStage* 
   }
 }
 
-// Trace for profiling: every workgroup's stager records 4 wall-clock stamps
-// per stage (barrier arrival, barrier passed, input staged, last output
-// stored), [stage][workgroup][4] for up to kTraceWgs workgroups.
+// Trace for profiling (plans made with MLXQ_DECODE_TRACE set): every
+// workgroup's stager records 4 wall-clock stamps per stage (barrier arrival,
+// barrier passed, input staged, last output stored), [stage][workgroup][4]
+// for up to kTraceWgs workgroups, after the header.
 size_t trace_bytes(int ns) { return static_cast<size_t>(ns) * kTraceWgs * 4 * 8; }
 
 const DStage* stage_table(void* ws, int ns) {
@@ -747,6 +749,7 @@ extern "C" int mlxq_decode_plan(const mlxq_decode_config* cfg, const mlxq_decode
   plan->max_k = max_k;
   plan->hidden = static_cast<int32_t>(d.hidden);
   plan->vocab = static_cast<int32_t>(d.vocab);
+  plan->trace = getenv("MLXQ_DECODE_TRACE") ? 1 : 0;
   return MLXQ_OK;
 }
 
@@ -758,7 +761,7 @@ extern "C" int mlxq_decode_step(const mlxq_decode_plan_t* plan, const void* x, v
   hipLaunchKernelGGL(kern, dim3(plan->grid), dim3(kThreads), plan->lds_bytes,
                      as_stream(stream), stage_table(plan->workspace, plan->stages), plan->stages, static_cast<const uint16_t*>(x),
                      static_cast<uint16_t*>(logits), static_cast<DHeader*>(plan->workspace), plan->max_k,
-                     plan->max_k, plan->hidden);
+                     plan->max_k, plan->hidden, plan->trace);
   return check_launch("decode_step");
 }
 

@@ -21,7 +21,8 @@
 //    v_dot2_f32_bf16 accumulates; per chunk y += s*dot + (b - OFF*s)*sum(x)
 //    (OFF = 128 for Q4, 0 for Q8), in f32.  One chunk never straddles a
 //    group (group sizes 32/64/128 >= chunk).
-//  * The 64 lanes of a row reduce with cross-lane adds; y = bf16(acc (+ bias)).
+//  * The 64 lanes of a row reduce with DPP adds and the gfx950 row swaps;
+//    y = bf16(acc (+ bias)).
 #include <hip/hip_runtime.h>
 
 #include <cstdlib>
@@ -37,6 +38,26 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
+}
+
+// Cross-lane adds on the VALU: DPP within rows of 16 lanes, then the row
+// swaps of gfx950 across rows (no LDS crossbar traffic).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+constexpr int kQuadXor1 = 0xB1, kQuadXor2 = 0x4E, kRowHalfMirror = 0x141, kRowMirror = 0x140;
+
+// sum over the wave, every lane gets it
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp<kQuadXor1>(v);
+  v += dpp<kQuadXor2>(v);
+  v += dpp<kRowHalfMirror>(v);  // lane i <-> 7-i: the other quad of the 8
+  v += dpp<kRowMirror>(v);      // lane i <-> 15-i: the other 8 of the row
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);  // rows 0+1, 2+3
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);  // halves
 }
 
 // Q8: 4 codes of one dword -> bf16 pairs (q0,q1), (q2,q3), exact through f32
@@ -118,9 +139,9 @@ __global__ __launch_bounds__(64 * W) void qmv_row_kernel(const uint16_t* __restr
       xp[q] = xv[i];
     }
     float sum = ((f[0] + f[1]) + (f[2] + f[3])) + ((f[4] + f[5]) + (f[6] + f[7]));
-    sum += __shfl_xor(sum, 1);  // Q8 chunk: 2 pieces
+    sum += dpp<kQuadXor1>(sum);  // Q8 chunk: 2 pieces
     if (BITS == 4) {
-      sum += __shfl_xor(sum, 2);  // Q4 chunk: 4 pieces
+      sum += dpp<kQuadXor2>(sum);  // Q4 chunk: 4 pieces
       if ((lane & 3) == 0) xs[q >> 2] = sum;
     } else {
       if ((lane & 1) == 0) xs[q >> 1] = sum;
@@ -181,9 +202,7 @@ __global__ __launch_bounds__(64 * W) void qmv_row_kernel(const uint16_t* __restr
   for (int r = 0; r < R; r++) {
 #pragma unroll
     for (int m = 0; m < MM; m++) {
-      float v = acc[r][m];
-#pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+      float v = wave_sum(acc[r][m]);
       const int n = row0 + r;
       if (lane == 0 && n < N) {
         if (bias) v += bf16_bits_to_f32(bias[n]);
