@@ -49,4 +49,31 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
 
 __host__ __device__ __forceinline__ int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// ---- cross-lane adds on the VALU (no LDS crossbar): DPP within rows of 16
+// lanes, the gfx950 row swaps across rows ----
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppQuadXor1 = 0xB1, kDppQuadXor2 = 0x4E, kDppRowHalfMirror = 0x141, kDppRowMirror = 0x140;
+
+// v + v of lane ^ 16 (rows 0+1, 2+3 of 16 lanes)
+__device__ __forceinline__ float add_xor16(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(a[0]) + __uint_as_float(a[1]);
+}
+// v + v of lane ^ 32 (the two halves of the wave)
+__device__ __forceinline__ float add_xor32(float v) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(a[0]) + __uint_as_float(a[1]);
+}
+// sum over the 64 lanes, every lane gets it
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp_f32<kDppQuadXor1>(v);
+  v += dpp_f32<kDppQuadXor2>(v);
+  v += dpp_f32<kDppRowHalfMirror>(v);  // lane i <-> 7-i: the other quad of the 8
+  v += dpp_f32<kDppRowMirror>(v);      // lane i <-> 15-i: the other 8 of the row
+  return add_xor32(add_xor16(v));
+}
+
 }  // namespace mlxq

@@ -308,8 +308,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_step_kernel(const DStage* 
             ss += hi * hi;
           }
         }
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+        ss = wave_sum(ss);
         if (lane == 0) norm_inv = 1.0f / sqrtf(ss / static_cast<float>(K) + st[s].eps);
       }
       __syncthreads();  // B1a: raw input, norm statistic and residuals in LDS
@@ -460,8 +459,8 @@ __global__ __launch_bounds__(kThreads, 1) void decode_step_kernel(const DStage* 
         for (int e = 0; e < 8; e++) h[e] = f32_to_bf16_bits(f[e]);
         xp[j] = make_uint4(h[0] | (h[4] << 16), h[1] | (h[5] << 16), h[2] | (h[6] << 16), h[3] | (h[7] << 16));
         float sum = ((f[0] + f[1]) + (f[2] + f[3])) + ((f[4] + f[5]) + (f[6] + f[7]));
-        sum += __shfl_xor(sum, 1);
-        sum += __shfl_xor(sum, 2);
+        sum += dpp_f32<kDppQuadXor1>(sum);
+        sum += dpp_f32<kDppQuadXor2>(sum);
         if ((lane & 3) == 0) xs[j >> 2] = sum;
       }
       __syncthreads();  // B1b
@@ -491,9 +490,9 @@ __global__ __launch_bounds__(kThreads, 1) void decode_step_kernel(const DStage* 
         const float sc = bf16_bits_to_f32(rs[j]), bi = bf16_bits_to_f32(rb[j]);
         acc += sc * d + (bi - 128.f * sc) * xsum;
         if (++ci == cRT) {
-          acc += __shfl_xor(acc, 1);
-          acc += __shfl_xor(acc, 2);
-          acc += __shfl_xor(acc, 4);
+          acc += dpp_f32<kDppQuadXor1>(acc);  // the 8 lanes of a row: quads, then the other quad
+          acc += dpp_f32<kDppQuadXor2>(acc);
+          acc += dpp_f32<kDppRowHalfMirror>(acc);
           if (c == 0) red[(par * kWaves + wv) * 8 + (lane >> 3)] = acc;
           __syncthreads();  // B2
           acc = 0.f;

@@ -46,8 +46,7 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const uint16_t* 
       ss = fmaf(q, q, ss);
     }
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+  ss = wave_sum(ss);
   if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
   __syncthreads();
   float tot = 0.f;

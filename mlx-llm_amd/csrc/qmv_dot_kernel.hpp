@@ -296,8 +296,7 @@ __global__ __launch_bounds__(64 * WV) void qmv_dot_kernel(const Params p) {
     }
 #pragma unroll
     for (int m = 0; m < MV; m++) {
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) ss[m] += __shfl_xor(ss[m], o, 64);
+      ss[m] = wave_sum(ss[m]);
       if (lane == 0) ssq[wave * MV + m] = ss[m];
     }
     __syncthreads();
@@ -466,8 +465,7 @@ __global__ __launch_bounds__(64 * WV) void qmv_dot_kernel(const Params p) {
 #pragma unroll
     for (int m = 0; m < MV; m++) {
       float v = acc[s][m];
-      v += __shfl_xor(v, 16, 64);
-      v += __shfl_xor(v, 32, 64);
+      v = add_xor32(add_xor16(v));
       if (gq == 0) red[(wave * MV + m) * R + 16 * s + r16] = v;
     }
   __syncthreads();

@@ -40,26 +40,6 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
 }
 
-// Cross-lane adds on the VALU: DPP within rows of 16 lanes, then the row
-// swaps of gfx950 across rows (no LDS crossbar traffic).
-template <int CTRL>
-__device__ __forceinline__ float dpp(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
-}
-constexpr int kQuadXor1 = 0xB1, kQuadXor2 = 0x4E, kRowHalfMirror = 0x141, kRowMirror = 0x140;
-
-// sum over the wave, every lane gets it
-__device__ __forceinline__ float wave_sum(float v) {
-  v += dpp<kQuadXor1>(v);
-  v += dpp<kQuadXor2>(v);
-  v += dpp<kRowHalfMirror>(v);  // lane i <-> 7-i: the other quad of the 8
-  v += dpp<kRowMirror>(v);      // lane i <-> 15-i: the other 8 of the row
-  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);  // rows 0+1, 2+3
-  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return __uint_as_float(b[0]) + __uint_as_float(b[1]);  // halves
-}
-
 // Q8: 4 codes of one dword -> bf16 pairs (q0,q1), (q2,q3), exact through f32
 __device__ __forceinline__ void decode_q8(uint32_t q, uint32_t& b0, uint32_t& b1) {
   const float f0 = static_cast<float>(q & 0xFFu), f1 = static_cast<float>((q >> 8) & 0xFFu);
@@ -139,9 +119,9 @@ __global__ __launch_bounds__(64 * W) void qmv_row_kernel(const uint16_t* __restr
       xp[q] = xv[i];
     }
     float sum = ((f[0] + f[1]) + (f[2] + f[3])) + ((f[4] + f[5]) + (f[6] + f[7]));
-    sum += dpp<kQuadXor1>(sum);  // Q8 chunk: 2 pieces
+    sum += dpp_f32<kDppQuadXor1>(sum);  // Q8 chunk: 2 pieces
     if (BITS == 4) {
-      sum += dpp<kQuadXor2>(sum);  // Q4 chunk: 4 pieces
+      sum += dpp_f32<kDppQuadXor2>(sum);  // Q4 chunk: 4 pieces
       if ((lane & 3) == 0) xs[q >> 2] = sum;
     } else {
       if ((lane & 1) == 0) xs[q >> 1] = sum;
