@@ -363,11 +363,12 @@ bool qmv_tile_preferred(int64_t M, int64_t N, int64_t K, int bits) {
   // Measured against the block kernel (qmv.hip) and the vector-ALU kernel
   // (qmv_dot) at the Llama-3-8B projection shapes: the tile kernel wins on
   // the large projections from M = 8 (Q4) / 16 (Q8),
-  // on Q4 gate/up already from M = 3, and on the small projections from
-  // M = 24 (Q4) / 32 (Q8).
+  // on Q4 gate/up already from M = 3, on short matrices (N <= 2048) from
+  // M = 16, and on the other small projections from M = 24 (Q4) / 32 (Q8).
   const bool large = N * K >= (int64_t(1) << 25);
   if (M <= 4) return large && K < N && bits == 4 && M >= 3;
   if (large) return M >= (bits == 4 ? 8 : 16);
+  if (N <= 2048) return M >= 16;  // k/v: M = 16 Q4 8.28 -> 7.93 us, Q8 9.27 -> 8.06; Q8 M = 24 11.07 -> 8.93
   return M >= (bits == 4 ? 24 : 32);
 }
 
