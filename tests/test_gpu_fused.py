@@ -124,3 +124,20 @@ def test_unsupported_shapes_launch_nothing(torch_gpu):
         mlxq.qmatmul_fused(dev(bf16_acts(61, 33, 512), True), [dw], 64, 4)
     with pytest.raises(mlxq.Unsupported):  # SwiGLU without a norm weight
         mlxq.qmatmul_fused(dev(bf16_acts(61, 1, 512), True), [dw, dict(dw)], 64, 4, swiglu=True)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+@pytest.mark.parametrize("k", [2048, 4096])
+def test_norm_gate_up_swiglu_batch1_ragged(torch_gpu, bits, gs, k):
+    """Batch-1 norm + gate/up + SwiGLU at every group size and both widths,
+    N (1002) not a multiple of the kernel's outputs per workgroup."""
+    n = 1002
+    x = bf16_acts(80 + k, 1, k)
+    w = orc.f32_to_bf16(orc.normal(81, k, 1.0, 0.1))
+    hg, dg = qlayer(82 + bits + gs, n, k, gs, bits)
+    hu, du = qlayer(83 + bits + gs, n, k, gs, bits)
+    dg["y"], du["y"] = out_like(1, n), out_like(1, n)
+    mlxq.qmatmul_fused(dev(x, True), [dg, du], gs, bits, norm_weight=dev(w, True), eps=1e-5, swiglu=True)
+    xn = orc.rms_norm(x, w, 1e-5)
+    check(dg["y"], orc.silu_mul(orc.qlinear_bf16(xn, hg, gs, bits), orc.qlinear_bf16(xn, hu, gs, bits)))
