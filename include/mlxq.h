@@ -185,6 +185,10 @@ typedef struct {
   int32_t stages, grid, lds_bytes, max_k, hidden, vocab;
   int32_t trace;  /* nonzero: the launch records per-stage wall-clock stamps
                      in the workspace (set from MLXQ_DECODE_TRACE at plan time) */
+  int64_t timeout_ticks;  /* longest grid-barrier wait, in 100 MHz wall-clock
+                             ticks (default 0.5 s; MLXQ_DECODE_TIMEOUT_TICKS
+                             at plan time overrides it, e.g. to force the
+                             time-out path in a test) */
 } mlxq_decode_plan_t;
 
 /* Device workspace bytes for a plan: header, stage table and the per-layer

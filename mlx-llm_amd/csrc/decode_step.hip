@@ -60,7 +60,7 @@ constexpr int kMaxResTasks = 8;                // residual stages: tasks per wor
 constexpr int kTraceWgs = 1024;                // profiling stamps kept for this many workgroups
 constexpr int kRing = 8;                       // ring depth (rounds in flight per wave; 8 measured faster than 16 or 20)
 constexpr int kLdsFloor = 96 * 1024;           // > half the CU's LDS: one workgroup per CU
-constexpr unsigned long long kTimeoutTicks = 50000000ull;  // 0.5 s at the 100 MHz wall clock
+constexpr long long kTimeoutTicks = 50000000ll;  // default barrier wait limit: 0.5 s at the 100 MHz wall clock
 
 enum : int32_t { ST_QKV = 0, ST_O = 1, ST_MLP = 2, ST_DOWN = 3, ST_HEAD = 4 };
 enum : int32_t { F_X_ARG = 1, F_RES_ARG = 2, F_Y_ARG = 4 };
@@ -182,7 +182,8 @@ template <int D>
 __global__ __launch_bounds__(kThreads, 1) void decode_step_kernel(const DStage* st_g, int NS,
                                                                   const uint16_t* __restrict__ x_arg,
                                                                   uint16_t* __restrict__ logits, DHeader* hdr,
-                                                                  int max_kin, int max_k, int hidden, int trace_on) {
+                                                                  int max_kin, int max_k, int hidden, int trace_on,
+                                                                  unsigned long long timeout_ticks) {
   extern __shared__ __align__(16) unsigned char smem[];
   const Lds L = lds_layout(max_kin, max_k, hidden, NS);
   uint16_t* raw = reinterpret_cast<uint16_t*>(smem + L.raw);
@@ -242,7 +243,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_step_kernel(const DStage* 
               ok = 0;
               break;
             }
-            if (wall_clock64() - t0 > kTimeoutTicks) {
+            if (wall_clock64() - t0 > timeout_ticks) {
               __hip_atomic_store(&hdr->error.v, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
               ok = 0;
               break;
@@ -749,6 +750,8 @@ extern "C" int mlxq_decode_plan(const mlxq_decode_config* cfg, const mlxq_decode
   plan->hidden = static_cast<int32_t>(d.hidden);
   plan->vocab = static_cast<int32_t>(d.vocab);
   plan->trace = getenv("MLXQ_DECODE_TRACE") ? 1 : 0;
+  plan->timeout_ticks = kTimeoutTicks;
+  if (const char* e = getenv("MLXQ_DECODE_TIMEOUT_TICKS")) plan->timeout_ticks = atoll(e);
   return MLXQ_OK;
 }
 
@@ -760,7 +763,8 @@ extern "C" int mlxq_decode_step(const mlxq_decode_plan_t* plan, const void* x, v
   hipLaunchKernelGGL(kern, dim3(plan->grid), dim3(kThreads), plan->lds_bytes,
                      as_stream(stream), stage_table(plan->workspace, plan->stages), plan->stages, static_cast<const uint16_t*>(x),
                      static_cast<uint16_t*>(logits), static_cast<DHeader*>(plan->workspace), plan->max_k,
-                     plan->max_k, plan->hidden, plan->trace);
+                     plan->max_k, plan->hidden, plan->trace,
+                     static_cast<unsigned long long>(plan->timeout_ticks > 0 ? plan->timeout_ticks : 1));
   return check_launch("decode_step");
 }
 

@@ -86,7 +86,8 @@ class DecodeConfig(ctypes.Structure):
 class DecodePlanT(ctypes.Structure):
     """mlxq_decode_plan_t (include/mlxq.h)."""
     _fields_ = [("workspace", _vp)] + [(n, ctypes.c_int32) for n in ("stages", "grid", "lds_bytes", "max_k",
-                                                                      "hidden", "vocab", "trace")]
+                                                                      "hidden", "vocab", "trace")] + \
+        [("timeout_ticks", ctypes.c_int64)]
 
 
 class MlxqError(RuntimeError):

@@ -110,3 +110,27 @@ def test_persistent_unsupported(torch_gpu):
     st = DecodeStack(StackConfig(bits=8, **SMALL), batch=1, seed=3)
     with pytest.raises(mlxq.Unsupported):
         st.persistent_plan()
+
+
+def test_persistent_barrier_timeout_path(torch_gpu, monkeypatch):
+    """Failure handling forced from the host: a 1-tick barrier wait limit
+    makes the grid barriers give up.  Every wave leaves the launch (the
+    bounded waits end it; nothing hangs), the plan reports the time-out, and a
+    fresh plan on the same weights computes the step correctly again."""
+    import torch
+    cfg = StackConfig(**SMALL)
+    st = DecodeStack(cfg, batch=1, seed=13, norm_noise=0.1)
+    x = orc.f32_to_bf16(orc.normal(777, cfg.hidden, 0.0, 1.0)).reshape(1, cfg.hidden)
+    st.x.copy_(dev(x, True))
+    monkeypatch.setenv("MLXQ_DECODE_TIMEOUT_TICKS", "1")
+    st.forward(1, persistent=True)
+    torch.cuda.synchronize()
+    assert st.persistent_plan().timed_out()
+    monkeypatch.delenv("MLXQ_DECODE_TIMEOUT_TICKS")
+    st._plan = None  # a new plan: the barrier state starts over
+    st.forward(1, persistent=True)
+    torch.cuda.synchronize()
+    assert not st.persistent_plan().timed_out()
+    layers, norm, lm = st.host_weights()
+    want = orc.decode_stack(x, layers, norm, lm, cfg.as_dict())
+    assert rel_err(orc.bf16_to_f32(host(st.logits)), orc.bf16_to_f32(want).astype(np.float64)) <= TOL
