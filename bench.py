@@ -452,9 +452,40 @@ def cpu_baseline(torch, weights, xs, seconds):
             nbytes += qbytes(1, n, k, 4)
         reps += 1
     dt = time.perf_counter() - t0
-    return {"value": round(nbytes / dt / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"Q4 g64 M=1, the 7 projections of one layer, {reps} passes in {dt:.1f} s "
-                      f"(oracle/baseline.c orc_qmatmul_f32, {threads} OpenMP threads)"}
+    out = {"value": round(nbytes / dt / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+           "sample": f"Q4 g64 M=1, the 7 projections of one layer, {reps} passes in {dt:.1f} s "
+                     f"(oracle/baseline.c orc_qmatmul_f32, {threads} OpenMP threads)",
+           "host_cpus": os.cpu_count()}
+    # the same GEMV on one core, and the reference's scalar GGUF dequant
+    # (src/gguf/dequant.rs, restated in oracle/oracle.c) on one core, a few
+    # seconds each
+    nbytes, reps, t0 = 0, 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds / 4 or reps == 0:
+        for name, k, n in PROJ:
+            wq, s, b = host[name]
+            orc.qmatmul_f32(xh[k], wq, s, b, 64, 4, threads=1)
+            nbytes += qbytes(1, n, k, 4)
+        reps += 1
+    dt = time.perf_counter() - t0
+    out["single_core"] = {"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s", "cores": 1,
+                          "sample": f"the same GEMV, {reps} passes in {dt:.1f} s"}
+    n = 14336 * 4096
+    be, bb = orc.gguf_block(12)  # Q4_K
+    rng = np.random.default_rng(0x5EED0400)
+    raw = rng.integers(0, 256, (n // be, bb), dtype=np.uint8)
+    for o in (0, 2):  # f16 d / dmin ~ 2^-7 .. 2^-5, positive
+        raw[:, o + 1] = 0x20 + rng.integers(0, 8, n // be, dtype=np.uint8)
+    raw = raw.reshape(-1)
+    reps, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds / 4 or reps == 0:
+        orc.gguf_dequantize(12, raw, n, threads=1)
+        reps += 1
+    dt = time.perf_counter() - t0
+    gb = reps * (raw.size + 4 * n) / 1e9
+    out["gguf_dequant_single_core"] = {"value": round(gb / dt, 3), "unit": "GB/s", "cores": 1,
+                                       "sample": f"Q4_K 14336x4096 to f32, {reps} passes in {dt:.1f} s "
+                                                 "(oracle/oracle.c, the reference's block loop, one thread)"}
+    return out
 
 
 if __name__ == "__main__":
