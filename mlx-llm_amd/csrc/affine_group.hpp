@@ -29,12 +29,22 @@ __device__ __forceinline__ void quantize_group8(const float (&v)[8], uint32_t (&
     w_max = fmaxf(w_max, v[i]);
     w_min = fminf(w_min, v[i]);
   }
-  // Butterfly within the LPG lanes of this group (groups never straddle a
-  // wavefront: LPG divides 64 and the lane index is group-aligned).
-#pragma unroll
-  for (int off = 1; off < LPG; off <<= 1) {
-    w_max = fmaxf(w_max, __shfl_xor(w_max, off, 64));
-    w_min = fminf(w_min, __shfl_xor(w_min, off, 64));
+  // All-reduce within the LPG lanes of this group (groups never straddle a
+  // 16-lane row: LPG is 4, 8 or 16 and the lane index is group-aligned) with
+  // DPP moves: quad swaps, then the other quad of 8 (lane i <-> 7 - i), then
+  // the other 8 of 16 (i <-> 15 - i).  Exact for max/min in any order.
+  static_assert(LPG == 4 || LPG == 8 || LPG == 16, "lanes per group");
+  w_max = fmaxf(w_max, dpp_f32<kDppQuadXor1>(w_max));
+  w_min = fminf(w_min, dpp_f32<kDppQuadXor1>(w_min));
+  w_max = fmaxf(w_max, dpp_f32<kDppQuadXor2>(w_max));
+  w_min = fminf(w_min, dpp_f32<kDppQuadXor2>(w_min));
+  if constexpr (LPG >= 8) {
+    w_max = fmaxf(w_max, dpp_f32<kDppRowHalfMirror>(w_max));
+    w_min = fminf(w_min, dpp_f32<kDppRowHalfMirror>(w_min));
+  }
+  if constexpr (LPG >= 16) {
+    w_max = fmaxf(w_max, dpp_f32<kDppRowMirror>(w_max));
+    w_min = fminf(w_min, dpp_f32<kDppRowMirror>(w_min));
   }
 
   constexpr float n_bins = static_cast<float>((1 << BITS) - 1);
@@ -50,9 +60,19 @@ __device__ __forceinline__ void quantize_group8(const float (&v)[8], uint32_t (&
     bias = edge;
   }
 
+  // code = rint(fl((w - bias) / scale)).  Fast form: t = (w - bias) *
+  // rcp(scale) is within 3 ulps of the correctly rounded quotient (v_rcp_f32
+  // 1 ulp, the product 0.5, the quotient 0.5; below 2e-4 for |t| < 1024), so
+  // wherever t is 5e-4 or more away from a half-integer, rint(t) equals rint
+  // of the correctly rounded quotient.  Near a tie (and for NaN/inf, where
+  // the comparison is false) the exact division decides.
+  const float rcp = __builtin_amdgcn_rcpf(scale);
 #pragma unroll
   for (int i = 0; i < 8; i++) {
-    float q = __builtin_rintf((v[i] - bias) / scale);
+    const float d = v[i] - bias;
+    const float t = d * rcp;
+    float q = __builtin_rintf(t);
+    if (!(fabsf(t - q) < 0.4995f && fabsf(t) < 1024.f)) q = __builtin_rintf(d / scale);
     q = fminf(fmaxf(q, 0.f), n_bins);
     codes[i] = static_cast<uint32_t>(q);
   }

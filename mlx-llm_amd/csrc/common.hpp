@@ -24,17 +24,17 @@ __device__ __forceinline__ float bits_to_f32(uint32_t u) { return __uint_as_floa
 
 // Exact binary16 -> binary32, NaNs quieted with payload kept (the conversion
 // `half::f16::to_f32` performs, used by src/gguf/dequant.rs:222-225).
+// Branch-free: the three encodings are formed and selected, so no per-call
+// control flow is left for the compiler to repeat at every use.
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
-  uint32_t sign = (h & 0x8000u) << 16;
-  uint32_t exp = (h >> 10) & 0x1Fu;
-  uint32_t man = h & 0x3FFu;
-  if (exp == 0x1Fu) return bits_to_f32(sign | 0x7F800000u | (man ? (0x400000u | (man << 13)) : 0u));
-  if (exp == 0u) {
-    // subnormal (or zero): man * 2^-24 is exact in f32
-    float v = static_cast<float>(man) * 5.9604644775390625e-08f;
-    return sign ? -v : v;
-  }
-  return bits_to_f32(sign | ((exp + 112u) << 23) | (man << 13));
+  const uint32_t sign = (h & 0x8000u) << 16;
+  const uint32_t exp = (h >> 10) & 0x1Fu;
+  const uint32_t man = h & 0x3FFu;
+  const uint32_t normal = sign | ((exp + 112u) << 23) | (man << 13);
+  const uint32_t special = sign | 0x7F800000u | (man ? (0x400000u | (man << 13)) : 0u);
+  // subnormal (or zero): man * 2^-24 is exact in f32
+  const uint32_t sub = sign | __float_as_uint(static_cast<float>(man) * 5.9604644775390625e-08f);
+  return bits_to_f32(exp == 0u ? sub : (exp == 0x1Fu ? special : normal));
 }
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return bits_to_f32(b << 16); }

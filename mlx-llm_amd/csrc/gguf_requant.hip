@@ -120,7 +120,7 @@ int launch_lpg(int rows, int K, int row_bytes, int perm_hd, const uint8_t* d, ui
                uint16_t* b, hipStream_t st) {
   const bool al = (reinterpret_cast<uintptr_t>(d) & 15u) == 0 && row_bytes % 16 == 0;
   const size_t lds = (static_cast<size_t>(row_bytes) + 15) / 16 * 16;
-  const dim3 grid(static_cast<unsigned>(std::min(rows, 8192)));
+  const dim3 grid(static_cast<unsigned>(rows));  // one row per workgroup: whole rounds of resident workgroups
   auto kern = al ? gguf_requant_kernel<TAG, BITS, LPG, true> : gguf_requant_kernel<TAG, BITS, LPG, false>;
   if (lds > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),

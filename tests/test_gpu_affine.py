@@ -85,3 +85,25 @@ def test_llama_shapes_bit_exact(torch_gpu, shape, bits):
     got = gpu_quantize(w, 64, bits, True)
     for r, g in zip(ref, got):
         assert np.array_equal(r.view(np.uint8), g.view(np.uint8))
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("factor", [1.0, 0.02, 3.0e-5, 7.0])
+def test_codes_at_rounding_ties(torch_gpu, bits, factor):
+    """Groups whose quotients (w - bias) / scale sit on or within a few ulps
+    of half-integers: min 0 and max n_bins (times `factor`) make scale
+    -factor and bias max, so every element j + 1/2 (times `factor`) lands on a
+    tie of the code rounding; with factor not a power of two the f32 products
+    put the quotients a few ulps to either side of it."""
+    rng = np.random.default_rng(77 + bits)
+    n_bins = (1 << bits) - 1
+    gs, rows, cols = 64, 64, 512
+    half = rng.integers(0, 2 * n_bins + 1, size=(rows, cols)).astype(np.float32) / 2
+    half = half.reshape(rows, cols // gs, gs)
+    half[:, :, 0] = 0
+    half[:, :, 1] = n_bins
+    w = (half.reshape(rows, cols) * np.float32(factor)).astype(np.float32)
+    ref = orc.affine_quantize(w, gs, bits, orc.F32)
+    got = gpu_quantize(w, gs, bits, False)
+    for r, g in zip(ref, got):
+        assert np.array_equal(np.asarray(r).view(np.uint8), np.asarray(g).view(np.uint8))
