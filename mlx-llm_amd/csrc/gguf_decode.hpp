@@ -28,15 +28,16 @@ __device__ __forceinline__ uint32_t rd_u32(const uint8_t* b) {
          (static_cast<uint32_t>(b[2]) << 16) | (static_cast<uint32_t>(b[3]) << 24);
 }
 
-// get_scale_min_k4 (dequant.rs:375-383)
+// get_scale_min_k4 (dequant.rs:375-383).  Branch-free (j differs between
+// the lanes of a wave, so a branch would run both sides): with a = q[j & 3],
+// b = q[(j & 3) + 4], c = q[(j & 3) + 8], sub-blocks 0-3 take the low 6 bits
+// of a / b, sub-blocks 4-7 the nibbles of c plus the top 2 bits of a / b.
 __device__ __forceinline__ void scale_min_k4(int j, const uint8_t* q, uint32_t& d, uint32_t& m) {
-  if (j < 4) {
-    d = q[j] & 63u;
-    m = q[j + 4] & 63u;
-  } else {
-    d = (q[j + 4] & 0x0Fu) | ((q[j - 4] >> 6) << 4);
-    m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
-  }
+  const int j3 = j & 3;
+  const uint32_t a = q[j3], b = q[j3 + 4], c = q[j3 + 8];
+  const bool low = j < 4;
+  d = low ? (a & 63u) : ((c & 0x0Fu) | ((a >> 6) << 4));
+  m = low ? (b & 63u) : ((c >> 4) | ((b >> 6) << 4));
 }
 
 // One element j of a block at b (LDS).  Tag is a template constant.

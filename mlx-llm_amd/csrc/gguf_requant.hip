@@ -96,7 +96,7 @@ __global__ __launch_bounds__(kThreads) void gguf_requant_kernel(const uint8_t* _
           for (int i = 0; i < 8; i++) v[i] = decode<TAG>(b, e - blk * E + i);  // 8 never straddle a block
         }
 #pragma unroll
-        for (int i = 0; i < 8; i++) v[i] = bf16_bits_to_f32(f32_to_bf16_bits(v[i]));  // as_dtype(bf16)
+        for (int i = 0; i < 8; i++) v[i] = static_cast<float>(static_cast<__bf16>(v[i]));  // as_dtype(bf16): v_cvt_pk_bf16_f32, round to nearest even (a NaN payload cannot reach a code: max/min skip NaN and a NaN quotient clamps to 0)
       }
       uint32_t codes[8];
       float scale, bias;
