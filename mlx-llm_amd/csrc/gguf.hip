@@ -16,6 +16,7 @@
 #include <string>
 
 #include "common.hpp"
+#define MLXQ_IQ4NL_IN_REGISTERS 1  // IQ4 codebook lookups by v_perm (this kernel is memory-bound)
 #include "gguf_decode.hpp"
 
 namespace mlxq {

@@ -17,8 +17,35 @@
 namespace mlxq {
 namespace {  // internal linkage: each including file has its own copy
 
-__constant__ int8_t kIq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
-                                  1,    13,   25,  38,  53,  69,  89,  113};
+constexpr int8_t kIq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
+                               1,    13,   25,  38,  53,  69,  89,  113};
+// The codebook as four little-endian dwords of bytes, so a lookup is a
+// v_perm byte select in registers instead of a per-lane memory load.
+constexpr uint32_t iq4nl_word(int w) {
+  return static_cast<uint32_t>(static_cast<uint8_t>(kIq4nl[4 * w])) |
+         (static_cast<uint32_t>(static_cast<uint8_t>(kIq4nl[4 * w + 1])) << 8) |
+         (static_cast<uint32_t>(static_cast<uint8_t>(kIq4nl[4 * w + 2])) << 16) |
+         (static_cast<uint32_t>(static_cast<uint8_t>(kIq4nl[4 * w + 3])) << 24);
+}
+// kIq4nl[q] for q in 0..15.  Two forms, chosen per including file by what
+// measured faster there: the memory-bound dequantizer defines
+// MLXQ_IQ4NL_IN_REGISTERS (v_perm picks byte q & 7 of the 8-byte half
+// selected by q & 8; selector values 0-3 address the second operand: 51 ->
+// 44 us for a 14336x4096 IQ4_NL tensor), the VALU-bound converter keeps the
+// table load (56 vs 61 us with the v_perm form).
+#ifdef MLXQ_IQ4NL_IN_REGISTERS
+__device__ __forceinline__ int iq4nl_value(uint32_t q) {
+  const uint32_t sel = q & 7u;
+  const uint32_t lo = __builtin_amdgcn_perm(iq4nl_word(1), iq4nl_word(0), sel);
+  const uint32_t hi = __builtin_amdgcn_perm(iq4nl_word(3), iq4nl_word(2), sel);
+  return static_cast<int8_t>((q & 8u) ? hi : lo);
+}
+#else
+__constant__ int8_t kIq4nlDev[16] = {kIq4nl[0],  kIq4nl[1],  kIq4nl[2],  kIq4nl[3],  kIq4nl[4],  kIq4nl[5],
+                                     kIq4nl[6],  kIq4nl[7],  kIq4nl[8],  kIq4nl[9],  kIq4nl[10], kIq4nl[11],
+                                     kIq4nl[12], kIq4nl[13], kIq4nl[14], kIq4nl[15]};
+__device__ __forceinline__ int iq4nl_value(uint32_t q) { return kIq4nlDev[q]; }
+#endif
 
 __device__ __forceinline__ float rd_f16(const uint8_t* b, int i) {
   return f16_bits_to_f32(static_cast<uint32_t>(b[i]) | (static_cast<uint32_t>(b[i + 1]) << 8));
@@ -158,8 +185,8 @@ __device__ __forceinline__ float decode<14>(const uint8_t* b, int j) {
   int idx = j >> 7, t = (j >> 5) & 3, l = j & 31;
   const uint8_t* qlp = b + 64 * idx;
   const uint8_t* qhp = b + 128 + 32 * idx;
-  uint32_t lo = (t & 1) ? qlp[l + 32] : qlp[l];
-  lo = (t & 2) ? (lo >> 4) : (lo & 0xFu);
+  // branch-free: byte l or l + 32 of ql, low or high nibble
+  const uint32_t lo = (static_cast<uint32_t>(qlp[l + 32 * (t & 1)]) >> (4 * (t >> 1))) & 0xFu;
   uint32_t hb = (qhp[l] >> (2 * t)) & 3u;
   int q = static_cast<int>(static_cast<int8_t>(lo | (hb << 4))) - 32;
   int sc = static_cast<int8_t>(b[192 + 8 * idx + (l >> 4) + 2 * t]);
@@ -172,7 +199,7 @@ __device__ __forceinline__ float decode<20>(const uint8_t* b, int j) {
   float d = rd_f16(b, 0);
   uint32_t byte = b[2 + (j & 15)];
   uint32_t q = j < 16 ? (byte & 0xFu) : (byte >> 4);
-  return d * static_cast<float>(kIq4nl[q]);
+  return d * static_cast<float>(iq4nl_value(q));
 }
 // IQ4_XS (dequant.rs:481-497)
 template <>
@@ -185,7 +212,7 @@ __device__ __forceinline__ float decode<23>(const uint8_t* b, int j) {
   float dl = d * static_cast<float>(ls - 32);
   uint32_t byte = b[8 + 16 * ib + (jj & 15)];
   uint32_t q = jj < 16 ? (byte & 0xFu) : (byte >> 4);
-  return dl * static_cast<float>(kIq4nl[q]);
+  return dl * static_cast<float>(iq4nl_value(q));
 }
 
 // ---- IQ grid types (dequant.rs:505-719).  Codebooks: the format's fixed
