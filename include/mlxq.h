@@ -64,6 +64,12 @@ const char* mlxq_last_error(void);
 /* Library version string. */
 const char* mlxq_version(void);
 
+/* Reads the MLXQ_* kernel-override environment variables (tuning and tests:
+ * force a GEMV kernel or a tile configuration) again.  No counterpart in the
+ * reference.  The dispatch reads them once, on first use, never per call, so
+ * a process that changes them calls this afterwards. */
+int mlxq_reload_overrides(void);
+
 /* ------------------------------------------------------------------ */
 /* Affine group-wise quantization                                      */
 /* ------------------------------------------------------------------ */
@@ -217,9 +223,15 @@ int mlxq_decode_plan(const mlxq_decode_config* cfg,
  * mlxq_repeat_kv / mlxq_add / mlxq_silu_mul up to f32 summation order.
  * One launch with one workgroup per CU, all resident, synchronising through
  * a grid barrier in the workspace; capturable in a HIP graph.  Calls on one
- * plan must not overlap (they share its barrier and activations).  A barrier
- * that waits longer than 0.5 s (workgroups not co-resident) ends the launch;
- * mlxq_decode_status then reports it and the plan must be made again. */
+ * plan must not overlap (they share its barrier and activations).
+ * Precondition: the launch's workgroups (one per CU) must all be resident at
+ * once, so no other kernel may hold CUs while a step runs (work on another
+ * stream or in another process on the same GPU breaks this).  A barrier that
+ * waits longer than 0.5 s (workgroups not co-resident) ends the launch
+ * without finishing the logits; mlxq_decode_status then reports it, every
+ * later step on the plan also ends at its first barrier, and the plan must
+ * be made again.  Callers that cannot guarantee co-residency check
+ * mlxq_decode_status after a step (a synchronous read). */
 int mlxq_decode_step(const mlxq_decode_plan_t* plan, const void* x,
                      void* logits, void* stream);
 

@@ -35,6 +35,7 @@ COMMON = [
 NO_CONTRACT = {"gguf.hip", "affine.hip", "gguf_requant.hip"}
 
 
+
 def sources() -> list[Path]:
     srcs = sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
     if HOST.is_dir():
@@ -76,6 +77,7 @@ def build(jobs: int = 8, verbose: bool = False) -> Path:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, LIB)
     build_host_tests(verbose)
+    build_cli(verbose)
     return LIB
 
 
@@ -93,6 +95,20 @@ def build_host_tests(verbose: bool = False) -> Path:
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"host tests build failed:\n{r.stdout}\n{r.stderr}")
+    return out
+
+
+def build_cli(verbose: bool = False) -> Path:
+    """bin/convert_gguf: the GGUF -> MLX snapshot converter (cli/convert_gguf.cpp)."""
+    BIN.mkdir(exist_ok=True)
+    out = BIN / "convert_gguf"
+    cmd = [HIPCC, "-O2", "-std=c++17", f"--offload-arch={ARCH}", "-x", "hip", f"-I{ROOT / 'include'}", f"-I{HOST}",
+           str(PKG / "cli" / "convert_gguf.cpp"), "-x", "none", str(LIB), "-Wl,-rpath,$ORIGIN/..", "-o", str(out)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"convert_gguf build failed:\n{r.stdout}\n{r.stderr}")
     return out
 
 

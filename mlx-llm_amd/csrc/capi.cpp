@@ -1,7 +1,11 @@
 // Host-side C ABI pieces that launch nothing: error strings, version, GGUF
 // block geometry.
 #include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
 
+#include <atomic>
+#include <mutex>
 #include <string>
 
 #include "common.hpp"
@@ -23,9 +27,65 @@ int check_launch(const char* what) {
   return MLXQ_OK;
 }
 
+namespace {
+
+const Overrides* read_overrides() {
+  auto* o = new Overrides{};
+  auto flag = [](const char* n) { return getenv(n) != nullptr; };
+  auto pair = [](const char* n, int* a, int* b) {
+    if (const char* e = getenv(n)) sscanf(e, "%d,%d", a, b);
+  };
+  auto num = [](const char* n) {
+    const char* e = getenv(n);
+    return e ? atoi(e) : 0;
+  };
+  o->qmv_row_all = flag("MLXQ_QMV_ROW_ALL");
+  o->qmv_no_row = flag("MLXQ_QMV_NO_ROW");
+  o->qmv_mfma = flag("MLXQ_QMV_MFMA");
+  o->qmv_dot_all = flag("MLXQ_QMV_DOT_ALL");
+  o->qmv_tile_all = flag("MLXQ_QMV_TILE_ALL");
+  o->qmv_legacy = flag("MLXQ_QMV_LEGACY");
+  o->qmv_stream = flag("MLXQ_QMV_STREAM");
+  o->qmv_narrow = flag("MLXQ_QMV_NARROW");
+  pair("MLXQ_QMV_TILE", &o->tile_wv, &o->tile_nch);
+  pair("MLXQ_QMV_DOT", &o->dot_sub, &o->dot_wv);
+  pair("MLXQ_QMV_MFMA_CFG", &o->mfma_sub, &o->mfma_wv);
+  o->qmv_sub = num("MLXQ_QMV_SUB");
+  o->row_r = num("MLXQ_QMV_ROW_R");
+  o->row_w = num("MLXQ_QMV_ROW_W");
+  o->qmm_cfg = num("MLXQ_QMM_CFG");
+  o->qmm_split = num("MLXQ_QMM_SPLIT");
+  return o;
+}
+
+// Published once and replaced whole by a reload; a replaced table is never
+// freed (a call on another thread may still be reading it).
+std::atomic<const Overrides*> g_overrides{nullptr};
+std::mutex g_overrides_mu;
+
+}  // namespace
+
+const Overrides& overrides() {
+  const Overrides* o = g_overrides.load(std::memory_order_acquire);
+  if (o) return *o;
+  std::lock_guard<std::mutex> lk(g_overrides_mu);
+  o = g_overrides.load(std::memory_order_relaxed);
+  if (!o) {
+    o = read_overrides();
+    g_overrides.store(o, std::memory_order_release);
+  }
+  return *o;
+}
+
 }  // namespace mlxq
 
 using namespace mlxq;
+
+extern "C" int mlxq_reload_overrides(void) {
+  std::lock_guard<std::mutex> lk(g_overrides_mu);
+  g_overrides.store(read_overrides(), std::memory_order_release);
+  return MLXQ_OK;
+}
 
 extern "C" const char* mlxq_last_error(void) { return g_last_error.c_str(); }
 

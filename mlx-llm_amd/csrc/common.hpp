@@ -17,6 +17,20 @@ int fail(int status, const std::string& msg);
 // Check the launch that was just enqueued.
 int check_launch(const char* what);
 
+// Kernel-choice overrides for tuning and tests, from MLXQ_* environment
+// variables.  Read once, on first use (not on every call: the dispatch path
+// does no environment lookups); mlxq_reload_overrides() reads them again.
+struct Overrides {
+  bool qmv_row_all, qmv_no_row, qmv_mfma, qmv_dot_all, qmv_tile_all, qmv_legacy, qmv_stream, qmv_narrow;
+  int tile_wv, tile_nch;    // MLXQ_QMV_TILE=waves,chunks
+  int dot_sub, dot_wv;      // MLXQ_QMV_DOT=sub,waves
+  int mfma_sub, mfma_wv;    // MLXQ_QMV_MFMA_CFG=sub,waves
+  int qmv_sub;              // MLXQ_QMV_SUB
+  int row_r, row_w;         // MLXQ_QMV_ROW_R, MLXQ_QMV_ROW_W
+  int qmm_cfg, qmm_split;   // MLXQ_QMM_CFG, MLXQ_QMM_SPLIT
+};
+const Overrides& overrides();
+
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 // ---- device scalar conversions (bit-level, independent of FP modes) ----

@@ -2,8 +2,6 @@
 // qmv / qmm choice (MLX makes the same choice from M inside quantized_matmul).
 #include <hip/hip_runtime.h>
 
-#include <stdlib.h>
-
 #include <string>
 
 #include "common.hpp"
@@ -82,11 +80,12 @@ extern "C" int mlxq_qmatmul_algo(const void* x, int64_t M, const uint32_t* wq, c
   // <= 2048: k/v 6.1 -> 5.6 us Q4, 6.9 -> 5.1 Q8 at M = 4; on taller ones
   // its per-row decode and LDS reads make it slower than the kernels below).
   // MLXQ_QMV_NO_ROW=1 skips it, MLXQ_QMV_ROW_ALL=1 takes it for every M <= 4.
-  if (qmv_row_eligible(M, N, K, group_size, bits) && (M == 1 || N <= 2048 || getenv("MLXQ_QMV_ROW_ALL")) &&
-      !getenv("MLXQ_QMV_NO_ROW") && !getenv("MLXQ_QMV_MFMA"))
+  const Overrides& ov = overrides();
+  if (qmv_row_eligible(M, N, K, group_size, bits) && (M == 1 || N <= 2048 || ov.qmv_row_all) && !ov.qmv_no_row &&
+      !ov.qmv_mfma)
     return launch_qmv_row(xp, M, wq, sp, bp, bias, N, K, group_size, bits, yp, st);
-  if (M <= kQmvDotMaxM && qmv_dot_eligible(M, N, K, group_size, bits) && !getenv("MLXQ_QMV_MFMA") &&
-      (qmv_dot_preferred(M, N, K, bits) || getenv("MLXQ_QMV_DOT_ALL")))
+  if (M <= kQmvDotMaxM && qmv_dot_eligible(M, N, K, group_size, bits) && !ov.qmv_mfma &&
+      (qmv_dot_preferred(M, N, K, bits) || ov.qmv_dot_all))
     return launch_qmv_dot(xp, M, wq, sp, bp, bias, N, K, group_size, bits, yp, st);
 
   // batched decode: activations shared through LDS, K split across
@@ -94,8 +93,7 @@ extern "C" int mlxq_qmatmul_algo(const void* x, int64_t M, const uint32_t* wq, c
   // below.  MLXQ_QMV_TILE_ALL=1 takes it for every eligible shape,
   // MLXQ_QMV_LEGACY=1 never.
   if (M <= kQmvMaxM && qmv_tile_eligible(M, N, K, group_size, bits) &&
-      (qmv_tile_preferred(M, N, K, bits) || getenv("MLXQ_QMV_TILE_ALL")) && !getenv("MLXQ_QMV_LEGACY") &&
-      !getenv("MLXQ_QMV_STREAM")) {
+      (qmv_tile_preferred(M, N, K, bits) || ov.qmv_tile_all) && !ov.qmv_legacy && !ov.qmv_stream) {
     rc = launch_qmv_tile(xp, M, wq, sp, bp, bias, N, K, group_size, bits, yp, workspace, workspace_bytes, st);
     if (rc != MLXQ_ERR_UNSUPPORTED) return rc;  // else: no split fits the workspace, use the block kernel
   }
@@ -103,7 +101,7 @@ extern "C" int mlxq_qmatmul_algo(const void* x, int64_t M, const uint32_t* wq, c
   // MLXQ_QMV_STREAM=1: the streaming matrix-core kernel (the fused entry
   // point's M > 4 form) for plain calls too; measured at parity or slower
   // than the block kernel below for most plain shapes, so not the default
-  if (M <= kQmvMaxM && qmv_mfma_eligible(M, K, group_size, bits) && getenv("MLXQ_QMV_STREAM")) {
+  if (M <= kQmvMaxM && qmv_mfma_eligible(M, K, group_size, bits) && ov.qmv_stream) {
     QmvFused f{};
     f.x = xp;
     f.M = M;
@@ -194,3 +192,4 @@ extern "C" int mlxq_qmatmul_fused(const void* x, int64_t M, int64_t K, const voi
   }
   return launch_qmv_dot_fused(f, as_stream(stream));
 }
+

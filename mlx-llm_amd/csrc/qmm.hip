@@ -442,7 +442,7 @@ int launch_cfg(const uint16_t* x, int M, const uint32_t* wq, const uint16_t* s, 
   if (splits > 1 || tiles256 * 8 >= cus * 7) cfg = even_steps ? 14 : 9;
   if (BITS == 4 && splits == 1 && N % 224 == 0 && (N / 224) * ceil_div(M, 256) * 8 >= cus * 7)
     cfg = even_steps ? 15 : 10;
-  if (const char* e = getenv("MLXQ_QMM_CFG")) cfg = atoi(e);
+  if (overrides().qmm_cfg) cfg = overrides().qmm_cfg;
   switch (cfg) {
     case 1: return launch<BITS, GS, 256, 256, 2, 4>(x, M, wq, s, b, bias, N, K, y, part, splits, st);
     case 2: return launch<BITS, GS, 256, 128, 2, 2>(x, M, wq, s, b, bias, N, K, y, part, splits, st);
@@ -465,8 +465,7 @@ int qmm_split_k(int64_t M, int64_t N, int64_t K) {
   // (one per CU) when the unsplit grid leaves most CUs idle; each slice
   // keeps at least 16 K steps and whole groups (K / splits % 128 == 0).
   // MLXQ_QMM_SPLIT overrides (tuning).
-  if (const char* e = getenv("MLXQ_QMM_SPLIT")) {
-    const int sp = atoi(e);
+  if (const int sp = overrides().qmm_split) {
     return sp >= 1 && sp <= kQmmMaxSplits && K % (128 * sp) == 0 ? sp : 1;
   }
   const int64_t cus = cu_count();

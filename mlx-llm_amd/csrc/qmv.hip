@@ -518,7 +518,7 @@ QmvPlan plan_qmv(int64_t M, int64_t N, int64_t K, int group_size, int bits) {
   // latency twice.
   int sub = 1;
   while (sub < 4 && ceil_div(N, 16 * sub) > 512) sub <<= 1;
-  if (const char* e = getenv("MLXQ_QMV_SUB")) sub = atoi(e) == 1 || atoi(e) == 2 || atoi(e) == 4 ? atoi(e) : sub;
+  if (const int o = overrides().qmv_sub; o == 1 || o == 2 || o == 4) sub = o;
   p.sub = sub;
   p.row_tiles = ceil_div(N, 16 * sub);
   // 16-byte-per-lane loads need whole 64-byte chunks per row, and the
@@ -530,7 +530,7 @@ QmvPlan plan_qmv(int64_t M, int64_t N, int64_t K, int group_size, int bits) {
   p.sub = sub;
   p.row_tiles = ceil_div(N, 16 * sub);
   p.wide = sub <= 2 && row_bytes % 64 == 0 && G % std::max<int64_t>(1, groups_per_block) == 0 &&
-           !getenv("MLXQ_QMV_NARROW");
+           !overrides().qmv_narrow;
   int unroll = 4;
   while (unroll > 1 && G % unroll) unroll >>= 1;
   p.unroll = unroll;

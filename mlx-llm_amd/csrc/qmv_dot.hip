@@ -102,8 +102,7 @@ int launch_qmv_dot_fused(const QmvFused& f, hipStream_t st) {
   const int64_t chunks = K * f.bits / 8 / 64;
   Cfg best;
   int64_t best_pass = -1, best_waves = 0;
-  int forced_sub = 0, forced_wv = 0;
-  if (const char* e = getenv("MLXQ_QMV_DOT")) sscanf(e, "%d,%d", &forced_sub, &forced_wv);
+  const int forced_sub = overrides().dot_sub, forced_wv = overrides().dot_wv;
   for (int sub = 1; sub <= 2; sub++)
     for (int wv = 4; wv <= 8; wv += 4) {
       if (f.swiglu && sub != 1) continue;

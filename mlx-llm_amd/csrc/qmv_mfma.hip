@@ -367,8 +367,7 @@ int launch_qmv_mfma(const QmvFused& f, hipStream_t st) {
   const int64_t chunks = K * f.bits / 8 / 64;
   Cfg best;
   int64_t best_pass = -1, best_waves = 0;
-  int forced_sub = 0, forced_wv = 0;
-  if (const char* e = getenv("MLXQ_QMV_MFMA_CFG")) sscanf(e, "%d,%d", &forced_sub, &forced_wv);
+  const int forced_sub = overrides().mfma_sub, forced_wv = overrides().mfma_wv;
   for (int sub = 1; sub <= (mt == 1 ? 2 : 1); sub++)  // two M-tiles: one row sub-tile (registers)
     for (int wv = 4; wv <= 8; wv += 4) {
       if ((forced_sub && sub != forced_sub) || (forced_wv && wv != forced_wv)) continue;

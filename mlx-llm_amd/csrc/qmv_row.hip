@@ -247,8 +247,8 @@ void qmv_row_geometry(int64_t N, int64_t K, int bits, int& R, int& W) {
   const int64_t ni = K * bits / 8 / 1024;
   R = bits == 4 && ni <= 2 && N >= 4096 ? 2 : 1;  // Q4 q/o 4.96 vs 5.18 us, gate 9.72 vs 10.48; Q8 best at 1
   W = 4;                                          // Q8 down: 15.8 us at 4 waves, 16.2 at 8, 17.6 at 16
-  if (const char* e = getenv("MLXQ_QMV_ROW_R")) R = atoi(e);
-  if (const char* e = getenv("MLXQ_QMV_ROW_W")) W = atoi(e);
+  if (overrides().row_r) R = overrides().row_r;
+  if (overrides().row_w) W = overrides().row_w;
 }
 
 int launch_qmv_row(const uint16_t* x, int64_t M, const uint32_t* wq, const uint16_t* s, const uint16_t* b,

@@ -29,7 +29,6 @@
 //    stores, counter atomic and loads are three serial trips past the L2.
 #include <hip/hip_runtime.h>
 
-#include <atomic>
 #include <cstdio>
 #include <cstdlib>
 #include <string>
@@ -62,22 +61,9 @@ struct TileParams {
   float* part;  // [splits][M][N] partial sums (splits > 1)
   int M, N, K;
   int splits;
-  int fuse;  // splits > 1: the last slice of a tile to finish adds the slices (no reduce launch)
-  int slot;  // arrival-counter slot of this call (fuse)
 };
 
 constexpr int kMaxSplitsK = 16;  // most K splits of one call
-
-// Arrival counters of the fused split-K sum: one per (slot, tile).  Zero at
-// load; the last arriving slice of a tile sets its counter back to zero, so
-// every counter is zero between calls.  Calls rotate over the slots, so calls
-// on different streams of one device use separate counters unless more than
-// kArrivalSlots of them overlap in time.
-constexpr int kArrivalSlots = 16;
-constexpr int kMaxArrivalTiles = 4096;
-__device__ unsigned tile_arrivals[kArrivalSlots * kMaxArrivalTiles];
-typedef __attribute__((address_space(1))) float gf32;
-typedef __attribute__((address_space(1))) unsigned gu32;
 
 // Q4 codes of one dword (k0..k7, LSB first) -> bf16 (128 + k) pairs
 // (k0,k2),(k4,k6),(k1,k3),(k5,k7): two masks pick the even / odd nibbles
@@ -242,80 +228,16 @@ __global__ __launch_bounds__(64 * WV) void qmv_tile_kernel(const TileParams p) {
     return;
   }
 
-  // partial tile of this slice; qmv_tile_reduce_kernel adds the slices, or
-  // (fuse) the last slice of this tile to arrive adds them
+  // partial tile of this slice; split_reduce4_kernel adds the slices
   if (nn < N) {
 #pragma unroll
     for (int mt = 0; mt < MT; mt++)
 #pragma unroll
       for (int v = 0; v < 4; v++) {
         const int m = 16 * mt + 4 * gq + v;
-        float* dst = p.part + (static_cast<int64_t>(split) * M + m) * N + nn;
-        if (m < M) {
-          if (p.fuse)  // agent-coherent: read by a workgroup on another XCD
-            __hip_atomic_store((gf32*)(dst), acc[mt][v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          else
-            *dst = acc[mt][v];
-        }
+        if (m < M) p.part[(static_cast<int64_t>(split) * M + m) * N + nn] = acc[mt][v];
       }
   }
-  if (!p.fuse) return;
-
-  // arrival: this workgroup's partial stores are complete (explicit wait)
-  // before one relaxed agent-scope add on the tile's counter
-  __shared__ int is_last;
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(0);
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __syncthreads();
-  if (tid == 0) {
-    gu32* ctr = (gu32*)(&tile_arrivals[p.slot * kMaxArrivalTiles + tile]);
-    const unsigned before = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const int last = before == static_cast<unsigned>(p.splits - 1);
-    if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    is_last = last;
-  }
-  __syncthreads();
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  if (!is_last || nn >= N) return;
-
-  // y = bf16(part[0] + part[1] + ... + part[splits-1] + bias), slices added
-  // in slice order (the sum of split_reduce4_kernel); this slice's own
-  // partial comes from registers, the others by agent-coherent loads, four
-  // slices' loads in flight at a time
-  float sum[MT][4];
-  for (int s0 = 0; s0 < p.splits; s0 += 4) {
-    float val[4][MT][4];
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-      for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-        for (int v = 0; v < 4; v++) {
-          const int sp = s0 + i, m = 16 * mt + 4 * gq + v;
-          val[i][mt][v] = acc[mt][v];
-          if (sp < p.splits && sp != split && m < M)
-            val[i][mt][v] = __hip_atomic_load(
-                (gf32*)(p.part + (static_cast<int64_t>(sp) * M + m) * N + nn), __ATOMIC_RELAXED,
-                __HIP_MEMORY_SCOPE_AGENT);
-        }
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-      if (s0 + i < p.splits)
-#pragma unroll
-        for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-          for (int v = 0; v < 4; v++) sum[mt][v] = s0 + i == 0 ? val[i][mt][v] : sum[mt][v] + val[i][mt][v];
-  }
-  const float bb = p.bias ? bf16_bits_to_f32(p.bias[nn]) : 0.f;
-#pragma unroll
-  for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-    for (int v = 0; v < 4; v++) {
-      const int m = 16 * mt + 4 * gq + v;
-      const float t = p.bias ? sum[mt][v] + bb : sum[mt][v];
-      if (m < M) p.y[static_cast<int64_t>(m) * N + nn] = static_cast<uint16_t>(f32_to_bf16_bits(t));
-    }
 }
 
 // y[m, n] = bf16(sum over splits of part[s, m, n] (in split order) + bias[n])
@@ -492,8 +414,7 @@ int launch_qmv_tile(const uint16_t* x, int64_t M, const uint32_t* wq, const uint
   } else {
     pref.wv = 4; pref.nch = bits == 4 && N < 2048 ? 4 : 8;
   }
-  int fwv = 0, fnch = 0;
-  if (const char* e = getenv("MLXQ_QMV_TILE")) sscanf(e, "%d,%d", &fwv, &fnch);
+  const int fwv = overrides().tile_wv, fnch = overrides().tile_nch;
   if (fwv) pref.wv = fwv;
   if (fnch) pref.nch = fnch;
   const Cfg order[] = {pref, {pref.mt, 8, 16}, {pref.mt, 8, 8}, {pref.mt, 4, 8}, {pref.mt, 4, 4}, {pref.mt, 8, 4}};
@@ -512,16 +433,12 @@ int launch_qmv_tile(const uint16_t* x, int64_t M, const uint32_t* wq, const uint
   a.part = a.splits > 1 ? static_cast<float*>(workspace) : nullptr;
   const int64_t tiles = ceil_div(N, 16 * pick->wv);
   // split K: the slices are added by a second launch (split_reduce4_kernel).
-  // MLXQ_QMV_SPLIT_FUSED=1 has each tile's last arriving slice add them
-  // instead (no second launch); measured slower at the Llama-3-8B shapes
-  // (Q8 M = 32 gate 26.1 -> 26.9 us, Q4 M = 32 sweep 1363 -> 1261 GB/s): the
-  // agent-coherent partial stores and the last slice's serial tail cost more
-  // than the launch they save.
-  static std::atomic<unsigned> next_slot{0};
-  a.fuse = a.splits > 1 && tiles <= kMaxArrivalTiles && getenv("MLXQ_QMV_SPLIT_FUSED");
-  a.slot = a.fuse ? static_cast<int>(next_slot.fetch_add(1, std::memory_order_relaxed) % kArrivalSlots) : 0;
+  // A hand-off inside this kernel (the last arriving slice of a tile adds the
+  // slices) was measured slower at the Llama-3-8B shapes (Q8 M = 32 gate
+  // 26.1 -> 26.9 us): its agent-coherent partial stores and serial tail cost
+  // more than the launch it saves.
   if (int rc = dispatch(bits, *pick, a, static_cast<int>(tiles), st, nullptr)) return rc;
-  if (a.splits == 1 || a.fuse) return MLXQ_OK;
+  if (a.splits == 1) return MLXQ_OK;
   return launch_split_reduce(a.part, bias, y, M, N, a.splits, st);
 }
 

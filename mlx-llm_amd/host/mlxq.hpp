@@ -9,6 +9,10 @@
 //                              <- gguf::dequant (src/gguf/dequant.rs:31-211)
 //   mlxq::gguf::requantize_projection
 //                              <- the per-projection chain of gguf::convert (src/gguf/convert.rs:131-176)
+//   mlxq::gguf::GgufFile, MetaValue, TensorInfo
+//                              <- gguf::reader (src/gguf/reader.rs:39-298)
+//   mlxq::gguf::convert, convert_file, remap_key
+//                              <- gguf::convert (src/gguf/convert.rs:80-262, 264-360)
 //   mlxq::snapshot::write_snapshot, save/load_safetensors, load_projection
 //                              <- snapshot::write_snapshot (src/snapshot.rs:86-148) and the
 //                                 pre-quantized loader branch (src/models/llama.rs:81-95)
@@ -24,6 +28,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <map>
 #include <memory>
 #include <optional>
 #include <stdexcept>
@@ -62,6 +67,9 @@ class Array {
 
   std::vector<float> to_f32() const;  // device -> host (F32 / F16 / BF16), synchronizes the stream
   std::vector<uint8_t> to_bytes() const;
+
+  // The same storage under another shape of the same element count.
+  Array reshape(std::vector<int64_t> shape) const;
 
   const std::vector<int64_t>& shape() const { return shape_; }
   int64_t dim(int i) const { return shape_.at(i < 0 ? shape_.size() + i : i); }
@@ -142,6 +150,94 @@ Array dequantize(uint32_t tag, const Array& data, size_t num_elements, DType out
 QuantizedLinear requantize_projection(uint32_t tag, const Array& data, int64_t rows, int64_t cols,
                                       int permute_heads, QuantSpec spec);
 
+// ---- GGUF container (src/gguf/reader.rs) ----
+
+// A typed metadata value (reader.rs:39-134).  Integers keep their width and
+// signedness in `type`; as_* follow the reference's conversions.
+struct MetaValue {
+  enum class Type { U8, I8, U16, I16, U32, I32, U64, I64, F32, F64, Bool, String, Array };
+  Type type = Type::U8;
+  uint64_t u = 0;  // unsigned and bool payloads
+  int64_t i = 0;   // signed payloads
+  double f = 0;    // float payloads (F32 widened exactly)
+  std::string s;
+  std::vector<MetaValue> arr;
+
+  std::optional<uint64_t> as_u64() const;  // any integer >= 0, bool
+  std::optional<int64_t> as_i64() const;   // any integer
+  std::optional<double> as_f64() const;    // F32 / F64
+  std::optional<std::string> as_str() const;
+  std::optional<bool> as_bool() const;
+  const std::vector<MetaValue>* as_array() const;
+};
+
+// One tensor of the header (reader.rs:137-156): shape in torch order (GGML
+// `ne` reversed), GGML type tag, offset into the data section.
+struct TensorInfo {
+  std::string name;
+  std::vector<int64_t> shape;
+  uint32_t ggml_type = 0;
+  uint64_t offset = 0;
+  int64_t num_elements() const;
+};
+
+// A parsed GGUF file (reader.rs:158-298): v2/v3 only (v1 -> Unsupported),
+// metadata, tensor table, data section at `general.alignment` (default 32).
+// open() maps the file read-only instead of reading it whole.
+class GgufFile {
+ public:
+  static GgufFile open(const std::string& path);
+  static GgufFile parse(std::vector<uint8_t> bytes);
+
+  const MetaValue* meta(const std::string& key) const;
+  std::optional<std::string> meta_str(const std::string& key) const;
+  std::optional<uint64_t> meta_u64(const std::string& key) const;
+  std::optional<double> meta_f64(const std::string& key) const;
+  // The tensor's raw block bytes (length from its type and element count);
+  // Msg error when they run past the end of the file.
+  std::pair<const uint8_t*, size_t> tensor_data(const TensorInfo& info) const;
+
+  std::map<std::string, MetaValue> metadata;
+  std::vector<TensorInfo> tensors;
+  uint64_t alignment = 32;
+  uint64_t data_start = 0;
+
+ private:
+  void parse_header();
+  std::shared_ptr<const uint8_t> base_;  // the image (owned vector or mapping)
+  size_t size_ = 0;
+};
+
+// ---- GGUF -> MLX snapshot (src/gguf/convert.rs) ----
+
+// GGML tensor name -> transformer key (convert.rs:213-242); nullopt for
+// names the engine does not load.
+std::optional<std::string> remap_key(const std::string& name);
+// Tensors the engine recomputes (rope frequencies; convert.rs:258-262).
+bool is_ignorable(const std::string& name);
+
+struct ConvertOptions {
+  std::optional<QuantSpec> quantize;        // requantize the projections
+  std::optional<std::string> tokenizer_json;  // written verbatim when given
+};
+
+struct ConvertReport {
+  std::string architecture, model_type;
+  size_t num_tensors = 0;
+  std::optional<QuantSpec> quantized;
+  std::string tokenizer;  // what happened to the tokenizer (not rebuilt from GGUF metadata here)
+  std::string out_dir;
+};
+
+// convert.rs:89-186.  Each mapped tensor's blocks go to the device once:
+// with `quantize`, projections run the fused requantize kernel (dequantize,
+// llama q/k un-permute, bf16, MLX affine quantize); every other tensor is
+// dequantized to bf16 (q/k of an unquantized llama conversion then have
+// their rows un-permuted).  Errors as the reference: Unsupported for another
+// architecture or an unmapped tensor, Msg for missing metadata.
+ConvertReport convert(const GgufFile& g, const std::string& out_dir, const ConvertOptions& opts);
+ConvertReport convert_file(const std::string& gguf_path, const std::string& out_dir, const ConvertOptions& opts);
+
 }  // namespace gguf
 
 // Quantized snapshot I/O (src/snapshot.rs): MLX's on-disk layout of a
@@ -168,6 +264,13 @@ struct Report {  // snapshot.rs:68-77
 Report write_snapshot(const std::string& out_dir, const Tensors& tensors, const std::string& config_json,
                       std::optional<QuantSpec> quantize, const std::optional<std::string>& tokenizer_json = {},
                       const std::optional<std::string>& tokenizer_config_json = {});
+
+// The writing half of write_snapshot: `tensors` already in their stored form
+// (projections as packed parts when `quantized` is set), which are written
+// with config.json (plus the quantization block) and the tokenizer files.
+Report write_parts(const std::string& out_dir, const Tensors& tensors, const std::string& config_json,
+                   std::optional<QuantSpec> quantized, const std::optional<std::string>& tokenizer_json = {},
+                   const std::optional<std::string>& tokenizer_config_json = {});
 
 void save_safetensors(const std::string& path, const Tensors& tensors);
 Tensors load_safetensors(const std::string& path);

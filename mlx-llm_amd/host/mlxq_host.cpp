@@ -128,6 +128,13 @@ Array::Array(std::vector<int64_t> shape, DType dtype) : shape_(std::move(shape))
   buf_ = std::shared_ptr<void>(p, [](void* q) { (void)hipFree(q); });
 }
 
+Array Array::reshape(std::vector<int64_t> shape) const {
+  Array r = *this;
+  r.shape_ = std::move(shape);
+  if (r.size() != size()) throw Error(Error::Kind::Msg, "reshape: element count differs");
+  return r;
+}
+
 int64_t Array::size() const {
   int64_t n = 1;
   for (int64_t d : shape_) n *= d;

@@ -2,6 +2,7 @@
 // mapping in mlxq.hpp): a standard safetensors reader / writer and the
 // snapshot writer's projection requant (src/snapshot.rs:86-148).
 #include <cctype>
+#include <cstdint>
 #include <cstring>
 #include <filesystem>
 #include <fstream>
@@ -77,8 +78,13 @@ struct Cursor {
     size_t j = i;
     if (j < s.size() && s[j] == '-') j++;
     while (j < s.size() && std::isdigit(static_cast<unsigned char>(s[j]))) j++;
-    if (j == i) msg("safetensors header: expected an integer");
-    const int64_t v = std::stoll(s.substr(i, j - i));
+    if (j == i || (j == i + 1 && s[i] == '-')) msg("safetensors header: expected an integer");
+    int64_t v = 0;
+    try {
+      v = std::stoll(s.substr(i, j - i));
+    } catch (const std::exception&) {
+      msg("safetensors header: integer out of range");
+    }
     i = j;
     return v;
   }
@@ -220,13 +226,23 @@ Tensors load_safetensors(const std::string& path) {
     if (c.peek(',')) c.i++;
   }
   const std::streamoff data0 = 8 + static_cast<std::streamoff>(n);
+  f.seekg(0, std::ios::end);
+  const int64_t data_len = static_cast<int64_t>(f.tellg()) - static_cast<int64_t>(data0);
   Tensors out;
   for (const Entry& e : entries) {
     const DType t = dtype_of(e.dtype);
+    // every bound checked before anything is sized from it: dimensions >= 0,
+    // no overflow of the element or byte count, 0 <= begin <= end <= data
+    const int64_t esz = static_cast<int64_t>(dtype_size(t));
     int64_t count = 1;
-    for (int64_t d : e.shape) count *= d;
-    if (e.end - e.begin != count * static_cast<int64_t>(dtype_size(t)) || e.begin < 0)
-      msg("safetensors: size of " + e.name + " does not match its shape");
+    for (int64_t d : e.shape) {
+      if (d < 0) msg("safetensors: negative dimension in the shape of " + e.name);
+      if (d != 0 && count > INT64_MAX / esz / d) msg("safetensors: shape of " + e.name + " is too large");
+      count *= d;
+    }
+    if (e.begin < 0 || e.end < e.begin || e.end > data_len)
+      msg("safetensors: data_offsets of " + e.name + " lie outside the file");
+    if (e.end - e.begin != count * esz) msg("safetensors: size of " + e.name + " does not match its shape");
     std::vector<uint8_t> bytes(static_cast<size_t>(e.end - e.begin));
     f.seekg(data0 + e.begin);
     if (!f.read(reinterpret_cast<char*>(bytes.data()), static_cast<std::streamsize>(bytes.size())))
@@ -239,7 +255,6 @@ Tensors load_safetensors(const std::string& path) {
 Report write_snapshot(const std::string& out_dir, const Tensors& tensors, const std::string& config_json,
                       std::optional<QuantSpec> quantize, const std::optional<std::string>& tokenizer_json,
                       const std::optional<std::string>& tokenizer_config_json) {
-  std::filesystem::create_directories(out_dir);
   Tensors out;
   for (const auto& [key, arr] : tensors) {
     if (quantize && is_projection(key)) {
@@ -253,15 +268,21 @@ Report write_snapshot(const std::string& out_dir, const Tensors& tensors, const 
       out.emplace_back(key, arr);
     }
   }
+  return write_parts(out_dir, out, config_json, quantize, tokenizer_json, tokenizer_config_json);
+}
 
+Report write_parts(const std::string& out_dir, const Tensors& out, const std::string& config_json,
+                   std::optional<QuantSpec> quantized, const std::optional<std::string>& tokenizer_json,
+                   const std::optional<std::string>& tokenizer_config_json) {
   std::string config = config_json;
   const size_t open = config.find_first_not_of(" \t\r\n"), close = config.find_last_not_of(" \t\r\n");
   if (open == std::string::npos || config[open] != '{' || config[close] != '}')
     throw Error(Error::Kind::Msg, "snapshot config.json is not a JSON object");
-  if (quantize) {
+  std::filesystem::create_directories(out_dir);
+  if (quantized) {
     const bool empty = config.find_first_not_of(" \t\r\n", open + 1) == close;
     config.insert(close, std::string(empty ? "" : ", ") + "\"quantization\": {\"group_size\": " +
-                             std::to_string(quantize->group_size) + ", \"bits\": " + std::to_string(quantize->bits) +
+                             std::to_string(quantized->group_size) + ", \"bits\": " + std::to_string(quantized->bits) +
                              "}");
   }
   write_file(out_dir + "/config.json", config);
@@ -270,7 +291,7 @@ Report write_snapshot(const std::string& out_dir, const Tensors& tensors, const 
   if (tokenizer_config_json) write_file(out_dir + "/tokenizer_config.json", *tokenizer_config_json);
   Report r;
   r.num_tensors = out.size();
-  r.quantized = quantize;
+  r.quantized = quantized;
   r.out_dir = out_dir;
   return r;
 }

@@ -37,6 +37,7 @@ _i64, _u32, _vp, _sz = ctypes.c_int64, ctypes.c_uint32, ctypes.c_void_p, ctypes.
 SIGNATURES = {
     "mlxq_last_error": (ctypes.c_char_p, []),
     "mlxq_version": (ctypes.c_char_p, []),
+    "mlxq_reload_overrides": (ctypes.c_int, []),
     "mlxq_quantize": (ctypes.c_int, [_vp, ctypes.c_int, _i64, _i64, ctypes.c_int, ctypes.c_int, _vp, _vp, _vp, _vp]),
     "mlxq_dequantize": (ctypes.c_int, [_vp, _vp, _vp, ctypes.c_int, _i64, _i64, ctypes.c_int, ctypes.c_int, _vp, _vp]),
     "mlxq_qmatmul_workspace_size": (ctypes.c_int, [_i64, _i64, _i64, ctypes.c_int, ctypes.c_int, ctypes.POINTER(_sz)]),
@@ -130,6 +131,11 @@ def check(rc: int) -> None:
 
 def version() -> str:
     return lib().mlxq_version().decode()
+
+
+def reload_overrides() -> None:
+    """Re-read the MLXQ_* kernel-override environment variables (read once otherwise)."""
+    check(lib().mlxq_reload_overrides())
 
 
 # ---------------------------------------------------------------- torch glue

@@ -156,17 +156,22 @@ class DecodeStack:
             self._plan = mlxq.DecodePlan(self.cfg.as_dict(), layers, self.norm, t(self.lm_head), self.device)
         return self._plan
 
-    def forward(self, b: int | None = None, fused: bool = True, persistent: bool = False):
+    def forward(self, b: int | None = None, fused: bool = True, persistent: bool = False, layers=None,
+                head: bool = True):
         """One decode step of b rows on the current stream: self.x[:b] -> self.logits[:b].
         fused: per layer, four launches of the fused decode kernel (norm + q/k/v,
         head repeat + o + residual, norm + gate/up + SwiGLU, down + residual)
         wherever it covers the shape; a call it does not cover (it rejects the
-        shape before launching anything) runs as the op-by-op chain."""
+        shape before launching anything) runs as the op-by-op chain.
+        layers (an iterable of layer indices, default all) and head=False run
+        part of the chain, for checking it layer by layer: without the head
+        the hidden state after the last layer run is returned."""
         if persistent:
             assert (self.batch if b is None else b) == 1, "the persistent step is batch 1"
+            assert layers is None and head, "the persistent step runs the whole chain"
             return self.persistent_plan().step(self.x[0], self.logits[0])
         if not fused:
-            return self._forward_ops(b)
+            return self._forward_ops(b, layers, head)
         c = self.cfg
         b = self.batch if b is None else b
         gs, bits = c.group_size, c.bits
@@ -187,9 +192,10 @@ class DecodeStack:
         # 3.01 -> 2.85 ms per step); q/k/v and o keep the fused forms (plain
         # calls there: 3.24 / 2.98 ms)
         split = {"mlp", "down"} if b > 4 else set()
-        for i, L in enumerate(self.layers):
+        for j, i in enumerate(range(len(self.layers)) if layers is None else layers):
+            L = self.layers[i]
             P = L.proj
-            xn = (self.xa if i % 2 == 0 else self.xb)[:b]
+            xn = (self.xa if j % 2 == 0 else self.xb)[:b]
 
             # where the single fused launch does not cover the shape (b > 4),
             # the norm / head repeat / SwiGLU run as their own kernels and the
@@ -227,12 +233,14 @@ class DecodeStack:
             else:
                 fz(a, [self._proj(P["down"], xn, res=h)], down)
             x = xn
+        if not head:
+            return x
 
-        def head(x=x):
+        def head_ops(x=x):
             mlxq.rms_norm(x, self.norm, c.eps, out=n)
             lin(n, self.lm_head, self.logits[:b])
 
-        fz(x, [self._proj(self.lm_head, self.logits[:b])], head, norm_weight=self.norm, eps=c.eps)
+        fz(x, [self._proj(self.lm_head, self.logits[:b])], head_ops, norm_weight=self.norm, eps=c.eps)
         return self.logits[:b]
 
     def _proj(self, p: QLinear, y, res=None):
@@ -241,14 +249,15 @@ class DecodeStack:
             d["residual"] = res
         return d
 
-    def _forward_ops(self, b: int | None = None):
+    def _forward_ops(self, b: int | None = None, layers=None, head: bool = True):
         c = self.cfg
         b = self.batch if b is None else b
         assert 1 <= b <= self.batch
         n, h, q, k, v, attn, o = (t[:b] for t in (self.n, self.h, self.q, self.k, self.v, self.attn, self.o))
         g, u, a, d = (t[:b] for t in (self.g, self.u, self.a, self.d))
         x = self.x[:b]
-        for i, L in enumerate(self.layers):
+        for j, i in enumerate(range(len(self.layers)) if layers is None else layers):
+            L = self.layers[i]
             P = L.proj
             mlxq.rms_norm(x, L.ln1, c.eps, out=n)
             self._lin(n, P["q"], q)
@@ -262,8 +271,10 @@ class DecodeStack:
             self._lin(n, P["up"], u)
             mlxq.silu_mul(g, u, out=a)
             self._lin(a, P["down"], d)
-            x = (self.xa if i % 2 == 0 else self.xb)[:b]
+            x = (self.xa if j % 2 == 0 else self.xb)[:b]
             mlxq.add(h, d, out=x)
+        if not head:
+            return x
         mlxq.rms_norm(x, self.norm, c.eps, out=n)
         self._lin(n, self.lm_head, self.logits[:b])
         return self.logits[:b]

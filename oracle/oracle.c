@@ -931,23 +931,41 @@ int orc_qmatmul_f64(const uint16_t* x, int64_t M, const uint32_t* wq,
   int rc = check_qargs(N, K, group_size, bits);
   if (rc) return rc;
   int64_t wpr = K * bits / 32, gpr = K / group_size;
+  int failed = 0;
+  /* each weight row is dequantized once (w = s*q + b in f64, exact) and
+   * then dotted with every activation row in k order */
 #ifdef _OPENMP
-#pragma omp parallel for schedule(static)
+#pragma omp parallel
 #endif
-  for (int64_t n = 0; n < N; n++) {
-    const uint32_t* row = wq + n * wpr;
-    for (int64_t m = 0; m < M; m++) {
-      double acc = 0.0;
+  {
+    double* w = (double*)malloc(sizeof(double) * (size_t)K);
+    if (!w) {
+#ifdef _OPENMP
+#pragma omp atomic write
+#endif
+      failed = 1;
+    }
+#ifdef _OPENMP
+#pragma omp for schedule(static)
+#endif
+    for (int64_t n = 0; n < N; n++) {
+      if (!w) continue;
+      const uint32_t* row = wq + n * wpr;
       for (int64_t k = 0; k < K; k++) {
         int64_t g = k / group_size;
-        double w = (double)orc_bf16_to_f32(scales[n * gpr + g]) * (double)code_at(row, k, bits) +
-                   (double)orc_bf16_to_f32(biases[n * gpr + g]);
-        acc += (double)orc_bf16_to_f32(x[m * K + k]) * w;
+        w[k] = (double)orc_bf16_to_f32(scales[n * gpr + g]) * (double)code_at(row, k, bits) +
+               (double)orc_bf16_to_f32(biases[n * gpr + g]);
       }
-      y[m * N + n] = acc;
+      for (int64_t m = 0; m < M; m++) {
+        const uint16_t* xr = x + m * K;
+        double acc = 0.0;
+        for (int64_t k = 0; k < K; k++) acc += (double)orc_bf16_to_f32(xr[k]) * w[k];
+        y[m * N + n] = acc;
+      }
     }
+    free(w);
   }
-  return 0;
+  return failed ? 4 : 0;
 }
 
 

@@ -244,6 +244,27 @@ def qlinear_bf16(x_bf16, w, group_size: int, bits: int) -> np.ndarray:
     return f32_to_bf16(y.astype(np.float32))
 
 
+def decode_layer(x_bf16, L, cfg) -> np.ndarray:
+    """One layer of the chain below (src/models/llama.rs:689-735 with the
+    identity attention): bf16 hidden state [M, hidden] in and out."""
+    gs, bits, eps = cfg["group_size"], cfg["bits"], cfg["eps"]
+    groups = cfg["heads"] // cfg["kv_heads"]
+    x = _u16(x_bf16)
+    n1 = rms_norm(x, L["ln1"], eps)
+    # q and k only feed attention, which the chain replaces: no effect on the output
+    v = qlinear_bf16(n1, L["v"], gs, bits)
+    attn = repeat_kv(v, cfg["kv_heads"], cfg["head_dim"], groups)
+    h = add(x, qlinear_bf16(attn, L["o"], gs, bits))
+    n2 = rms_norm(h, L["ln2"], eps)
+    a = silu_mul(qlinear_bf16(n2, L["gate"], gs, bits), qlinear_bf16(n2, L["up"], gs, bits))
+    return add(h, qlinear_bf16(a, L["down"], gs, bits))
+
+
+def decode_head(x_bf16, final_norm, lm_head, cfg) -> np.ndarray:
+    """Final norm and lm_head (src/models/llama.rs:595-603): bf16 logits."""
+    return qlinear_bf16(rms_norm(_u16(x_bf16), final_norm, cfg["eps"]), lm_head, cfg["group_size"], cfg["bits"])
+
+
 def decode_stack(x_bf16, layers, final_norm, lm_head, cfg) -> np.ndarray:
     """One decode step of the quantized Llama layer chain with attention replaced
     by the identity on v (GQA heads repeated): src/models/llama.rs:689-735
@@ -251,19 +272,10 @@ def decode_stack(x_bf16, layers, final_norm, lm_head, cfg) -> np.ndarray:
     lm_head).  layers: dicts with packed (wq, scales, biases) numpy triples
     under q, k, v, o, gate, up, down and bf16 norm weights ln1, ln2.
     Returns bf16 logits [M, vocab]."""
-    gs, bits, eps = cfg["group_size"], cfg["bits"], cfg["eps"]
-    groups = cfg["heads"] // cfg["kv_heads"]
     x = _u16(x_bf16)
     for L in layers:
-        n1 = rms_norm(x, L["ln1"], eps)
-        # q and k only feed attention, which the chain replaces: no effect on the output
-        v = qlinear_bf16(n1, L["v"], gs, bits)
-        attn = repeat_kv(v, cfg["kv_heads"], cfg["head_dim"], groups)
-        h = add(x, qlinear_bf16(attn, L["o"], gs, bits))
-        n2 = rms_norm(h, L["ln2"], eps)
-        a = silu_mul(qlinear_bf16(n2, L["gate"], gs, bits), qlinear_bf16(n2, L["up"], gs, bits))
-        x = add(h, qlinear_bf16(a, L["down"], gs, bits))
-    return qlinear_bf16(rms_norm(x, final_norm, eps), lm_head, gs, bits)
+        x = decode_layer(x, L, cfg)
+    return decode_head(x, final_norm, lm_head, cfg)
 
 
 def permute_inverse_qk(w: np.ndarray, n_head: int) -> np.ndarray:

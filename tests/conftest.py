@@ -33,3 +33,32 @@ def torch_gpu():
 
     assert torch.cuda.is_available(), "GPU test run without a visible GPU"
     return torch
+
+
+@pytest.fixture(autouse=True)
+def _kernel_overrides(monkeypatch):
+    """The library reads its MLXQ_* kernel overrides once; a test that sets or
+    removes one through monkeypatch has them read again, and again after the
+    environment is restored."""
+    import mlxq
+
+    set_env, del_env = monkeypatch.setenv, monkeypatch.delenv
+    touched = []
+
+    def setenv(name, value, prepend=None):
+        set_env(name, value, prepend)
+        if name.startswith("MLXQ_"):
+            touched.append(name)
+            mlxq.reload_overrides()
+
+    def delenv(name, raising=True):
+        del_env(name, raising)
+        if name.startswith("MLXQ_"):
+            touched.append(name)
+            mlxq.reload_overrides()
+
+    monkeypatch.setenv, monkeypatch.delenv = setenv, delenv
+    yield
+    monkeypatch.undo()
+    if touched:
+        mlxq.reload_overrides()

@@ -5,6 +5,7 @@
 //
 //   host_tests           run every case, print one line per case, exit 1 on any failure
 //   host_tests --list    print the case names only (touches no GPU)
+//   host_tests --cpu     run only the cases that touch no GPU (host parsing and checks)
 //   host_tests --copy-safetensors IN OUT   load IN, save it as OUT
 #include <cmath>
 #include <cstdio>
@@ -13,6 +14,7 @@
 #include <filesystem>
 #include <fstream>
 #include <sstream>
+#include <algorithm>
 #include <functional>
 #include <string>
 #include <vector>
@@ -487,6 +489,279 @@ void quantized_write_loads_through_prequantized_branch() {
   std::filesystem::remove_all(dir);
 }
 
+
+// ---------------------------------------------------------------- gguf/reader.rs
+
+// A GGUF image builder (the reference's tests build their images the same
+// way, reader.rs:397-430): little-endian header, metadata, tensor infos,
+// padding to the data alignment, data.
+struct GgufImage {
+  std::vector<uint8_t> b;
+  void u32(uint32_t v) {
+    for (int i = 0; i < 4; i++) b.push_back(static_cast<uint8_t>(v >> (8 * i)));
+  }
+  void u64(uint64_t v) {
+    for (int i = 0; i < 8; i++) b.push_back(static_cast<uint8_t>(v >> (8 * i)));
+  }
+  void str(const std::string& s) {
+    u64(s.size());
+    b.insert(b.end(), s.begin(), s.end());
+  }
+  void header(uint32_t version, uint64_t tensors, uint64_t meta) {
+    u32(0x46554747u);
+    u32(version);
+    u64(tensors);
+    u64(meta);
+  }
+  void pad(size_t align) {
+    while (b.size() % align) b.push_back(0);
+  }
+};
+
+// reader.rs:397-449 parse_minimal_gguf_roundtrip
+void gguf_parse_minimal_roundtrip() {
+  GgufImage g;
+  g.header(3, 1, 2);
+  g.str("general.architecture");
+  g.u32(8);
+  g.str("llama");
+  g.str("llama.block_count");
+  g.u32(4);
+  g.u32(7);
+  g.str("w");
+  g.u32(2);
+  g.u64(3);
+  g.u64(2);
+  g.u32(0);
+  g.u64(0);
+  g.pad(32);
+  const float vals[6] = {1, 2, 3, 4, 5, 6};
+  for (float v : vals) {
+    uint32_t u;
+    std::memcpy(&u, &v, 4);
+    g.u32(u);
+  }
+  const gguf::GgufFile f = gguf::GgufFile::parse(g.b);
+  EXPECT(f.meta_str("general.architecture") == std::string("llama"));
+  EXPECT(f.meta_u64("llama.block_count") == uint64_t(7));
+  EXPECT(f.tensors.size() == 1);
+  const gguf::TensorInfo& t = f.tensors[0];
+  EXPECT(t.name == "w");
+  EXPECT((t.shape == std::vector<int64_t>{2, 3}));  // ne reversed
+  EXPECT(t.num_elements() == 6);
+  const auto [p, n] = f.tensor_data(t);
+  EXPECT(n == 24);
+  EXPECT(std::memcmp(p, vals, 24) == 0);
+}
+
+// reader.rs:451-459 rejects_bad_magic, :461-469 rejects_v1
+void gguf_rejects_bad_magic_and_v1() {
+  GgufImage bad;
+  bad.u32(0xdeadbeefu);
+  bad.u32(3);
+  bad.u64(0);
+  bad.u64(0);
+  expect_error(Error::Kind::Msg, [&] { gguf::GgufFile::parse(bad.b); });
+  GgufImage v1;
+  v1.header(1, 0, 0);
+  expect_error(Error::Kind::Unsupported, [&] { gguf::GgufFile::parse(v1.b); });
+  GgufImage v4;
+  v4.header(4, 0, 0);
+  expect_error(Error::Kind::Unsupported, [&] { gguf::GgufFile::parse(v4.b); });
+  GgufImage v2;  // v2 shares the u64 layout
+  v2.header(2, 0, 0);
+  EXPECT(gguf::GgufFile::parse(v2.b).tensors.empty());
+}
+
+// reader.rs:471-500 parses_int_and_float_and_array_metadata
+void gguf_parses_int_float_array_metadata() {
+  GgufImage g;
+  g.header(3, 0, 3);
+  g.str("a.f32");
+  g.u32(6);
+  const float f = 1.5f;
+  uint32_t u;
+  std::memcpy(&u, &f, 4);
+  g.u32(u);
+  g.str("a.i64");
+  g.u32(11);
+  g.u64(static_cast<uint64_t>(int64_t(-42)));
+  g.str("a.arr");
+  g.u32(9);
+  g.u32(4);
+  g.u64(2);
+  g.u32(10);
+  g.u32(20);
+  const gguf::GgufFile h = gguf::GgufFile::parse(g.b);
+  EXPECT(h.meta_f64("a.f32") == 1.5);
+  EXPECT(h.meta("a.i64")->as_i64() == int64_t(-42));
+  EXPECT(!h.meta("a.i64")->as_u64());  // a negative integer has no u64 reading
+  const auto* arr = h.meta("a.arr")->as_array();
+  EXPECT(arr && arr->size() == 2);
+  EXPECT((*arr)[0].as_u64() == uint64_t(10) && (*arr)[1].as_u64() == uint64_t(20));
+}
+
+// The reader's error paths (reader.rs:206-211 dims, :240-244 data start,
+// :282-298 tensor_data bounds, :321-329 truncation, :361-367 nested arrays,
+// :375-377 unknown value types) and general.alignment (:231-236).
+void gguf_reader_errors_and_alignment() {
+  auto tensor_file = [](uint32_t n_dims, uint64_t offset, uint64_t align) {
+    GgufImage g;
+    g.header(3, 1, align ? 1 : 0);
+    if (align) {
+      g.str("general.alignment");
+      g.u32(4);
+      g.u32(static_cast<uint32_t>(align));
+    }
+    g.str("t");
+    g.u32(n_dims);
+    for (uint32_t d = 0; d < n_dims; d++) g.u64(4);
+    g.u32(0);
+    g.u64(offset);
+    g.pad(align ? align : 32);
+    for (int i = 0; i < 64; i++) g.u32(i);  // 256 bytes of data
+    return g.b;
+  };
+  expect_error(Error::Kind::Msg, [&] { gguf::GgufFile::parse(tensor_file(0, 0, 0)); });
+  expect_error(Error::Kind::Msg, [&] { gguf::GgufFile::parse(tensor_file(5, 0, 0)); });
+  {  // 4x4 f32 = 64 bytes at offset 192 ends at 256: in range; at 200: not
+    const gguf::GgufFile ok = gguf::GgufFile::parse(tensor_file(2, 192, 0));
+    EXPECT(ok.tensor_data(ok.tensors[0]).second == 64);
+    const gguf::GgufFile past = gguf::GgufFile::parse(tensor_file(2, 200, 0));
+    expect_error(Error::Kind::Msg, [&] { past.tensor_data(past.tensors[0]); });
+  }
+  {  // general.alignment = 64 moves the data section to the next multiple of 64
+    const gguf::GgufFile a = gguf::GgufFile::parse(tensor_file(1, 0, 64));
+    EXPECT(a.alignment == 64 && a.data_start % 64 == 0);
+    EXPECT(std::memcmp(a.tensor_data(a.tensors[0]).first, "\0\0\0\0\1\0\0\0", 8) == 0);
+  }
+  {  // truncated anywhere in the header
+    const std::vector<uint8_t> full = tensor_file(2, 0, 0);
+    for (size_t cut : {size_t(3), size_t(20), size_t(30), size_t(40)}) {
+      std::vector<uint8_t> t(full.begin(), full.begin() + cut);
+      expect_error(Error::Kind::Msg, [&] { gguf::GgufFile::parse(t); });
+    }
+  }
+  {  // nested array: Unsupported; unknown value type: Msg; bad utf-8: Msg
+    GgufImage g;
+    g.header(3, 0, 1);
+    g.str("n");
+    g.u32(9);
+    g.u32(9);
+    g.u64(0);
+    expect_error(Error::Kind::Unsupported, [&] { gguf::GgufFile::parse(g.b); });
+    GgufImage h;
+    h.header(3, 0, 1);
+    h.str("x");
+    h.u32(13);
+    expect_error(Error::Kind::Msg, [&] { gguf::GgufFile::parse(h.b); });
+    GgufImage k;
+    k.header(3, 0, 1);
+    k.str(std::string("\xC3\x28", 2));
+    k.u32(0);
+    k.b.push_back(1);
+    expect_error(Error::Kind::Msg, [&] { gguf::GgufFile::parse(k.b); });
+    GgufImage big;  // an array count far past the end of the image
+    big.header(3, 0, 1);
+    big.str("a");
+    big.u32(9);
+    big.u32(0);
+    big.u64(uint64_t(1) << 60);
+    expect_error(Error::Kind::Msg, [&] { gguf::GgufFile::parse(big.b); });
+  }
+  {  // a metadata-only file may end before the aligned boundary
+    GgufImage g;
+    g.header(3, 0, 1);
+    g.str("k");
+    g.u32(0);
+    g.b.push_back(1);
+    EXPECT(gguf::GgufFile::parse(g.b).meta_u64("k") == uint64_t(1));
+  }
+}
+
+// ---------------------------------------------------------------- gguf/convert.rs
+
+// convert.rs:366-371 remaps_non_layer_keys, :373-395 remaps_layer_keys,
+// :425-432 unknown_keys_and_ignorables
+void gguf_remap_keys_and_ignorables() {
+  EXPECT(gguf::remap_key("token_embd.weight") == std::string("model.embed_tokens.weight"));
+  EXPECT(gguf::remap_key("output_norm.weight") == std::string("model.norm.weight"));
+  EXPECT(gguf::remap_key("output.weight") == std::string("lm_head.weight"));
+  EXPECT(gguf::remap_key("blk.0.attn_q.weight") == std::string("model.layers.0.self_attn.q_proj.weight"));
+  EXPECT(gguf::remap_key("blk.13.ffn_down.weight") == std::string("model.layers.13.mlp.down_proj.weight"));
+  EXPECT(gguf::remap_key("blk.5.attn_norm.weight") == std::string("model.layers.5.input_layernorm.weight"));
+  EXPECT(gguf::remap_key("blk.5.ffn_norm.weight") ==
+         std::string("model.layers.5.post_attention_layernorm.weight"));
+  EXPECT(gguf::remap_key("blk.2.attn_q_norm.weight") == std::string("model.layers.2.self_attn.q_norm.weight"));
+  EXPECT(!gguf::remap_key("blk.0.some_future_tensor.weight"));
+  EXPECT(!gguf::remap_key("rope_freqs.weight"));
+  EXPECT(!gguf::remap_key("blk.x.attn_q.weight") && !gguf::remap_key("blk..attn_q.weight"));
+  EXPECT(gguf::is_ignorable("rope_freqs.weight"));
+  EXPECT(gguf::is_ignorable("blk.0.rope_freqs.weight"));
+  EXPECT(!gguf::is_ignorable("blk.0.attn_q.weight"));
+}
+
+// convert.rs:96-147: unsupported architecture and unmapped tensors are
+// refused before any tensor is decoded (host-only paths).
+void gguf_convert_refuses_before_decoding() {
+  GgufImage g;
+  g.header(3, 0, 1);
+  g.str("general.architecture");
+  g.u32(8);
+  g.str("gpt2");
+  expect_error(Error::Kind::Unsupported, [&] { gguf::convert(gguf::GgufFile::parse(g.b), "/nonexistent", {}); });
+  GgufImage h;
+  h.header(3, 1, 2);
+  h.str("general.architecture");
+  h.u32(8);
+  h.str("llama");
+  h.str("llama.attention.head_count");
+  h.u32(4);
+  h.u32(2);
+  h.str("blk.0.mystery.weight");
+  h.u32(1);
+  h.u64(4);
+  h.u32(0);
+  h.u64(0);
+  h.pad(32);
+  for (int i = 0; i < 4; i++) h.u32(0);
+  expect_error(Error::Kind::Unsupported, [&] { gguf::convert(gguf::GgufFile::parse(h.b), "/nonexistent", {}); });
+  GgufImage m;  // missing head count
+  m.header(3, 0, 1);
+  m.str("general.architecture");
+  m.u32(8);
+  m.str("llama");
+  expect_error(Error::Kind::Msg, [&] { gguf::convert(gguf::GgufFile::parse(m.b), "/nonexistent", {}); });
+}
+
+// load_safetensors refuses malformed headers before sizing anything from
+// them: negative dimensions, element counts that overflow, offsets outside
+// the file or reversed.
+void safetensors_rejects_malformed_headers() {
+  const std::string dir = tmp_dir("st_bad");
+  auto write = [&](const std::string& header, size_t data_bytes) {
+    std::string h = header;
+    while (h.size() % 8) h += ' ';
+    std::ofstream f(dir + "/x.safetensors", std::ios::binary);
+    const uint64_t n = h.size();
+    for (int i = 0; i < 8; i++) f.put(static_cast<char>(n >> (8 * i)));
+    f << h << std::string(data_bytes, '\0');
+  };
+  const std::pair<std::string, size_t> bad[] = {
+      {R"({"t": {"dtype": "F32", "shape": [-1], "data_offsets": [0, 0]}})", 16},
+      {R"({"t": {"dtype": "F32", "shape": [-2], "data_offsets": [8, 0]}})", 16},
+      {R"({"t": {"dtype": "F32", "shape": [4611686018427387904, 4], "data_offsets": [0, 0]}})", 16},
+      {R"({"t": {"dtype": "F32", "shape": [2], "data_offsets": [8, 0]}})", 16},
+      {R"({"t": {"dtype": "F32", "shape": [8], "data_offsets": [0, 32]}})", 16},
+      {R"({"t": {"dtype": "F32", "shape": [2], "data_offsets": [-8, 0]}})", 16},
+  };
+  for (const auto& [h, n] : bad) {
+    write(h, n);
+    expect_error(Error::Kind::Msg, [&] { mlxq::snapshot::load_safetensors(dir + "/x.safetensors"); });
+  }
+  std::filesystem::remove_all(dir);
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -512,7 +787,21 @@ int main(int argc, char** argv) {
       {"projection_predicate_selects_only_attn_mlp_projections", projection_predicate_selects_only_attn_mlp_projections},
       {"dense_write_round_trips_bit_identical", dense_write_round_trips_bit_identical},
       {"quantized_write_loads_through_prequantized_branch", quantized_write_loads_through_prequantized_branch},
+      {"gguf_parse_minimal_roundtrip", gguf_parse_minimal_roundtrip},
+      {"gguf_rejects_bad_magic_and_v1", gguf_rejects_bad_magic_and_v1},
+      {"gguf_parses_int_float_array_metadata", gguf_parses_int_float_array_metadata},
+      {"gguf_reader_errors_and_alignment", gguf_reader_errors_and_alignment},
+      {"gguf_remap_keys_and_ignorables", gguf_remap_keys_and_ignorables},
+      {"gguf_convert_refuses_before_decoding", gguf_convert_refuses_before_decoding},
+      {"safetensors_rejects_malformed_headers", safetensors_rejects_malformed_headers},
   };
+  // cases that touch no GPU (run by the CPU test suite with --cpu)
+  const std::vector<std::string> host_only = {
+      "projection_predicate_selects_only_attn_mlp_projections", "gguf_parse_minimal_roundtrip",
+      "gguf_rejects_bad_magic_and_v1", "gguf_parses_int_float_array_metadata", "gguf_reader_errors_and_alignment",
+      "gguf_remap_keys_and_ignorables", "gguf_convert_refuses_before_decoding",
+      "safetensors_rejects_malformed_headers"};
+  const bool cpu_only = argc > 1 && std::strcmp(argv[1], "--cpu") == 0;
   if (argc == 4 && std::strcmp(argv[1], "--copy-safetensors") == 0) {
     // interop check driven from Python: read a file the safetensors package
     // wrote, write it back through this library
@@ -524,7 +813,10 @@ int main(int argc, char** argv) {
     return 0;
   }
   int failed = 0;
+  size_t ran = 0;
   for (const auto& c : cases) {
+    if (cpu_only && std::find(host_only.begin(), host_only.end(), c.first) == host_only.end()) continue;
+    ran++;
     try {
       c.second();
       std::printf("ok %s\n", c.first);
@@ -537,6 +829,6 @@ int main(int argc, char** argv) {
     }
     std::fflush(stdout);
   }
-  std::printf("%zu cases, %d failed\n", cases.size(), failed);
+  std::printf("%zu cases, %d failed\n", ran, failed);
   return failed ? 1 : 0;
 }

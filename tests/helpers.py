@@ -39,3 +39,13 @@ def host(t) -> np.ndarray:
 def rel_err(y: np.ndarray, ref: np.ndarray) -> float:
     """max |y - ref| / max |ref| (the max-relative-error figure the parity bar uses)."""
     return float(np.max(np.abs(y.astype(np.float64) - ref)) / max(np.max(np.abs(ref)), 1e-30))
+
+
+def rel_err_elem(y: np.ndarray, ref: np.ndarray, floor: float = 1e-3) -> float:
+    """max over elements of |y - ref| / |ref|, leaving out elements with
+    |ref| < floor * max |ref| (near-zero references, where a relative error
+    says nothing); reported beside rel_err."""
+    ref = np.asarray(ref, dtype=np.float64)
+    a = np.abs(ref)
+    keep = a >= floor * max(a.max(), 1e-30)
+    return float(np.max(np.abs(y.astype(np.float64)[keep] - ref[keep]) / a[keep]))

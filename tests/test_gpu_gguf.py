@@ -94,3 +94,37 @@ def test_config4_full_tensor(torch_gpu, tag):
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
     got_bf16 = gpu_dequant(tag, blocks, n, torch_gpu.bfloat16)
     assert np.array_equal(got_bf16, orc.f32_to_bf16(ref))
+
+
+@pytest.mark.parametrize("tag", DEVICE_TAGS)
+def test_random_blocks_any_f16_scale(torch_gpu, tag):
+    """Unrestricted block bytes: f16 scales negative, subnormal, infinite or
+    NaN (the reference decodes them through half::f16::to_f32 and passes
+    them on, dequant.rs:222-225).  Every non-NaN output is bit-exact.  Where
+    the output is NaN, the oracle's is too; a NaN that propagates from a NaN
+    scale keeps its payload bit for bit; one that an operation creates
+    (inf - inf, 0 * inf) is the platform's default NaN, which differs in the
+    sign bit between x86 and this GPU, so those are compared as NaN only.
+    Types whose outputs combine two f16 scales (d and dmin: Q4_1, Q5_1, Q2_K,
+    Q4_K, Q5_K) can meet two NaN operands in one operation; IEEE 754 leaves
+    which payload survives to the implementation, so there only the NaN
+    positions are compared."""
+    e, b = orc.gguf_block(tag)
+    nblk = 2048 // e * 3 + 7
+    raw = np.random.default_rng(1000 + tag).integers(0, 256, size=nblk * b, dtype=np.uint8)
+    n = e * nblk
+    ref = orc.gguf_dequantize(tag, raw, n).view(np.uint32)
+    got = gpu_dequant(tag, raw, n).view(np.uint32)
+    rn = (ref & 0x7FFFFFFF) > 0x7F800000
+    gn = (got & 0x7FFFFFFF) > 0x7F800000
+    assert np.array_equal(rn, gn)
+    assert np.array_equal(got[~rn], ref[~rn])
+    if tag not in (3, 7, 10, 12, 13):
+        created = (ref[rn] & 0x7FFFFFFF) == 0x7FC00000  # a default NaN, either sign
+        assert np.array_equal(got[rn][~created], ref[rn][~created])
+        assert np.all((got[rn][created] & 0x7FFFFFFF) == 0x7FC00000)
+    got_bf16 = gpu_dequant(tag, raw, n, torch_gpu.bfloat16)
+    want_bf16 = orc.f32_to_bf16(ref.view(np.float32))
+    bn = (want_bf16 & 0x7FFF) > 0x7F80
+    assert np.array_equal((got_bf16 & 0x7FFF) > 0x7F80, bn)
+    assert np.array_equal(got_bf16[~bn], want_bf16[~bn])

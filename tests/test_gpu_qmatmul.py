@@ -7,11 +7,12 @@ import pytest
 
 import mlxq
 import oracle as orc
-from helpers import bf16_acts, bf16_weights, dev, host, rel_err
+from helpers import bf16_acts, bf16_weights, dev, host, rel_err, rel_err_elem
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-2
 TIGHT = 4e-3     # what the kernels actually achieve (bf16 output rounding ~2e-3)
+ELEM_TOL = 2e-2  # element-wise |y - ref| / |ref| over outputs >= 1% of the largest
 LLAMA = {"q_o": (4096, 4096), "k_v": (4096, 1024), "gate_up": (4096, 14336), "down": (14336, 4096)}
 
 
@@ -58,8 +59,13 @@ def test_qmv_llama_shapes(torch_gpu, bits, name, m):
     ref = orc.qmatmul_f64(x, wq, s, b, 64, bits)
     y = run(x, wq, s, b, 64, bits)
     err = rel_err(y, ref)
+    # element-wise relative error beside the max-normalised bar, over the
+    # outputs at least 1% of the largest (bf16 output rounding is 2^-9)
+    elem = rel_err_elem(y, ref, floor=1e-2)
+    print(f"Q{bits} {name} M={m}: rel_err {err:.2e}, elementwise {elem:.2e}")
     assert err <= TIGHT, err
     assert err <= TOL
+    assert elem <= ELEM_TOL, elem
 
 
 def test_qmv_config1_single_decode(torch_gpu):
@@ -69,6 +75,7 @@ def test_qmv_config1_single_decode(torch_gpu):
     ref = orc.qmatmul_f64(x, wq, s, b, 64, 4)
     y = run(x, wq, s, b, 64, 4)
     assert rel_err(y, ref) <= TIGHT
+    assert rel_err_elem(y, ref, floor=1e-2) <= ELEM_TOL
 
 
 def test_qmv_repeat_reuses_workspace(torch_gpu):
@@ -151,6 +158,12 @@ def test_qmm_config3_prefill(torch_gpu, name):
     rows = np.sort(np.random.default_rng(3).choice(2048, 64, replace=False))
     ref = orc.qmatmul_f64(x[rows], wq, s, b, 64, 4)
     err = rel_err(y[rows], ref)
+    elem = rel_err_elem(y[rows], ref, floor=1e-2)
+    # reported, not asserted: the prefill path rounds each dequantized
+    # weight to bf16 (the values MLX's qmm stages), and with the x20 outlier
+    # channels the largest outputs are far above the typical one, so the
+    # outputs near 1% of the largest carry relative errors of several %
+    print(f"prefill {name}: rel_err {err:.2e}, elementwise {elem:.2e}")
     assert err <= TIGHT, err
 
 

@@ -102,55 +102,3 @@ def test_tile_graph_replay(torch_gpu, tile_all):
         assert torch.equal(c.out, e), f"replay {i}"
         mlxq.qmatmul(x[:8], *d, 64, 4)
         torch.cuda.synchronize()
-
-
-@pytest.mark.parametrize("bits", [4, 8])
-@pytest.mark.parametrize("cfg", ["4,4", "8,8", "8,16"])
-@pytest.mark.parametrize("m", [3, 17, 32])
-def test_tile_fused_sum_matches_reduce_launch(torch_gpu, tile_all, bits, cfg, m):
-    """MLXQ_QMV_SPLIT_FUSED=1: the split-K slices added in-kernel by each tile's last arriving slice
-    equal, bit for bit, the separate reduce launch (the same split-order sum),
-    on several calls in a row (the arrival counters reset themselves), with a
-    bias and ragged M and N."""
-    tile_all.setenv("MLXQ_QMV_TILE", cfg)
-    n, k = 328, 4096
-    wq, s, b = make_layer(80 + bits, n, k, 64, bits)
-    x = bf16_acts(81 + m, m, k)
-    bias = orc.f32_to_bf16(np.random.default_rng(82).normal(0, 1, n).astype(np.float32))
-    tile_all.delenv("MLXQ_QMV_SPLIT_FUSED", raising=False)
-    want = run(x, wq, s, b, 64, bits, bias=bias)
-    tile_all.setenv("MLXQ_QMV_SPLIT_FUSED", "1")
-    for i in range(4):
-        assert np.array_equal(run(x, wq, s, b, 64, bits, bias=bias), want), i
-    ref = orc.qmatmul_f64(x, wq, s, b, 64, bits) + orc.bf16_to_f32(bias)[None, :].astype(np.float64)
-    assert rel_err(want, ref) <= TIGHT
-
-
-def test_tile_fused_sum_two_streams(torch_gpu, tile_all):
-    """Calls queued on two streams at once use separate arrival-counter slots
-    and separate outputs/workspaces; each matches its single-stream result."""
-    torch = torch_gpu
-    tile_all.setenv("MLXQ_QMV_SPLIT_FUSED", "1")
-    k, n, m = 4096, 1024, 32
-    la = make_layer(90, n, k, 64, 4)
-    lb = make_layer(91, n, k, 64, 8)
-    xa, xb = bf16_acts(92, m, k), bf16_acts(93, m, k)
-    want_a, want_b = run(xa, *la, 64, 4), run(xb, *lb, 64, 8)
-    ta = [dev(xa, bf16=True), dev(la[0]), dev(la[1], bf16=True), dev(la[2], bf16=True)]
-    tb = [dev(xb, bf16=True), dev(lb[0]), dev(lb[1], bf16=True), dev(lb[2], bf16=True)]
-    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
-    torch.cuda.synchronize()
-    with torch.cuda.stream(s1):
-        ca = mlxq.bind_qmatmul(*ta, 64, 4)
-    ws_b = torch.zeros(mlxq.workspace_size(m, n, k, 64, 8), dtype=torch.uint8, device="cuda:0")
-    yb = torch.empty((m, n), dtype=torch.bfloat16, device="cuda:0")
-    f = mlxq.lib().mlxq_qmatmul_algo
-    for _ in range(8):
-        with torch.cuda.stream(s1):
-            ca()
-        with torch.cuda.stream(s2):
-            mlxq.check(f(mlxq._ptr(tb[0]), m, mlxq._ptr(tb[1]), mlxq._ptr(tb[2]), mlxq._ptr(tb[3]), None, n, k,
-                         64, 8, mlxq._ptr(yb), mlxq._ptr(ws_b), ws_b.numel(), mlxq.ALGO_AUTO, s2.cuda_stream))
-    torch.cuda.synchronize()
-    assert np.array_equal(orc.bf16_to_f32(host(ca.out)), want_a)
-    assert np.array_equal(orc.bf16_to_f32(host(yb)), want_b)

@@ -17,7 +17,19 @@ CASES = [
     "requantize_projection_undoes_qk_permute",
     "projection_predicate_selects_only_attn_mlp_projections", "dense_write_round_trips_bit_identical",
     "quantized_write_loads_through_prequantized_branch",
+    "gguf_parse_minimal_roundtrip", "gguf_rejects_bad_magic_and_v1", "gguf_parses_int_float_array_metadata",
+    "gguf_reader_errors_and_alignment", "gguf_remap_keys_and_ignorables", "gguf_convert_refuses_before_decoding",
+    "safetensors_rejects_malformed_headers",
 ]
+
+
+def test_host_only_cases_pass_on_cpu():
+    """The host-only cases (GGUF reader and convert refusals, safetensors
+    header checks, the projection predicate) run here without a GPU."""
+    r = subprocess.run([str(BIN), "--cpu"], capture_output=True, text=True, timeout=120)
+    print(r.stdout)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "8 cases, 0 failed" in r.stdout
 
 
 def test_host_tests_built_and_listed():
