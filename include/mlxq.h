@@ -127,6 +127,27 @@ int mlxq_qmatmul_algo(const void* x, int64_t M, const uint32_t* wq,
                       int group_size, int bits, void* y, void* workspace,
                       size_t workspace_bytes, int algo, void* stream);
 
+/* mlxq_qmatmul for callers that cannot allocate or pass a workspace (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference.  Same kernels and results as
+ * mlxq_qmatmul with a workspace of mlxq_qmatmul_workspace_size bytes, but
+ * the split-K partial sums live in a fixed library scratch array in device
+ * memory (mlxq_qmatmul_noalloc_max_scratch() bytes, 64 MiB, held by every
+ * device the library runs on until the process ends); nothing is allocated.
+ * A shape whose workspace size exceeds the scratch returns
+ * MLXQ_ERR_WORKSPACE before any launch (e.g. a 4096 -> 128256 lm_head at
+ * M = 32: 16 x M x N x 4 bytes).
+ * All calls on one device share its scratch: calls that can overlap in time
+ * on one device (two streams, two threads) race and must be serialized by
+ * the caller. */
+int mlxq_qmatmul_noalloc(const void* x, int64_t M, const uint32_t* wq,
+                         const void* scales, const void* biases,
+                         const void* bias_vec, int64_t N, int64_t K,
+                         int group_size, int bits, void* y, void* stream);
+
+/* Size in bytes of mlxq_qmatmul_noalloc's scratch array. */
+size_t mlxq_qmatmul_noalloc_max_scratch(void);
+
 /* One projection of a fused decode call (mlxq_qmatmul_fused). */
 typedef struct {
   const uint32_t* wq;    /* [N, K*bits/32] packed codes                     */

@@ -2,6 +2,7 @@
 // qmv / qmm choice (MLX makes the same choice from M inside quantized_matmul).
 #include <hip/hip_runtime.h>
 
+#include <mutex>
 #include <string>
 
 #include "common.hpp"
@@ -193,3 +194,64 @@ extern "C" int mlxq_qmatmul_fused(const void* x, int64_t M, int64_t K, const voi
   return launch_qmv_dot_fused(f, as_stream(stream));
 }
 
+// ---------------------------------------------------------------- no-alloc
+
+namespace {
+
+// Library-owned scratch of the allocation-free entry point: the split-K
+// partial sums mlxq_qmatmul keeps in the caller's workspace.  Each device
+// holds its own copy for the life of the process.  In host code `scratch`
+// is only a handle for hipGetSymbolAddress: kernels receive the per-device
+// address it returns.
+constexpr size_t kScratchBytes = size_t(64) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+void* g_scratch_ptr[kMaxDevices] = {};
+std::mutex g_scratch_mu;
+
+// This device's address of `scratch`, looked up once per device (with that
+// device current) and kept.
+int scratch_ptr(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(MLXQ_ERR_DEVICE, std::string("qmatmul_noalloc: hipGetDevice: ") + hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(MLXQ_ERR_DEVICE, "qmatmul_noalloc: device index out of range");
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(MLXQ_ERR_DEVICE, std::string("qmatmul_noalloc: hipGetSymbolAddress: ") + hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return MLXQ_OK;
+}
+
+}  // namespace
+
+extern "C" size_t mlxq_qmatmul_noalloc_max_scratch(void) { return kScratchBytes; }
+
+extern "C" int mlxq_qmatmul_noalloc(const void* x, int64_t M, const uint32_t* wq, const void* scales,
+                                    const void* biases, const void* bias_vec, int64_t N, int64_t K, int group_size,
+                                    int bits, void* y, void* stream) {
+  clear_error();
+  size_t need = 0;
+  int rc = mlxq_qmatmul_workspace_size(M, N, K, group_size, bits, &need);
+  if (rc) return rc;
+  if (need > kScratchBytes)
+    return fail(MLXQ_ERR_WORKSPACE, "qmatmul_noalloc: this shape needs " + std::to_string(need) +
+                                        " bytes of scratch; the library's fixed scratch holds " +
+                                        std::to_string(kScratchBytes) + " (use mlxq_qmatmul with a workspace)");
+  void* ws = nullptr;
+  if (need) {
+    rc = scratch_ptr(&ws);
+    if (rc) return rc;
+  }
+  // the same kernels as mlxq_qmatmul with a workspace of exactly `need`
+  // bytes; every partial they read back is written earlier in the same
+  // call, so the scratch needs no clearing
+  return mlxq_qmatmul_algo(x, M, wq, scales, biases, bias_vec, N, K, group_size, bits, y, ws, need, MLXQ_ALGO_AUTO,
+                           stream);
+}

@@ -43,6 +43,9 @@ SIGNATURES = {
     "mlxq_qmatmul_workspace_size": (ctypes.c_int, [_i64, _i64, _i64, ctypes.c_int, ctypes.c_int, ctypes.POINTER(_sz)]),
     "mlxq_qmatmul": (ctypes.c_int, [_vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, ctypes.c_int, ctypes.c_int, _vp, _vp, _sz, _vp]),
     "mlxq_qmatmul_algo": (ctypes.c_int, [_vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, ctypes.c_int, ctypes.c_int, _vp, _vp, _sz, ctypes.c_int, _vp]),
+    "mlxq_qmatmul_noalloc": (ctypes.c_int, [_vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, ctypes.c_int, ctypes.c_int,
+                                            _vp, _vp]),
+    "mlxq_qmatmul_noalloc_max_scratch": (_sz, []),
     "mlxq_qmatmul_fused": (ctypes.c_int, [_vp, _i64, _i64, _vp, ctypes.c_float, ctypes.c_int, ctypes.c_int,
                                           ctypes.c_int, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                           ctypes.c_int, _vp]),
