@@ -33,7 +33,10 @@ COMMON = [
     f"-I{ROOT / 'include'}", f"-I{CSRC}",
 ]
 NO_CONTRACT = {"gguf.hip", "affine.hip", "gguf_requant.hip"}
-
+# MFMA results in ordinary VGPRs (no accumulator-register copies before the
+# per-group fold): the batched-decode kernels' results are read by the VALU
+# after every group, so the copies were pure overhead there
+MFMA_VGPR = {"qmv_tile.hip"}
 
 
 def sources() -> list[Path]:
@@ -48,6 +51,8 @@ def compile_one(src: Path, verbose: bool) -> Path:
     cmd = [HIPCC, *COMMON]
     if src.name in NO_CONTRACT:
         cmd.append("-ffp-contract=off")
+    if src.name in MFMA_VGPR:
+        cmd += ["-mllvm", "-amdgpu-mfma-vgpr-form"]
     if src.suffix == ".cpp":
         cmd += ["-x", "hip"]  # host files include hip_runtime for stream types
     cmd += ["-c", str(src), "-o", str(obj)]

@@ -47,7 +47,7 @@ const Overrides* read_overrides() {
   o->qmv_legacy = flag("MLXQ_QMV_LEGACY");
   o->qmv_stream = flag("MLXQ_QMV_STREAM");
   o->qmv_narrow = flag("MLXQ_QMV_NARROW");
-  pair("MLXQ_QMV_TILE", &o->tile_wv, &o->tile_nch);
+  if (const char* e = getenv("MLXQ_QMV_TILE")) sscanf(e, "%d,%d,%d", &o->tile_wv, &o->tile_nch, &o->tile_kh);
   pair("MLXQ_QMV_DOT", &o->dot_sub, &o->dot_wv);
   pair("MLXQ_QMV_MFMA_CFG", &o->mfma_sub, &o->mfma_wv);
   o->qmv_sub = num("MLXQ_QMV_SUB");

@@ -22,7 +22,7 @@ int check_launch(const char* what);
 // does no environment lookups); mlxq_reload_overrides() reads them again.
 struct Overrides {
   bool qmv_row_all, qmv_no_row, qmv_mfma, qmv_dot_all, qmv_tile_all, qmv_legacy, qmv_stream, qmv_narrow;
-  int tile_wv, tile_nch;    // MLXQ_QMV_TILE=waves,chunks
+  int tile_wv, tile_nch, tile_kh;  // MLXQ_QMV_TILE=waves,chunks[,K parts]
   int dot_sub, dot_wv;      // MLXQ_QMV_DOT=sub,waves
   int mfma_sub, mfma_wv;    // MLXQ_QMV_MFMA_CFG=sub,waves
   int qmv_sub;              // MLXQ_QMV_SUB

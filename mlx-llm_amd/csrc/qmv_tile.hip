@@ -19,8 +19,11 @@
 //    the math on chunk c waits only for chunks <= c.
 //  * Math per chunk: lane (r16, gq) holds 16 bytes of weight row r16; a
 //    4 x 4 dword transpose across the lane rows gives group-pure MFMA
-//    blocks; P = sum x (OFF + q), S = sum x (MFMA against ones),
-//    acc += s P + (b - OFF s) S per group in f32.
+//    blocks; P = sum x (OFF + q) per group, acc += s P in f32.  The rest of
+//    the affine term, sum_g S_g (b - OFF s) with S_g the group's sum of x,
+//    is one MFMA (two for Q4) per slice: the group sums are formed once per
+//    workgroup while staging (not per wave and chunk) and fed as bf16 hi/lo
+//    halves against the bf16 biases (and scales).
 //  * Split K: blockIdx.y picks the slice.  With more than one slice the
 //    workgroups store f32 partial tiles in the caller's workspace and a
 //    second, elementwise kernel adds them in slice order (deterministic),
@@ -86,90 +89,172 @@ __device__ __forceinline__ void act_order_q4_bytes(const uint32_t* x, uint32_t* 
   a[3] = __builtin_amdgcn_perm(x[3], x[2], 0x07060302u);
 }
 
-template <int BITS, int GS, int MT, int WV, int NCH>
+// Geometry of a workgroup: WV waves in RG = WV / KH row groups of 16 weight
+// rows times KH parts of the workgroup's K slice, NCH chunks per wave.
+template <int BITS, int GS, int MT, int WV, int NCH, int KH>
 struct TileGeom {
   using Bk = Blk<BITS, GS>;
   static constexpr int T = 64 * WV;                  // threads
+  static constexpr int RG = WV / KH;                 // row groups (16 weight rows each)
   static constexpr int MR = 16 * MT;                 // activation rows staged (padded)
-  static constexpr int KS = NCH * Bk::KC;            // k per slice
-  static constexpr int ROW16 = KS / 8 + 1;           // 16-byte slots per staged row (one of padding)
-  static constexpr int XP = MR * (KS / 8) / T;       // 16-byte activation pieces per thread
-  static constexpr int NG = KS / GS;                 // groups per slice
-  static constexpr int NGW = NG / 2;                 // parameter words per row and slice
-  static_assert(XP >= 1 && MR * (KS / 8) % T == 0, "activation pieces must divide over the threads");
+  static constexpr int KS = NCH * Bk::KC;            // k per wave slice
+  static constexpr int KW = KH * KS;                 // k per workgroup slice
+  static constexpr int ROW16 = KW / 8 + 1;           // 16-byte slots per staged row (one of padding)
+  static constexpr int XP = MR * (KW / 8) / T;       // 16-byte activation pieces per thread
+  static constexpr int NG = KS / GS;                 // groups per wave slice
+  static constexpr int NGW = NG / 2;                 // parameter words per row and wave slice
+  // group sums of the staged activations, as MFMA A operands of the bias
+  // term: per row and K part [hi(0..NGP), lo(0..NGP), zeros] in bf16, KB
+  // blocks of 32 k
+  static constexpr int NGP = NG < 8 ? 8 : NG;        // groups padded to whole 8-lane slices
+  static constexpr int KB = (2 * NGP + 31) / 32;     // bias-term MFMAs per M tile
+  static constexpr int SXP = 32 * KB;                // bf16 per K part
+  static constexpr int SXS = KH * SXP + 8;           // bf16 per row (8 of padding)
+  static_assert(WV % KH == 0, "K parts divide the waves");
+  static_assert(XP >= 1 && MR * (KW / 8) % T == 0, "activation pieces must divide over the threads");
   static_assert(NG % 2 == 0 && (NGW == 2 || NGW % 4 == 0), "parameters load as whole vectors");
+  static_assert(NGP % 8 == 0 && (KW / 8) % 8 == 0, "a group's eight pieces sit in eight consecutive lanes");
 };
 
-template <int BITS, int GS, int MT, int WV, int NCH>
-__global__ __launch_bounds__(64 * WV) void qmv_tile_kernel(const TileParams p) {
-  using Tg = TileGeom<BITS, GS, MT, WV, NCH>;
-  using Bk = typename Tg::Bk;
-  constexpr float OFF = BITS == 4 ? 128.f : 0.f;
-  __shared__ u32x4 xs[Tg::MR * Tg::ROW16];
+__device__ __forceinline__ uint32_t bf16_rne_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return u >> 16;
+}
 
-  const int K = p.K, M = p.M, N = p.N;
+// One work item (16 RG weight rows x one workgroup K slice): its global
+// data, held in registers from the loads until they are used -- the
+// activation pieces until the LDS staging, the parameters and codes until
+// the math.
+template <int BITS, int GS, int MT, int WV, int NCH, int KH>
+struct TileX {
+  u32x4 xg[TileGeom<BITS, GS, MT, WV, NCH, KH>::XP];  // activation pieces of the slice
+};
+template <int BITS, int GS, int MT, int WV, int NCH, int KH>
+struct TileW {
+  using Tg = TileGeom<BITS, GS, MT, WV, NCH, KH>;
+  uint32_t sw[Tg::NGW], bw[Tg::NGW];  // this lane's row's scales / biases over the wave's slice
+  u32x4 w[NCH];                       // this lane's 16 bytes of its row, per chunk
+};
+
+// The activation loads of the workgroup's slice: piece i of this thread is
+// 16-byte slot tid + T i of the slice's rows of C slots; its row and column
+// follow from tid at compile-time steps.
+template <int BITS, int GS, int MT, int WV, int NCH, int KH>
+__device__ __forceinline__ void tile_load_x(const TileParams& p, int split, TileX<BITS, GS, MT, WV, NCH, KH>& X) {
+  using Tg = TileGeom<BITS, GS, MT, WV, NCH, KH>;
   const int tid = threadIdx.x;
-  const int lane = tid & 63;
+  constexpr int C = Tg::KW / 8;
+  const uint16_t* xs0 = p.x + split * Tg::KW;  // slice start (element offsets stay below 2^31)
+#pragma unroll
+  for (int i = 0; i < Tg::XP; i++) {  // rows past M read row M-1: they only feed output rows >= M
+    const int row = Tg::T >= C ? tid / C + i * (Tg::T / C) : i / (C / Tg::T);
+    const int col = Tg::T >= C ? tid % C : tid + Tg::T * (i % (C / Tg::T));
+    X.xg[i] = *reinterpret_cast<const u32x4*>(xs0 + min(row, p.M - 1) * p.K + col * 8);
+  }
+}
+
+// The group parameters, then the codes chunk by chunk (the math on chunk c
+// waits only for chunks <= c), of this lane's weight row over this wave's
+// part of the slice.
+template <int BITS, int GS, int MT, int WV, int NCH, int KH>
+__device__ __forceinline__ void tile_load_w(const TileParams& p, int tile, int split,
+                                            TileW<BITS, GS, MT, WV, NCH, KH>& W) {
+  using Tg = TileGeom<BITS, GS, MT, WV, NCH, KH>;
+  using Bk = typename Tg::Bk;
+  const int K = p.K;
+  const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rg = wave % Tg::RG, kh = wave / Tg::RG;
   const int r16 = lane & 15, gq = lane >> 4;
   const int G = K / GS;
   const int64_t row_u4 = static_cast<int64_t>(K) * BITS / 128;
-  const int tile = blockIdx.x, split = blockIdx.y;
-  const int n0 = tile * 16 * WV + wave * 16;  // this wave's 16 weight rows
-  const int c0 = split * NCH;                 // first chunk of the slice
-  const int n = min(n0 + r16, N - 1);         // rows past N repeat row N-1 (results dropped)
-
-  // 1. activations of the slice (issued first: the LDS staging waits on them)
-  u32x4 xg[Tg::XP];
-  int xdst[Tg::XP];
-#pragma unroll
-  for (int i = 0; i < Tg::XP; i++) {
-    const int q = tid + Tg::T * i;
-    const int row = q / (Tg::KS / 8), col = q % (Tg::KS / 8);
-    // rows past M read row M-1: they only feed output rows >= M
-    xg[i] = *reinterpret_cast<const u32x4*>(p.x + static_cast<int64_t>(min(row, M - 1)) * K +
-                                            static_cast<int64_t>(c0) * Bk::KC + col * 8);
-    xdst[i] = row * Tg::ROW16 + col;
-  }
-  // 2. this lane's row's group parameters over the slice, then 3. its codes,
-  // chunk by chunk (the math on chunk c waits only for chunks <= c)
-  uint32_t sw[Tg::NGW], bw[Tg::NGW];
-  load_param_words<Tg::NGW>(p.s + static_cast<int64_t>(n) * G + c0 * Bk::KC / GS, sw);
-  load_param_words<Tg::NGW>(p.b + static_cast<int64_t>(n) * G + c0 * Bk::KC / GS, bw);
-  u32x4 w[NCH];
+  const int c0 = (split * KH + kh) * NCH;  // first chunk of the wave's part
+  const int n = min(tile * 16 * Tg::RG + rg * 16 + r16, p.N - 1);  // rows past N repeat row N-1 (results dropped)
+  load_param_words<Tg::NGW>(p.s + static_cast<int64_t>(n) * G + c0 * Bk::KC / GS, W.sw);
+  load_param_words<Tg::NGW>(p.b + static_cast<int64_t>(n) * G + c0 * Bk::KC / GS, W.bw);
   const u32x4* wrow = reinterpret_cast<const u32x4*>(p.wq) + n * row_u4 + gq;
 #pragma unroll
-  for (int c = 0; c < NCH; c++) w[c] = wrow[static_cast<int64_t>(c0 + c) * 4];
-  __builtin_amdgcn_sched_barrier(0);  // every load is issued before the first wait
+  for (int c = 0; c < NCH; c++) W.w[c] = wrow[static_cast<int64_t>(c0 + c) * 4];
+}
 
+// Stage the workgroup slice's activations in LDS (and their group sums),
+// then a barrier.
+template <int BITS, int GS, int MT, int WV, int NCH, int KH>
+__device__ __forceinline__ void tile_stage(const TileX<BITS, GS, MT, WV, NCH, KH>& X, u32x4* xs, uint16_t* sx) {
+  using Tg = TileGeom<BITS, GS, MT, WV, NCH, KH>;
+  const int tid = threadIdx.x;
+  constexpr int C = Tg::KW / 8;
   // staged in the order of the Q4 decode (pairs (x0,x2),(x4,x6),...): the
-  // permutation is done once here instead of by every wave per block
+  // permutation is done once here instead of by every wave per block.  The
+  // sum of x over each group (row m, group g) is formed here once for the
+  // workgroup: a piece's 8 values with v_dot2 against ones, then the group's
+  // 8 pieces (8 consecutive lanes) with DPP adds; it is stored as the bf16
+  // pair hi + lo (hi = bf16(S), lo = bf16(S - hi): S to about 2^-16).
+  const uint32_t one2 = 0x3F803F80u;  // bf16 (1, 1)
 #pragma unroll
   for (int i = 0; i < Tg::XP; i++) {
+    float ps = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; w++) ps = dot::dot2(X.xg[i][w], one2, ps);
+    ps += dpp_f32<kDppQuadXor1>(ps);
+    ps += dpp_f32<kDppQuadXor2>(ps);
+    ps += dpp_f32<kDppRowHalfMirror>(ps);  // the 8 lanes of the group now hold its sum
+    const int row = Tg::T >= C ? tid / C + i * (Tg::T / C) : i / (C / Tg::T);
+    const int col = Tg::T >= C ? tid % C : tid + Tg::T * (i % (C / Tg::T));
     if constexpr (BITS == 4) {
-      const uint32_t xv[4] = {xg[i][0], xg[i][1], xg[i][2], xg[i][3]};
+      const uint32_t xv[4] = {X.xg[i][0], X.xg[i][1], X.xg[i][2], X.xg[i][3]};
       uint32_t a[4];
       act_order_q4_bytes(xv, a);
-      xs[xdst[i]] = u32x4{a[0], a[1], a[2], a[3]};
+      xs[row * Tg::ROW16 + col] = u32x4{a[0], a[1], a[2], a[3]};
     } else {
-      xs[xdst[i]] = xg[i];
+      xs[row * Tg::ROW16 + col] = X.xg[i];
     }
+    // the group's 8 lanes store the same value (no branch)
+    const int gw = col / (GS / 8);  // group within the workgroup slice
+    const uint32_t hi = bf16_rne_bits(ps);
+    uint16_t* sr = sx + row * Tg::SXS + (gw / Tg::NG) * Tg::SXP + gw % Tg::NG;
+    sr[0] = static_cast<uint16_t>(hi);
+    sr[Tg::NGP] = static_cast<uint16_t>(bf16_rne_bits(ps - __uint_as_float(hi << 16)));
+  }
+  // zeros in the padding of the group-sum rows (groups NG..NGP of each
+  // half, and past 2 NGP, in every K part)
+  for (int e = tid; e < Tg::MR * KH * Tg::SXP; e += Tg::T) {
+    const int row = e / (KH * Tg::SXP), t = e % Tg::SXP, part = (e / Tg::SXP) % KH;
+    if (t >= 2 * Tg::NGP || t % Tg::NGP >= Tg::NG) sx[row * Tg::SXS + part * Tg::SXP + t] = 0;
   }
   __syncthreads();
+}
+
+// The math of one workgroup item from the staged activations and the
+// wave's parameters and codes: group-pure MFMAs and per-group folds, the
+// bias term; the K parts' sums meet in LDS (added in part order), then y
+// (one slice) or the slice's f32 partial tile.
+template <int BITS, int GS, int MT, int WV, int NCH, int KH>
+__device__ __forceinline__ void tile_math(const TileParams& p, int tile, int split,
+                                          const TileW<BITS, GS, MT, WV, NCH, KH>& L, const u32x4* xs,
+                                          const uint16_t* sx, f32x4* red) {
+  using Tg = TileGeom<BITS, GS, MT, WV, NCH, KH>;
+  using Bk = typename Tg::Bk;
+  constexpr float OFF = BITS == 4 ? 128.f : 0.f;
+  const int M = p.M, N = p.N;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rg = wave % Tg::RG, kh = wave / Tg::RG;
+  const int r16 = lane & 15, gq = lane >> 4;
+  const int n0 = tile * 16 * Tg::RG + rg * 16;  // this wave's 16 weight rows
+  const int xc0 = kh * NCH;                      // the wave's first chunk within the staged slice
 
   f32x4 acc[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; mt++) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  uint32_t ones[4];
-#pragma unroll
-  for (int i = 0; i < 4; i++) ones[i] = 0x3F803F80u;  // bf16 1.0 pairs
 
 #pragma unroll
   for (int c = 0; c < NCH; c++) {
-    uint32_t d[4] = {w[c][0], w[c][1], w[c][2], w[c][3]};
+    uint32_t d[4] = {L.w[c][0], L.w[c][1], L.w[c][2], L.w[c][3]};
     if constexpr (!Bk::NAT) transpose_rows(d);
     const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-    f32x4 P[MT], SX[MT];
+    f32x4 P[MT];
 #pragma unroll
     for (int j = 0; j < Bk::NB; j++) {
       const bool first = j % Bk::BPG == 0;
@@ -186,7 +271,7 @@ __global__ __launch_bounds__(64 * WV) void qmv_tile_kernel(const TileParams p) {
       for (int mt = 0; mt < MT; mt++) {
         // A operand: activation row 16 mt + r16, this lane's slice of block j
         const u32x4* rowp = xs + (16 * mt + r16) * Tg::ROW16;
-        const int e = c * Bk::KC + Bk::xoff(j, gq);
+        const int e = (xc0 + c) * Bk::KC + Bk::xoff(j, gq);
         uint32_t a[4];
         if constexpr (Bk::XW == 4) {
           const u32x4 v = rowp[e / 8];
@@ -195,49 +280,114 @@ __global__ __launch_bounds__(64 * WV) void qmv_tile_kernel(const TileParams p) {
           const uint2 v = reinterpret_cast<const uint2*>(rowp)[e / 4];
           a[0] = v.x; a[1] = v.y;
         }
-        SX[mt] = mma<Bk::X32>(a, ones, first ? zero : SX[mt]);
         P[mt] = mma<Bk::X32>(a, bq, first ? zero : P[mt]);
       }
       if (j % Bk::BPG == Bk::BPG - 1) {
-        const int g = (c * Bk::KC + Bk::code0(j)) / GS;  // group within the slice (compile-time)
-        const float sc = __uint_as_float((g & 1) ? (sw[g >> 1] & 0xFFFF0000u) : (sw[g >> 1] << 16));
-        const float bb = __uint_as_float((g & 1) ? (bw[g >> 1] & 0xFFFF0000u) : (bw[g >> 1] << 16));
-        const float cf = bb - OFF * sc;
+        const int g = (c * Bk::KC + Bk::code0(j)) / GS;  // group within the wave slice (compile-time)
+        const float sc = __uint_as_float((g & 1) ? (L.sw[g >> 1] & 0xFFFF0000u) : (L.sw[g >> 1] << 16));
 #pragma unroll
         for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-          for (int v = 0; v < 4; v++) acc[mt][v] = fmaf(sc, P[mt][v], fmaf(cf, SX[mt][v], acc[mt][v]));
+          for (int v = 0; v < 4; v++) acc[mt][v] = fmaf(sc, P[mt][v], acc[mt][v]);
       }
     }
+  }
+
+  // The bias term sum_g S[m, g] (b[n, g] - OFF s[n, g]) of the wave slice on
+  // the matrix cores: A = the staged group sums (hi and lo halves), B = this
+  // row's biases (and scales) over the same k positions, both halves.  Lane
+  // (r16, gq) supplies k = 32 kb + 8 gq + [0, 8): groups g0.. of one half.
+  {
+    f32x4 ab[MT], as[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) ab[mt] = as[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < Tg::KB; kb++) {
+      const int t0 = 32 * kb + 8 * gq;
+      const bool valid = t0 < 2 * Tg::NGP;
+      const int g0 = t0 % Tg::NGP;
+      uint32_t bb[4] = {0u, 0u, 0u, 0u}, bs[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int cg = 0; cg < Tg::NGP / 8; cg++)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          if (4 * cg + i < Tg::NGW) {
+            const bool take = valid && g0 == 8 * cg;
+            bb[i] = take ? L.bw[4 * cg + i] : bb[i];
+            if constexpr (BITS == 4) bs[i] = take ? L.sw[4 * cg + i] : bs[i];
+          }
+#pragma unroll
+      for (int mt = 0; mt < MT; mt++) {
+        const u32x4 av =
+            *reinterpret_cast<const u32x4*>(sx + (16 * mt + r16) * Tg::SXS + kh * Tg::SXP + t0);
+        const uint32_t a[4] = {av[0], av[1], av[2], av[3]};
+        ab[mt] = mma<true>(a, bb, ab[mt]);
+        if constexpr (BITS == 4) as[mt] = mma<true>(a, bs, as[mt]);
+      }
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+      for (int v = 0; v < 4; v++)
+        acc[mt][v] += BITS == 4 ? fmaf(-OFF, as[mt][v], ab[mt][v]) : ab[mt][v];
+  }
+
+  // K parts 1.. hand their sums to part 0 through LDS (added in part order)
+  if constexpr (KH > 1) {
+    if (kh > 0)
+#pragma unroll
+      for (int mt = 0; mt < MT; mt++) red[(((kh - 1) * Tg::RG + rg) * MT + mt) * 64 + lane] = acc[mt];
+    __syncthreads();
+    if (kh > 0) return;
+#pragma unroll
+    for (int h = 1; h < KH; h++)
+#pragma unroll
+      for (int mt = 0; mt < MT; mt++) {
+        const f32x4 o = red[(((h - 1) * Tg::RG + rg) * MT + mt) * 64 + lane];
+#pragma unroll
+        for (int v = 0; v < 4; v++) acc[mt][v] += o[v];
+      }
   }
 
   // C layout of a 16x16 MFMA tile: lane holds column (weight row) r16 and
   // activation rows 4 gq + v of the M-tile.
   const int nn = n0 + r16;
+  if (nn >= N) return;
   if (p.splits == 1) {
-    if (nn < N) {
-      const float bb = p.bias ? bf16_bits_to_f32(p.bias[nn]) : 0.f;
-#pragma unroll
-      for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-        for (int v = 0; v < 4; v++) {
-          const int m = 16 * mt + 4 * gq + v;
-          if (m < M) p.y[static_cast<int64_t>(m) * N + nn] = static_cast<uint16_t>(f32_to_bf16_bits(acc[mt][v] + bb));
-        }
-    }
-    return;
-  }
-
-  // partial tile of this slice; split_reduce4_kernel adds the slices
-  if (nn < N) {
+    const float bb = p.bias ? bf16_bits_to_f32(p.bias[nn]) : 0.f;
 #pragma unroll
     for (int mt = 0; mt < MT; mt++)
 #pragma unroll
       for (int v = 0; v < 4; v++) {
         const int m = 16 * mt + 4 * gq + v;
-        if (m < M) p.part[(static_cast<int64_t>(split) * M + m) * N + nn] = acc[mt][v];
+        if (m < M) p.y[static_cast<int64_t>(m) * N + nn] = static_cast<uint16_t>(f32_to_bf16_bits(acc[mt][v] + bb));
       }
+    return;
   }
+  // partial tile of this slice; split_reduce4_kernel adds the slices
+#pragma unroll
+  for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      const int m = 16 * mt + 4 * gq + v;
+      if (m < M) p.part[(static_cast<int64_t>(split) * M + m) * N + nn] = acc[mt][v];
+    }
+}
+
+// One item per workgroup: blockIdx.x = tile of 16 RG rows, blockIdx.y = K slice.
+template <int BITS, int GS, int MT, int WV, int NCH, int KH>
+__global__ __launch_bounds__(64 * WV) void qmv_tile_kernel(const TileParams p) {
+  using Tg = TileGeom<BITS, GS, MT, WV, NCH, KH>;
+  __shared__ u32x4 xs[Tg::MR * Tg::ROW16];
+  __shared__ __align__(16) uint16_t sx[Tg::MR * Tg::SXS];
+  __shared__ f32x4 red[KH > 1 ? (KH - 1) * Tg::RG * MT * 64 : 1];
+  TileX<BITS, GS, MT, WV, NCH, KH> X;
+  TileW<BITS, GS, MT, WV, NCH, KH> W;
+  tile_load_x(p, blockIdx.y, X);
+  tile_load_w(p, blockIdx.x, blockIdx.y, W);
+  __builtin_amdgcn_sched_barrier(0);  // every load is issued before the first wait
+  tile_stage(X, xs, sx);
+  tile_math(p, blockIdx.x, blockIdx.y, W, xs, sx, red);
 }
 
 // y[m, n] = bf16(sum over splits of part[s, m, n] (in split order) + bias[n])
@@ -301,12 +451,12 @@ namespace tile {
 constexpr int kMaxSplits = kMaxSplitsK;
 
 struct Cfg {
-  int mt = 1, wv = 4, nch = 8;
+  int mt = 1, wv = 4, nch = 8, kh = 1;
 };
 
-template <int BITS, int MT, int WV, int NCH>
+template <int BITS, int MT, int WV, int NCH, int KH>
 int run(const TileParams& a, int tiles, hipStream_t st, int* query) {
-  auto kern = qmv_tile_kernel<BITS, 64, MT, WV, NCH>;
+  auto kern = qmv_tile_kernel<BITS, 64, MT, WV, NCH, KH>;
   if (query) {
     static int cached = -1;
     if (cached < 0) {
@@ -322,13 +472,22 @@ int run(const TileParams& a, int tiles, hipStream_t st, int* query) {
   return check_launch("qmv_tile");
 }
 
-// (waves, chunks per slice): slices of 16 chunks only with 8 waves, which
-// keeps the activation staging at <= 16 pieces per thread
+// The instantiated (waves, chunks per wave, K parts) forms: slices of 16
+// chunks only with 8 waves and one K part (<= 16 activation pieces per
+// thread); K parts of 2 (4 or 8 chunks) and 4 (4 chunks) with 8 waves, so a
+// workgroup slice stays within 16 chunks.
+bool cfg_known(const Cfg& c) {
+  if (c.kh == 1) return (c.wv == 4 && (c.nch == 4 || c.nch == 8)) || (c.wv == 8 && (c.nch == 4 || c.nch == 8 || c.nch == 16));
+  return c.wv == 8 && ((c.kh == 2 && (c.nch == 4 || c.nch == 8)) || (c.kh == 4 && c.nch == 4));
+}
+
 template <int BITS, int MT>
 int run_wn(const Cfg& c, const TileParams& a, int tiles, hipStream_t st, int* q) {
-  if (c.wv == 4) return c.nch == 4 ? run<BITS, MT, 4, 4>(a, tiles, st, q) : run<BITS, MT, 4, 8>(a, tiles, st, q);
-  if (c.nch == 4) return run<BITS, MT, 8, 4>(a, tiles, st, q);
-  return c.nch == 8 ? run<BITS, MT, 8, 8>(a, tiles, st, q) : run<BITS, MT, 8, 16>(a, tiles, st, q);
+  if (c.kh == 2) return c.nch == 4 ? run<BITS, MT, 8, 4, 2>(a, tiles, st, q) : run<BITS, MT, 8, 8, 2>(a, tiles, st, q);
+  if (c.kh == 4) return run<BITS, MT, 8, 4, 4>(a, tiles, st, q);
+  if (c.wv == 4) return c.nch == 4 ? run<BITS, MT, 4, 4, 1>(a, tiles, st, q) : run<BITS, MT, 4, 8, 1>(a, tiles, st, q);
+  if (c.nch == 4) return run<BITS, MT, 8, 4, 1>(a, tiles, st, q);
+  return c.nch == 8 ? run<BITS, MT, 8, 8, 1>(a, tiles, st, q) : run<BITS, MT, 8, 16, 1>(a, tiles, st, q);
 }
 
 int dispatch(int bits, const Cfg& c, const TileParams& a, int tiles, hipStream_t st, int* q) {
@@ -398,40 +557,44 @@ int launch_qmv_tile(const uint16_t* x, int64_t M, const uint32_t* wq, const uint
   const bool ws_ok = workspace && !(reinterpret_cast<uintptr_t>(workspace) & 255u);
   const int64_t fit = ws_ok ? static_cast<int64_t>(workspace_bytes / (M * N * 4)) : 1;  // slices that fit
 
-  // (waves, chunks per slice).  Measured best at the Llama-3-8B shapes
-  // (M = 8..32): large N*K with K >= 2N (down): 8 waves, 16-chunk slices;
-  // other large N*K: Q4 8 waves / 8 chunks, Q8 4 waves / 8 chunks; small
-  // N*K: 4 waves, 8 chunks (4 for Q4 with N < 2048).  Taken when it divides
-  // K into at most 16 slices that fit the workspace, else the first such of
+  // (waves, chunks per wave, K parts).  Measured best at the Llama-3-8B
+  // shapes (M = 16 / 32, weights streamed from HBM): large N*K (gate, up,
+  // down): 8 waves as 4 row groups x 2 K parts of 8 chunks (Q8 M = 32 gate
+  // 25.6 -> 24.0 us, down 28.4 -> 25.7; Q4 M = 32 down 22.1 -> 20.8 against
+  // one K part); q/o: Q8 M = 32 the same (12.7 -> 10.7 us), else 2 row
+  // groups x 4 K parts of 4 chunks; k/v: that too (Q8 M = 32 8.5 -> 8.1 us)
+  // except Q4 M = 32, 4 waves, 4 chunks, one part.  Taken when it divides K
+  // into at most 16 slices that fit the workspace, else the first such of
   // the others.
   const bool large = N * K >= (int64_t(1) << 25);
   Cfg pref;
   pref.mt = M <= 16 ? 1 : 2;
-  if (large && K >= 2 * N) {
-    pref.wv = 8; pref.nch = 16;
-  } else if (large) {
-    pref.wv = bits == 4 ? 8 : 4; pref.nch = 8;
+  if (large || (bits == 8 && M > 16 && N > 2048)) {
+    pref.wv = 8; pref.nch = 8; pref.kh = 2;
+  } else if (N <= 2048 && bits == 4 && M > 16) {
+    pref.wv = 4; pref.nch = 4; pref.kh = 1;
   } else {
-    pref.wv = 4; pref.nch = bits == 4 && N < 2048 ? 4 : 8;
+    pref.wv = 8; pref.nch = 4; pref.kh = 4;
   }
-  const int fwv = overrides().tile_wv, fnch = overrides().tile_nch;
+  const int fwv = overrides().tile_wv, fnch = overrides().tile_nch, fkh = overrides().tile_kh;
   if (fwv) pref.wv = fwv;
   if (fnch) pref.nch = fnch;
-  const Cfg order[] = {pref, {pref.mt, 8, 16}, {pref.mt, 8, 8}, {pref.mt, 4, 8}, {pref.mt, 4, 4}, {pref.mt, 8, 4}};
+  if (fkh) pref.kh = fkh;
+  const Cfg order[] = {pref,           {pref.mt, 8, 16, 1}, {pref.mt, 8, 8, 1}, {pref.mt, 4, 8, 1},
+                       {pref.mt, 4, 4, 1}, {pref.mt, 8, 4, 1}};
   const Cfg* pick = nullptr;
   for (const Cfg& c : order) {
-    if ((c.wv != 4 && c.wv != 8) || (c.nch != 4 && c.nch != 8 && c.nch != 16) || (c.nch == 16 && c.wv != 8))
-      continue;
-    if (ch % c.nch) continue;
-    const int64_t splits = ch / c.nch;
+    if (!cfg_known(c)) continue;
+    if (ch % (c.nch * c.kh)) continue;
+    const int64_t splits = ch / (c.nch * c.kh);
     if (splits > kMaxSplits || (splits > 1 && splits > fit)) continue;
     pick = &c;
     break;
   }
   if (!pick) return MLXQ_ERR_UNSUPPORTED;  // no slicing fits the workspace: the caller picks another kernel
-  a.splits = static_cast<int>(ch / pick->nch);
+  a.splits = static_cast<int>(ch / (pick->nch * pick->kh));
   a.part = a.splits > 1 ? static_cast<float*>(workspace) : nullptr;
-  const int64_t tiles = ceil_div(N, 16 * pick->wv);
+  const int64_t tiles = ceil_div(N, 16 * (pick->wv / pick->kh));
   // split K: the slices are added by a second launch (split_reduce4_kernel).
   // A hand-off inside this kernel (the last arriving slice of a tile adds the
   // slices) was measured slower at the Llama-3-8B shapes (Q8 M = 32 gate
