@@ -33,6 +33,13 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, published
 METRIC = "Q4/Q8 qmatmul GB/s & TFLOP/s (% roofline), Llama-3-8B proj shapes, 1 GPU"
 # measured HBM traffic per launch (bytes) of a dominant-kernel candidate, keyed (bits, M, K, N)
 TRAFFIC_BYTES = {(8, 32, 4096, 14336): 95_506_516}
+# measured HBM traffic per call of the Q4 g64 M=1 GEMV, by projection shape
+# (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated; profiles/qmv_q4_m1_traffic.md)
+HEADLINE_TRAFFIC = {"q": 9_586_401, "k": 2_483_355, "v": 2_483_355, "o": 9_586_401, "gate": 33_212_044,
+                    "up": 33_212_044, "down": 33_439_531}
+# MFMA busy fraction of the prefill qmm calls from SQ counters
+# (SQ_VALU_MFMA_BUSY_CYCLES / (SIMDs x GRBM_GUI_ACTIVE); profiles/qmm_prefill_m2048_mfma_counters.md)
+PREFILL_MFMA_BUSY = {"gate_up": 0.408, "down": 0.468}
 
 # (name, K, N): y[M, N] = x[M, K] . W[N, K]^T
 PROJ = [("q", 4096, 4096), ("k", 4096, 1024), ("v", 4096, 1024), ("o", 4096, 4096),
@@ -254,7 +261,9 @@ def main(argv=None) -> int:
     # the north-star headline: Q4 g64 decode GEMV (M=1) at each projection shape
     headline = {nm: {"us": round(per[(4, 1, nm)][0], 2),
                      "GB/s": round(per[(4, 1, nm)][1] / per[(4, 1, nm)][0] / 1e3, 1),
-                     "frac_hbm": round(per[(4, 1, nm)][1] / per[(4, 1, nm)][0] / 1e3 / HBM_PEAK_GBS, 3)}
+                     "frac_hbm": round(per[(4, 1, nm)][1] / per[(4, 1, nm)][0] / 1e3 / HBM_PEAK_GBS, 3),
+                     "algorithmic_bytes": per[(4, 1, nm)][1], "traffic": HEADLINE_TRAFFIC[nm],
+                     "traffic_ratio": round(HEADLINE_TRAFFIC[nm] / per[(4, 1, nm)][1], 3)}
                 for nm, _, _ in PROJ}
     q4m1 = kernels["q4_m1"]
     del copies
@@ -299,7 +308,7 @@ def bench_prefill(torch, mlxq, iters=10):
         x = torch.randn((2048, k), generator=g, device="cuda").to(torch.bfloat16)
         y = torch.empty((2048, n), device="cuda", dtype=torch.bfloat16)
         fn = mlxq.bind_qmatmul(x, wq, s, b, 64, 4, out=y)
-        for _ in range(20):  # the first launches of a ~300 us kernel run below full clocks
+        for _ in range(100):  # the first launches of a ~300 us kernel run below full clocks (~30 ms to settle)
             fn()
         torch.cuda.synchronize()
         reps = []
@@ -313,7 +322,11 @@ def bench_prefill(torch, mlxq, iters=10):
             reps.append(e0.elapsed_time(e1) * 1e3 / iters)
         us = sorted(reps)[len(reps) // 2]
         tf = 2.0 * 2048 * n * k / (us * 1e-6) / 1e12
-        res[name] = {"us": round(us, 1), "TFLOP/s": round(tf, 1), "frac_mfma_bf16": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)}
+        res[name] = {"us": round(us, 1), "TFLOP/s": round(tf, 1), "frac_mfma_bf16": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                     "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
+                                  "unit": "TFLOP/s", "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                                  "flops_per_launch": 2 * 2048 * n * k,
+                                  "mfma_busy_counter": PREFILL_MFMA_BUSY[name]}}
         # reference point, not part of the path: the library's plain bf16 GEMM
         # (torch -> hipBLASLt) of the same shape on already dequantized weights
         wd = w.to(torch.bfloat16)

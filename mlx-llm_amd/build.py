@@ -80,6 +80,12 @@ def build(jobs: int = 8, verbose: bool = False) -> Path:
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
+    # a kernel whose host-side stub the compiler dropped (it can, silently,
+    # for some builtins in template kernels) would only fail at load time
+    nm = subprocess.run(["nm", "-u", str(tmp)], capture_output=True, text=True)
+    missing = [ln.split()[-1] for ln in nm.stdout.splitlines() if "__device_stub__" in ln]
+    if missing:
+        raise RuntimeError("kernel stubs missing from the library:\n" + "\n".join(missing[:10]))
     os.replace(tmp, LIB)
     build_host_tests(verbose)
     build_cli(verbose)

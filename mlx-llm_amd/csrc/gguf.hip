@@ -42,44 +42,68 @@ __device__ __forceinline__ void store_vec(void* out, int64_t e, const float (&v)
   }
 }
 
-// One workgroup per chunk of kChunkElems elements (a whole number of blocks).
-// Chunk bytes are a multiple of 16 for every tag, so with a 16-byte aligned
-// base every chunk start is 16-byte aligned and staged with uint4 loads.
+// One workgroup per kCpw chunks of kChunkElems elements (each a whole number
+// of blocks): every byte of the workgroup's chunks is requested before the
+// barrier (one memory round trip per workgroup, kCpw x the bytes in flight
+// of a one-chunk workgroup), then each thread decodes kVec elements of every
+// chunk and writes them with 16-byte stores.  Chunk bytes are a multiple of
+// 16 for every tag, so with a 16-byte aligned base every chunk start is
+// 16-byte aligned and staged with uint4 loads.
+constexpr int kCpw = 4;
+
+// 16 bytes per lane from global memory straight into LDS (a wave's 64 lanes
+// fill 1 KB from `l`)
+__device__ __forceinline__ void lds_dma16(const uint8_t* g, uint8_t* l) {
+  __builtin_amdgcn_global_load_lds(g, l, 16, 0, 0);
+}
+
 template <int TAG, bool BF16OUT, bool ALIGNED16>
 __global__ __launch_bounds__(kThreads) void gguf_dequant_kernel(const uint8_t* __restrict__ data,
                                                                  int64_t nblocks, void* __restrict__ out) {
   constexpr int E = Geo<TAG>::E, B = Geo<TAG>::B;
   constexpr int BPC = kChunkElems / E;         // blocks per chunk
   constexpr int CB = BPC * B;                  // chunk bytes
+  constexpr int WB = kCpw * CB;                // workgroup bytes
   static_assert(CB % 16 == 0, "chunk bytes must be a multiple of 16");
-  __shared__ __align__(16) uint8_t lds[CB];
+  __shared__ __align__(16) uint8_t lds[(WB + 1023) / 1024 * 1024];
 
-  const int64_t chunk = blockIdx.x;
-  const int64_t blk0 = chunk * BPC;
-  const int nb = static_cast<int>(min<int64_t>(BPC, nblocks - blk0));
+  const int64_t blk0 = static_cast<int64_t>(blockIdx.x) * kCpw * BPC;
+  const int nb = static_cast<int>(min<int64_t>(kCpw * BPC, nblocks - blk0));  // blocks of this workgroup
   const int bytes = nb * B;
   const uint8_t* src = data + blk0 * B;
   const int tid = threadIdx.x;
 
   if constexpr (ALIGNED16) {
+    // direct global -> LDS loads: each wave instruction moves 1 KB (16 B per
+    // lane) into a contiguous LDS range, no registers held while in flight
     const int n16 = bytes >> 4;  // whole uint4s (bytes is a multiple of 2 at least)
-    for (int i = tid; i < n16; i += kThreads)
-      reinterpret_cast<uint4*>(lds)[i] = reinterpret_cast<const uint4*>(src)[i];
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    constexpr int kPieces = (WB + 1023) / 1024;  // 1 KB pieces of the workgroup
+#pragma unroll
+    for (int k = 0; k < (kPieces + kThreads / 64 - 1) / (kThreads / 64); k++) {
+      const int piece = k * (kThreads / 64) + wave;
+      if (piece < kPieces && piece * 64 + lane < n16)
+        lds_dma16(src + (piece * 64 + lane) * 16, lds + piece * 1024);
+    }
     for (int i = (n16 << 4) + tid; i < bytes; i += kThreads) lds[i] = src[i];
+    __builtin_amdgcn_s_waitcnt(0);
   } else {
     for (int i = tid; i < bytes; i += kThreads) lds[i] = src[i];
   }
   __syncthreads();
 
-  const int e0 = tid * kVec;  // element within the chunk
-  if (e0 >= nb * E) return;
-  float v[kVec];
 #pragma unroll
-  for (int i = 0; i < kVec; i++) {
-    int e = e0 + i;
-    v[i] = decode<TAG>(lds + (e / E) * B, e % E);
+  for (int c = 0; c < kCpw; c++) {
+    const int e0 = c * kChunkElems + tid * kVec;  // element within the workgroup
+    if (e0 >= nb * E) return;
+    float v[kVec];
+#pragma unroll
+    for (int i = 0; i < kVec; i++) {
+      const int e = e0 + i;
+      v[i] = decode<TAG>(lds + (e / E) * B, e % E);
+    }
+    store_vec<BF16OUT>(out, static_cast<int64_t>(blockIdx.x) * kCpw * kChunkElems + e0, v);
   }
-  store_vec<BF16OUT>(out, chunk * kChunkElems + e0, v);
 }
 
 // F32 / F16 / BF16 pass-through (dequant.rs:174-188): one element per thread.
@@ -102,7 +126,7 @@ __global__ __launch_bounds__(kThreads) void gguf_float_kernel(const uint8_t* __r
 template <int TAG, bool BF16OUT>
 void launch_blocks(const uint8_t* data, int64_t nblocks, void* out, hipStream_t st) {
   constexpr int E = Geo<TAG>::E;
-  int64_t chunks = ceil_div(nblocks * E, kChunkElems);
+  int64_t chunks = ceil_div(nblocks * E, static_cast<int64_t>(kCpw) * kChunkElems);  // workgroups
   if (chunks == 0) return;
   bool aligned = (reinterpret_cast<uintptr_t>(data) & 15u) == 0;
   if (aligned)
