@@ -48,6 +48,10 @@ const Overrides* read_overrides() {
   o->qmv_stream = flag("MLXQ_QMV_STREAM");
   o->qmv_narrow = flag("MLXQ_QMV_NARROW");
   if (const char* e = getenv("MLXQ_QMV_TILE")) sscanf(e, "%d,%d,%d", &o->tile_wv, &o->tile_nch, &o->tile_kh);
+  if (const char* e = getenv("MLXQ_QMV_TILE_STREAM")) {
+    o->stream_set = true;
+    sscanf(e, "%d,%d,%d,%d", &o->stream_wv, &o->stream_nch, &o->stream_kh, &o->stream_splits);
+  }
   pair("MLXQ_QMV_DOT", &o->dot_sub, &o->dot_wv);
   pair("MLXQ_QMV_MFMA_CFG", &o->mfma_sub, &o->mfma_wv);
   o->qmv_sub = num("MLXQ_QMV_SUB");

@@ -64,6 +64,7 @@ struct TileParams {
   float* part;  // [splits][M][N] partial sums (splits > 1)
   int M, N, K;
   int splits;
+  int steps;  // K slices per workgroup (streaming form)
 };
 
 constexpr int kMaxSplitsK = 16;  // most K splits of one call
@@ -181,7 +182,8 @@ __device__ __forceinline__ void tile_load_w(const TileParams& p, int tile, int s
 // Stage the workgroup slice's activations in LDS (and their group sums),
 // then a barrier.
 template <int BITS, int GS, int MT, int WV, int NCH, int KH>
-__device__ __forceinline__ void tile_stage(const TileX<BITS, GS, MT, WV, NCH, KH>& X, u32x4* xs, uint16_t* sx) {
+__device__ __forceinline__ void tile_stage(const TileX<BITS, GS, MT, WV, NCH, KH>& X, u32x4* xs, uint16_t* sx,
+                                           bool pad = true) {
   using Tg = TileGeom<BITS, GS, MT, WV, NCH, KH>;
   const int tid = threadIdx.x;
   constexpr int C = Tg::KW / 8;
@@ -219,6 +221,7 @@ __device__ __forceinline__ void tile_stage(const TileX<BITS, GS, MT, WV, NCH, KH
   }
   // zeros in the padding of the group-sum rows (groups NG..NGP of each
   // half, and past 2 NGP, in every K part)
+  if (pad)
   for (int e = tid; e < Tg::MR * KH * Tg::SXP; e += Tg::T) {
     const int row = e / (KH * Tg::SXP), t = e % Tg::SXP, part = (e / Tg::SXP) % KH;
     if (t >= 2 * Tg::NGP || t % Tg::NGP >= Tg::NG) sx[row * Tg::SXS + part * Tg::SXP + t] = 0;
@@ -226,28 +229,21 @@ __device__ __forceinline__ void tile_stage(const TileX<BITS, GS, MT, WV, NCH, KH
   __syncthreads();
 }
 
-// The math of one workgroup item from the staged activations and the
-// wave's parameters and codes: group-pure MFMAs and per-group folds, the
-// bias term; the K parts' sums meet in LDS (added in part order), then y
-// (one slice) or the slice's f32 partial tile.
+// The math of one K slice from the staged activations and the wave's
+// parameters and codes: group-pure MFMAs and per-group folds, then the bias
+// term, added into the wave's accumulators acc (16 weight rows x 16 MT
+// activation rows).
 template <int BITS, int GS, int MT, int WV, int NCH, int KH>
-__device__ __forceinline__ void tile_math(const TileParams& p, int tile, int split,
-                                          const TileW<BITS, GS, MT, WV, NCH, KH>& L, const u32x4* xs,
-                                          const uint16_t* sx, f32x4* red) {
+__device__ __forceinline__ void tile_accum(f32x4 (&acc)[MT], const TileW<BITS, GS, MT, WV, NCH, KH>& L,
+                                           const u32x4* xs, const uint16_t* sx) {
   using Tg = TileGeom<BITS, GS, MT, WV, NCH, KH>;
   using Bk = typename Tg::Bk;
   constexpr float OFF = BITS == 4 ? 128.f : 0.f;
-  const int M = p.M, N = p.N;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int rg = wave % Tg::RG, kh = wave / Tg::RG;
+  const int kh = wave / Tg::RG;
   const int r16 = lane & 15, gq = lane >> 4;
-  const int n0 = tile * 16 * Tg::RG + rg * 16;  // this wave's 16 weight rows
-  const int xc0 = kh * NCH;                      // the wave's first chunk within the staged slice
-
-  f32x4 acc[MT];
-#pragma unroll
-  for (int mt = 0; mt < MT; mt++) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int xc0 = kh * NCH;  // the wave's first chunk within the staged slice
 
 #pragma unroll
   for (int c = 0; c < NCH; c++) {
@@ -331,6 +327,20 @@ __device__ __forceinline__ void tile_math(const TileParams& p, int tile, int spl
       for (int v = 0; v < 4; v++)
         acc[mt][v] += BITS == 4 ? fmaf(-OFF, as[mt][v], ab[mt][v]) : ab[mt][v];
   }
+}
+
+// The end of a workgroup item: K parts 1.. hand their sums to part 0 through
+// LDS (added in part order), then y (one K split) or the split's f32 partial
+// tile.
+template <int BITS, int GS, int MT, int WV, int NCH, int KH>
+__device__ __forceinline__ void tile_finish(const TileParams& p, int tile, int split, f32x4 (&acc)[MT], f32x4* red) {
+  using Tg = TileGeom<BITS, GS, MT, WV, NCH, KH>;
+  const int M = p.M, N = p.N;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rg = wave % Tg::RG, kh = wave / Tg::RG;
+  const int r16 = lane & 15, gq = lane >> 4;
+  const int n0 = tile * 16 * Tg::RG + rg * 16;  // this wave's 16 weight rows
 
   // K parts 1.. hand their sums to part 0 through LDS (added in part order)
   if constexpr (KH > 1) {
@@ -387,7 +397,54 @@ __global__ __launch_bounds__(64 * WV) void qmv_tile_kernel(const TileParams p) {
   tile_load_w(p, blockIdx.x, blockIdx.y, W);
   __builtin_amdgcn_sched_barrier(0);  // every load is issued before the first wait
   tile_stage(X, xs, sx);
-  tile_math(p, blockIdx.x, blockIdx.y, W, xs, sx, red);
+  f32x4 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; mt++) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  tile_accum(acc, W, xs, sx);
+  tile_finish<BITS, GS, MT, WV, NCH, KH>(p, blockIdx.x, blockIdx.y, acc, red);
+}
+
+// Streaming form: a workgroup owns its 16 RG weight rows over `steps`
+// consecutive K slices (blockIdx.y picks the run of slices when K is split).
+// While the waves work on slice s from one LDS buffer, the codes of slices
+// s + 1 and s + 2 and the activations of s + 1 are already in flight, and s + 1
+// is staged into the other buffer: the memory stream of the workgroup keeps
+// going under its arithmetic instead of alternating with it, and a whole
+// projection needs no second pass over partial sums.
+template <int BITS, int GS, int MT, int WV, int NCH, int KH>
+__global__ __launch_bounds__(64 * WV) void qmv_stream_kernel(const TileParams p) {
+  using Tg = TileGeom<BITS, GS, MT, WV, NCH, KH>;
+  __shared__ u32x4 xs[2][Tg::MR * Tg::ROW16];
+  __shared__ __align__(16) uint16_t sx[2][Tg::MR * Tg::SXS];
+  __shared__ f32x4 red[KH > 1 ? (KH - 1) * Tg::RG * MT * 64 : 1];
+  const int steps = p.steps, s0 = blockIdx.y * steps, tile = blockIdx.x;
+  TileX<BITS, GS, MT, WV, NCH, KH> X0, X1;
+  TileW<BITS, GS, MT, WV, NCH, KH> W0, W1;
+  tile_load_x(p, s0, X0);
+  tile_load_w(p, tile, s0, W0);
+  if (steps > 1) {
+    tile_load_x(p, s0 + 1, X1);
+    tile_load_w(p, tile, s0 + 1, W1);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  tile_stage(X0, xs[0], sx[0]);
+  f32x4 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; mt++) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // slice s: codes W0 / buffer 0 (s even), W1 / buffer 1 (s odd); each
+  // register set and buffer is refilled as soon as its slice is used
+  for (int s = 0; s < steps; s += 2) {
+    if (s + 2 < steps) tile_load_x(p, s0 + s + 2, X0);
+    tile_accum(acc, W0, xs[0], sx[0]);
+    if (s + 2 < steps) tile_load_w(p, tile, s0 + s + 2, W0);
+    if (s + 1 >= steps) break;
+    tile_stage(X1, xs[1], sx[1], s == 0);
+    if (s + 3 < steps) tile_load_x(p, s0 + s + 3, X1);
+    tile_accum(acc, W1, xs[1], sx[1]);
+    if (s + 3 < steps) tile_load_w(p, tile, s0 + s + 3, W1);
+    if (s + 2 < steps) tile_stage(X0, xs[0], sx[0], false);
+  }
+  tile_finish<BITS, GS, MT, WV, NCH, KH>(p, tile, blockIdx.y, acc, red);
 }
 
 // y[m, n] = bf16(sum over splits of part[s, m, n] (in split order) + bias[n])
@@ -470,6 +527,66 @@ int run(const TileParams& a, int tiles, hipStream_t st, int* query) {
   }
   hipLaunchKernelGGL(kern, dim3(tiles, a.splits), dim3(64 * WV), 0, st, a);
   return check_launch("qmv_tile");
+}
+
+template <int BITS, int MT, int WV, int NCH, int KH>
+int run_stream(const TileParams& a, int tiles, hipStream_t st) {
+  hipLaunchKernelGGL((qmv_stream_kernel<BITS, 64, MT, WV, NCH, KH>), dim3(tiles, a.splits), dim3(64 * WV), 0, st, a);
+  return check_launch("qmv_stream");
+}
+
+// The streaming forms: (waves, Q4 chunks per wave and slice, K parts); Q8
+// takes twice the chunks, so a slice covers the same K either way.
+struct SCfg {
+  int wv = 8, nch = 2, kh = 2;
+};
+bool scfg_known(const SCfg& c) {
+  if (c.wv == 8 && (c.kh == 1 || c.kh == 2)) return c.nch == 2 || c.nch == 4;
+  if (c.wv == 8 && c.kh == 4) return c.nch == 2;
+  if (c.wv == 4 && c.kh == 1) return c.nch == 2 || c.nch == 4;
+  return false;
+}
+template <int BITS, int MT>
+int dispatch_stream_mt(const SCfg& c, const TileParams& a, int tiles, hipStream_t st) {
+  constexpr int F = BITS == 4 ? 1 : 2;
+  if (c.wv == 8 && c.kh == 2)
+    return c.nch == 2 ? run_stream<BITS, MT, 8, 2 * F, 2>(a, tiles, st) : run_stream<BITS, MT, 8, 4 * F, 2>(a, tiles, st);
+  if (c.wv == 8 && c.kh == 4) return run_stream<BITS, MT, 8, 2 * F, 4>(a, tiles, st);
+  if (c.wv == 4)
+    return c.nch == 2 ? run_stream<BITS, MT, 4, 2 * F, 1>(a, tiles, st) : run_stream<BITS, MT, 4, 4 * F, 1>(a, tiles, st);
+  return c.nch == 2 ? run_stream<BITS, MT, 8, 2 * F, 1>(a, tiles, st) : run_stream<BITS, MT, 8, 4 * F, 1>(a, tiles, st);
+}
+// Where the streaming form is the default, from interleaved A/B timings
+// against the single-slice form at the Llama-3-8B shapes (weights streamed
+// from HBM, clocks warmed): large gate/up-like matrices (K < N) from M = 8:
+// Q4 M = 32 19.9 -> 17.4 us, Q8 24.3 -> 23.1, Q4 M = 16 14.5 -> 13.8, Q8 21.2
+// -> 19.5; down-like (K > N) with 4 K splits: M = 32 Q4 21.2 -> 19.6, Q8 25.8
+// -> 24.1, Q8 M = 16 23.1 -> 21.1 (Q4 M = 16 at parity).  The shorter
+// matrices (q/o, k/v) stay on the single-slice form (parity or slower).
+bool stream_preferred(int64_t M, int64_t N, int64_t K, int bits, SCfg& c, int& splits) {
+  const bool large = N * K >= (int64_t(1) << 25);
+  if (!large || M < 8) return false;
+  if (K < N) {
+    c = M > 16 && bits == 8 ? SCfg{8, 2, 2} : SCfg{8, 4, 2};
+    splits = 1;
+    return true;
+  }
+  if (M > 16) {
+    c = SCfg{8, 2, 2};
+    splits = 4;
+    return true;
+  }
+  if (bits == 8 && M == 16) {
+    c = SCfg{4, 4, 1};
+    splits = 4;
+    return true;
+  }
+  return false;
+}
+
+int dispatch_stream(int bits, int mt, const SCfg& c, const TileParams& a, int tiles, hipStream_t st) {
+  if (bits == 4) return mt == 1 ? dispatch_stream_mt<4, 1>(c, a, tiles, st) : dispatch_stream_mt<4, 2>(c, a, tiles, st);
+  return mt == 1 ? dispatch_stream_mt<8, 1>(c, a, tiles, st) : dispatch_stream_mt<8, 2>(c, a, tiles, st);
 }
 
 // The instantiated (waves, chunks per wave, K parts) forms: slices of 16
@@ -556,6 +673,33 @@ int launch_qmv_tile(const uint16_t* x, int64_t M, const uint32_t* wq, const uint
   const int64_t ch = chunks_of(K, bits);
   const bool ws_ok = workspace && !(reinterpret_cast<uintptr_t>(workspace) & 255u);
   const int64_t fit = ws_ok ? static_cast<int64_t>(workspace_bytes / (M * N * 4)) : 1;  // slices that fit
+
+  // streaming form: where stream_preferred says (or MLXQ_QMV_TILE_STREAM=
+  // waves,chunks,K parts,K splits; =0 keeps the single-slice form)
+  {
+    const Overrides& ov = overrides();
+    SCfg c;
+    int splits = 1;
+    bool use = false;
+    if (ov.stream_set) {
+      use = ov.stream_wv > 0;
+      c.wv = ov.stream_wv; c.nch = ov.stream_nch; c.kh = ov.stream_kh;
+      splits = ov.stream_splits > 0 ? ov.stream_splits : 1;
+    } else {
+      use = stream_preferred(M, N, K, bits, c, splits);
+    }
+    const int64_t per = c.nch * (bits == 4 ? 1 : 2) * c.kh;  // chunks per K slice
+    if (use && scfg_known(c) && ch % per == 0 && (ch / per) % splits == 0 && splits <= kMaxSplits &&
+        (splits == 1 || splits <= fit)) {
+      a.splits = splits;
+      a.steps = static_cast<int>(ch / per / splits);
+      a.part = splits > 1 ? static_cast<float*>(workspace) : nullptr;
+      const int64_t tiles = ceil_div(N, 16 * (c.wv / c.kh));
+      if (int rc = dispatch_stream(bits, M <= 16 ? 1 : 2, c, a, static_cast<int>(tiles), st)) return rc;
+      if (splits == 1) return MLXQ_OK;
+      return launch_split_reduce(a.part, bias, y, M, N, splits, st);
+    }
+  }
 
   // (waves, chunks per wave, K parts).  Measured best at the Llama-3-8B
   // shapes (M = 16 / 32, weights streamed from HBM): large N*K (gate, up,
