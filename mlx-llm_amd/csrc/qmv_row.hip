@@ -12,12 +12,14 @@
 //  * A wave owns R rows and the whole of K: R * NI 16-byte loads per lane
 //    (NI = K*bits/8 / 1 KB), all issued before any arithmetic, after the
 //    workgroup's loads of x.  No K split, no partial sums, no second launch.
-//  * The workgroup stages x once in LDS: Q4 as bf16 pairs (x0,x4) (x1,x5)
-//    (x2,x6) (x3,x7) of every 8 elements, matching the codes' nibble order,
+//  * The workgroup stages x once in LDS: Q4 as bf16 pairs (x0,x2) (x4,x6)
+//    (x1,x3) (x5,x7) of every 8 elements, the order of the Q4 decode below,
 //    Q8 in natural order; plus the sum of x over every lane chunk (32 codes
 //    for Q4, 16 for Q8).
-//  * Q4 codes become bf16 (128 + q) pairs with one and-or each (0x4300 is
-//    bf16 128, whose ulp is 1); Q8 codes are converted exactly through f32.
+//  * Q4 codes become bf16 (128 + q) pairs: the even and the odd nibbles are
+//    masked into bytes and interleaved with 0x43 bytes by v_perm (0x43nn is
+//    bf16 128 + nn, whose ulp is 1), 7 instructions per 8 codes; Q8 codes
+//    are converted exactly through f32.
 //    v_dot2_f32_bf16 accumulates; per chunk y += s*dot + (b - OFF*s)*sum(x)
 //    (OFF = 128 for Q4, 0 for Q8), in f32.  One chunk never straddles a
 //    group (group sizes 32/64/128 >= chunk).
@@ -71,7 +73,8 @@ __global__ __launch_bounds__(64 * W) void qmv_row_kernel(const uint16_t* __restr
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int row0 = (blockIdx.x * W + wave) * R;
-  const int G = K / gs;
+  const int gsh = __builtin_ctz(gs);  // group sizes are powers of two (32, 64, 128)
+  const int G = K >> gsh;
 
   // 1. x pieces (first: the staging waits on them, the codes can keep coming)
   uint4 xv[XPT];
@@ -95,7 +98,7 @@ __global__ __launch_bounds__(64 * W) void qmv_row_kernel(const uint16_t* __restr
     const int n = min(row0 + r, N - 1);
 #pragma unroll
     for (int t = 0; t < NI; t++) {
-      const int g = (t * 64 + lane) * CPL / gs;
+      const int g = ((t * 64 + lane) * CPL) >> gsh;
       sv[r][t] = sc[static_cast<int64_t>(n) * G + g];
       bv[r][t] = bi[static_cast<int64_t>(n) * G + g];
     }
@@ -113,8 +116,8 @@ __global__ __launch_bounds__(64 * W) void qmv_row_kernel(const uint16_t* __restr
       f[2 * e + 1] = bf16_bits_to_f32(a[e] >> 16);
     }
     if (BITS == 4) {
-      xp[q] = make_uint4((a[0] & 0xFFFFu) | (a[2] << 16), (a[0] >> 16) | (a[2] & 0xFFFF0000u),
-                         (a[1] & 0xFFFFu) | (a[3] << 16), (a[1] >> 16) | (a[3] & 0xFFFF0000u));
+      xp[q] = make_uint4(__builtin_amdgcn_perm(a[1], a[0], 0x05040100u), __builtin_amdgcn_perm(a[3], a[2], 0x05040100u),
+                         __builtin_amdgcn_perm(a[1], a[0], 0x07060302u), __builtin_amdgcn_perm(a[3], a[2], 0x07060302u));
     } else {
       xp[q] = xv[i];
     }
@@ -145,7 +148,11 @@ __global__ __launch_bounds__(64 * W) void qmv_row_kernel(const uint16_t* __restr
 #pragma unroll
       for (int k = 0; k < 4; k++) {
         if (BITS == 4) {
-          p[2 * k] = wd[k];  // decoded per use below (one and-or each)
+          // even nibbles (k0,k2,k4,k6) and odd nibbles as bytes, interleaved
+          // with 0x43: (k0,k2) (k4,k6) (k1,k3) (k5,k7); p[2k], p[2k+1] and
+          // the next pair of slots of the same k are reused below
+          p[2 * k] = wd[k] & 0x0F0F0F0Fu;
+          p[2 * k + 1] = (wd[k] >> 4) & 0x0F0F0F0Fu;
         } else {
           decode_q8(wd[k], p[2 * k], p[2 * k + 1]);
         }
@@ -160,11 +167,11 @@ __global__ __launch_bounds__(64 * W) void qmv_row_kernel(const uint16_t* __restr
 #pragma unroll
           for (int k = 0; k < 4; k++) {
             const uint4 X = xq[k];
-            const uint32_t w = p[2 * k];
-            d = dot2((w & 0x000F000Fu) | 0x43004300u, X.x, d);
-            d = dot2(((w >> 4) & 0x000F000Fu) | 0x43004300u, X.y, d);
-            d = dot2(((w >> 8) & 0x000F000Fu) | 0x43004300u, X.z, d);
-            d = dot2(((w >> 12) & 0x000F000Fu) | 0x43004300u, X.w, d);
+            const uint32_t lo = p[2 * k], hi = p[2 * k + 1], c43 = 0x43434343u;
+            d = dot2(__builtin_amdgcn_perm(lo, c43, 0x00050004u), X.x, d);
+            d = dot2(__builtin_amdgcn_perm(lo, c43, 0x00070006u), X.y, d);
+            d = dot2(__builtin_amdgcn_perm(hi, c43, 0x00050004u), X.z, d);
+            d = dot2(__builtin_amdgcn_perm(hi, c43, 0x00070006u), X.w, d);
           }
         } else {
           const uint4* xq = xp + m * NP + ch * 2;
