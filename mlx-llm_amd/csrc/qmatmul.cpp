@@ -82,8 +82,11 @@ extern "C" int mlxq_qmatmul_algo(const void* x, int64_t M, const uint32_t* wq, c
   // its per-row decode and LDS reads make it slower than the kernels below).
   // MLXQ_QMV_NO_ROW=1 skips it, MLXQ_QMV_ROW_ALL=1 takes it for every M <= 4.
   const Overrides& ov = overrides();
-  if (qmv_row_eligible(M, N, K, group_size, bits) && (M == 1 || N <= 2048 || ov.qmv_row_all) && !ov.qmv_no_row &&
-      !ov.qmv_mfma)
+  // M = 2: also on the taller matrices except Q4 gate/up-like ones (Q8 gate
+  // 17.0 -> 14.4 us, Q8 q 7.0 -> 6.3, Q4 q 6.0 -> 5.7; Q4 gate stays on qmv_dot)
+  const bool row_m2 = M == 2 && !(bits == 4 && K < N && N * K >= (int64_t(1) << 25));
+  if (qmv_row_eligible(M, N, K, group_size, bits) && (M == 1 || row_m2 || N <= 2048 || ov.qmv_row_all) &&
+      !ov.qmv_no_row && !ov.qmv_mfma)
     return launch_qmv_row(xp, M, wq, sp, bp, bias, N, K, group_size, bits, yp, st);
   if (M <= kQmvDotMaxM && qmv_dot_eligible(M, N, K, group_size, bits) && !ov.qmv_mfma &&
       (qmv_dot_preferred(M, N, K, bits) || ov.qmv_dot_all))
@@ -191,6 +194,9 @@ extern "C" int mlxq_qmatmul_fused(const void* x, int64_t M, int64_t K, const voi
                                             " only the residual / multi-projection forms (M <= 32) are fused");
     return launch_qmv_mfma(f, as_stream(stream));
   }
+  // whole-row kernel where it covers the shape (M = 1, rows of 1, 2 or 4 KB:
+  // the batch-1 chain's q/k/v, o and gate/up); MLXQ_QMV_NO_ROW=1 skips it
+  if (qmv_row_fused_eligible(f) && !overrides().qmv_no_row) return launch_qmv_row_fused(f, as_stream(stream));
   return launch_qmv_dot_fused(f, as_stream(stream));
 }
 

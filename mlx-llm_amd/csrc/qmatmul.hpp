@@ -63,6 +63,10 @@ struct QmvFused {
   int group_size, bits;
 };
 int launch_qmv_dot_fused(const QmvFused& f, hipStream_t st);
+// the same fused forms on the whole-row kernel (qmv_row.hip): M = 1, K*bits/8
+// of 1, 2 or 4 KB
+bool qmv_row_fused_eligible(const QmvFused& f);
+int launch_qmv_row_fused(const QmvFused& f, hipStream_t st);
 
 // qmv_mfma: matrix-core GEMV for M <= kQmvMaxM with the streaming structure
 // of qmv_dot; plain and residual / multi-projection forms (no norm, SwiGLU or

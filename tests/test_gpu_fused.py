@@ -141,3 +141,45 @@ def test_norm_gate_up_swiglu_batch1_ragged(torch_gpu, bits, gs, k):
     mlxq.qmatmul_fused(dev(x, True), [dg, du], gs, bits, norm_weight=dev(w, True), eps=1e-5, swiglu=True)
     xn = orc.rms_norm(x, w, 1e-5)
     check(dg["y"], orc.silu_mul(orc.qlinear_bf16(xn, hg, gs, bits), orc.qlinear_bf16(xn, hu, gs, bits)))
+
+
+@pytest.mark.parametrize("path", ["row", "dot"])
+@pytest.mark.parametrize("bits", [4, 8])
+def test_batch1_forms_both_kernels(torch_gpu, monkeypatch, path, bits):
+    """The batch-1 fused forms on both kernels that serve them: the whole-row
+    kernel (the default where it covers the shape) and the vector-ALU kernel
+    (MLXQ_QMV_NO_ROW=1): norm + q/k/v, head repeat + o + residual, norm +
+    gate/up + SwiGLU, ragged N, against the oracle's unfused chain."""
+    if path == "dot":
+        monkeypatch.setenv("MLXQ_QMV_NO_ROW", "1")
+    else:
+        monkeypatch.delenv("MLXQ_QMV_NO_ROW", raising=False)
+    k, gs = 4096, 64
+    x = bf16_acts(140 + bits, 1, k)
+    w = orc.f32_to_bf16(orc.normal(141, k, 1.0, 0.1))
+    xn = orc.rms_norm(x, w, 1e-5)
+    host_w, projs = [], []
+    for i, n in enumerate([4096, 1000, 1000]):
+        hw, dw = qlayer(142 + i + bits, n, k, gs, bits)
+        host_w.append(hw)
+        dw["y"] = out_like(1, n)
+        projs.append(dw)
+    mlxq.qmatmul_fused(dev(x, True), projs, gs, bits, norm_weight=dev(w, True), eps=1e-5)
+    for hw, p in zip(host_w, projs):
+        check(p["y"], orc.qlinear_bf16(xn, hw, gs, bits))
+    # head repeat + o + residual
+    kvh, hd, groups = 8, 128, 4
+    v = bf16_acts(146, 1, kvh * hd)
+    r = bf16_acts(147, 1, 4000)
+    ho, do = qlayer(148 + bits, 4000, k, gs, bits)
+    do["y"] = out_like(1, 4000)
+    do["residual"] = dev(r, True)
+    mlxq.qmatmul_fused(dev(v, True), [do], gs, bits, repeat=(kvh, hd, groups))
+    xr = orc.repeat_kv(v, kvh, hd, groups)
+    check(do["y"], orc.add(r, orc.qlinear_bf16(xr, ho, gs, bits)))
+    # norm + gate/up + SwiGLU
+    hg, dg = qlayer(149 + bits, 1500, k, gs, bits)
+    hu, du = qlayer(150 + bits, 1500, k, gs, bits)
+    dg["y"], du["y"] = out_like(1, 1500), out_like(1, 1500)
+    mlxq.qmatmul_fused(dev(x, True), [dg, du], gs, bits, norm_weight=dev(w, True), eps=1e-5, swiglu=True)
+    check(dg["y"], orc.silu_mul(orc.qlinear_bf16(xn, hg, gs, bits), orc.qlinear_bf16(xn, hu, gs, bits)))
