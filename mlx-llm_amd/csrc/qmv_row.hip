@@ -406,6 +406,9 @@ int launch_fused_r(RowParams& a, int R, hipStream_t st) {
 }
 template <int BITS, int F>
 int launch_fused_f(RowParams& a, int64_t ni, int R, hipStream_t st) {
+  if constexpr (BITS == 4 && F == 0) {  // the down projection (+ residual): 7 KB rows, 8 waves
+    if (ni == 7) return launch_rw<4, 7, 1, 8, 1, 0>(a, set_tiles(a, 1, 8, false), st);
+  }
   if (ni == 1) return launch_fused_r<BITS, 1, F>(a, R, st);
   if (ni == 2) return launch_fused_r<BITS, 2, F>(a, R, st);
   return launch_fused_r<BITS, 4, F>(a, R, st);
@@ -427,10 +430,10 @@ bool qmv_row_eligible(int64_t M, int64_t N, int64_t K, int group_size, int bits)
   if (M > 1 && K > 4096) return false;  // the activation rows share the workgroup's LDS
   if ((K * bits / 8) % 1024) return false;
   const int64_t ni = K * bits / 8 / 1024;
-  // Q4 with 7 KB rows (the down projection, K = 14336) measured faster on
-  // qmv_dot (10.3 vs 10.9 us): the 28 KB activation staging per workgroup of
-  // 4 rows costs more than the whole-row loads save there
-  if (bits == 4 && ni >= 7) return false;
+  // Q4 with 7 KB rows (the down projection, K = 14336): 8 waves per
+  // workgroup share the 28 KB activation staging (9.92 -> 9.50 us against
+  // qmv_dot); 14 KB and longer Q4 rows stay on qmv_dot
+  if (bits == 4 && ni >= 14 && !overrides().qmv_row_all) return false;
   return ni == 1 || ni == 2 || ni == 4 || ni == 7 || ni == 8 || ni == 14 || ni == 16;
 }
 
@@ -439,7 +442,7 @@ bool qmv_row_eligible(int64_t M, int64_t N, int64_t K, int group_size, int bits)
 void qmv_row_geometry(int64_t N, int64_t K, int bits, int& R, int& W) {
   const int64_t ni = K * bits / 8 / 1024;
   R = bits == 4 && ni <= 2 && N >= 4096 ? 2 : 1;  // Q4 q/o 4.96 vs 5.18 us, gate 9.72 vs 10.48; Q8 best at 1
-  W = 4;                                          // Q8 down: 15.8 us at 4 waves, 16.2 at 8, 17.6 at 16
+  W = bits == 4 && ni >= 7 ? 8 : 4;               // Q8 down: 14.2 us at 4 waves, 16.9 at 8; Q4 down 9.7 at 4, 9.5 at 8
   if (overrides().row_r) R = overrides().row_r;
   if (overrides().row_w) W = overrides().row_w;
 }
@@ -503,7 +506,8 @@ bool qmv_row_fused_eligible(const QmvFused& f) {
   if (f.group_size != 32 && f.group_size != 64 && f.group_size != 128) return false;
   if ((f.K * f.bits / 8) % 1024) return false;
   const int64_t ni = f.K * f.bits / 8 / 1024;
-  if (ni != 1 && ni != 2 && ni != 4) return false;
+  const bool plain = !f.norm_w && !f.swiglu && f.rep <= 1;
+  if (ni != 1 && ni != 2 && ni != 4 && !(ni == 7 && f.bits == 4 && plain)) return false;
   if (f.nproj < 1 || f.nproj > row::kMaxSegs || (f.swiglu && f.nproj != 2)) return false;
   if (f.swiglu && f.proj[0].N != f.proj[1].N) return false;
   if (f.rep > 1 && (f.rep_hd <= 0 || f.rep_hd % 8 || f.K % (static_cast<int64_t>(f.rep_hd) * f.rep))) return false;

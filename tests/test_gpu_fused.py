@@ -183,3 +183,10 @@ def test_batch1_forms_both_kernels(torch_gpu, monkeypatch, path, bits):
     dg["y"], du["y"] = out_like(1, 1500), out_like(1, 1500)
     mlxq.qmatmul_fused(dev(x, True), [dg, du], gs, bits, norm_weight=dev(w, True), eps=1e-5, swiglu=True)
     check(dg["y"], orc.silu_mul(orc.qlinear_bf16(xn, hg, gs, bits), orc.qlinear_bf16(xn, hu, gs, bits)))
+    # down + residual at K = 14336 (Q4: 7 KB rows on the whole-row kernel)
+    hd_, dd = qlayer(151 + bits, 1000, 14336, gs, bits)
+    a = bf16_acts(152, 1, 14336)
+    r2 = bf16_acts(153, 1, 1000)
+    dd["y"], dd["residual"] = out_like(1, 1000), dev(r2, True)
+    mlxq.qmatmul_fused(dev(a, True), [dd], gs, bits)
+    check(dd["y"], orc.add(r2, orc.qlinear_bf16(a, hd_, gs, bits)))
