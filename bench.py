@@ -32,11 +32,11 @@ HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, published
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, published
 METRIC = "Q4/Q8 qmatmul GB/s & TFLOP/s (% roofline), Llama-3-8B proj shapes, 1 GPU"
 # measured HBM traffic per launch (bytes) of a dominant-kernel candidate, keyed (bits, M, K, N)
-TRAFFIC_BYTES = {(8, 32, 4096, 14336): 95_506_516}
+TRAFFIC_BYTES = {(8, 32, 4096, 14336): 65_598_036}
 # measured HBM traffic per call of the Q4 g64 M=1 GEMV, by projection shape
 # (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated; profiles/qmv_q4_m1_traffic.md)
-HEADLINE_TRAFFIC = {"q": 9_586_401, "k": 2_483_355, "v": 2_483_355, "o": 9_586_401, "gate": 33_212_044,
-                    "up": 33_212_044, "down": 33_439_531}
+HEADLINE_TRAFFIC = {"q": 9_584_354, "k": 2_482_332, "v": 2_482_332, "o": 9_584_354, "gate": 33_209_997,
+                    "up": 33_209_997, "down": 33_357_387}
 # MFMA busy fraction of the prefill qmm calls from SQ counters
 # (SQ_VALU_MFMA_BUSY_CYCLES / (SIMDs x GRBM_GUI_ACTIVE); profiles/qmm_prefill_m2048_mfma_counters.md)
 PREFILL_MFMA_BUSY = {"gate_up": 0.408, "down": 0.468}
@@ -248,14 +248,20 @@ def main(argv=None) -> int:
     achieved = dbytes / (avg_us * 1e-6) / 1e9
     # which kernels serve the call (the dispatch rule of qmatmul.cpp /
     # qmv_tile.hip, restated here for the label only)
-    if dot_preferred(dm, dn, dk, dbits):
+    if dm == 1:
+        kname = "qmv_row_kernel (vector ALU, whole rows per wave)"
+    elif dot_preferred(dm, dn, dk, dbits):
         kname = "qmv_dot_kernel (vector ALU)"
+    elif tile_preferred(dm, dn, dk, dbits) and stream_splits(dm, dn, dk, dbits) == 1:
+        kname = "qmv_stream_kernel (MFMA, a workgroup streams its rows over the whole K; one launch)"
+    elif tile_preferred(dm, dn, dk, dbits) and stream_splits(dm, dn, dk, dbits):
+        kname = "qmv_stream_kernel + split_reduce4_kernel (MFMA, K in 4 splits; one call = both launches)"
     elif tile_preferred(dm, dn, dk, dbits):
         kname = "qmv_tile_kernel + split_reduce4_kernel (MFMA, split K; one call = both launches)"
     else:
         kname = "qmv_kernel (MFMA)"
-    # HBM bytes per call (both kernels) from rocprofv3 FETCH_SIZE / WRITE_SIZE
-    # runs (scaled by a 64 MiB copy's readings), profiles/qmv_tile_q8_m32_gate_traffic.md;
+    # HBM bytes per call from rocprofv3 FETCH_SIZE / WRITE_SIZE
+    # runs (scaled by a 64 MiB copy's readings), profiles/qmv_stream_q8_m32_gate_traffic.md;
     # known for that call only
     traffic = TRAFFIC_BYTES.get((dbits, dm, dk, dn))
     roofline = {"kernel": f"{kname}, Q{dbits} g64, M={dm}, K={dk} -> N={dn}", "bound": "hbm",
@@ -407,6 +413,18 @@ def tile_preferred(m, n, k, bits):
     if large:
         return m >= (8 if bits == 4 else 16)
     return m >= (24 if bits == 4 else 32)
+
+
+def stream_splits(m, n, k, bits):
+    """K splits of the streaming form where qmv_tile.hip's stream_preferred
+    takes it (0: not taken), for labels."""
+    if n * k < 1 << 25 or m < 8:
+        return 0
+    if k < n:
+        return 1
+    if m > 16 or (bits == 8 and m == 16):
+        return 4
+    return 0
 
 
 def dot_preferred(m, n, k, bits):
