@@ -182,8 +182,8 @@ template <int D>
 __global__ __launch_bounds__(kThreads, 1) void decode_step_kernel(const DStage* st_g, int NS,
                                                                   const uint16_t* __restrict__ x_arg,
                                                                   uint16_t* __restrict__ logits, DHeader* hdr,
-                                                                  int max_kin, int max_k, int hidden, int trace_on,
-                                                                  unsigned long long timeout_ticks) {
+                                                                  int max_kin, int max_k, int hidden, int vocab,
+                                                                  int trace_on, unsigned long long timeout_ticks) {
   extern __shared__ __align__(16) unsigned char smem[];
   const Lds L = lds_layout(max_kin, max_k, hidden, NS);
   uint16_t* raw = reinterpret_cast<uint16_t*>(smem + L.raw);
@@ -217,11 +217,15 @@ __global__ __launch_bounds__(kThreads, 1) void decode_step_kernel(const DStage* 
       const int kind = st[s].kind, flags = st[s].flags;
       stamp(s, 0);
       if (s > 0) {
-        // grid barrier: this workgroup's outputs (agent-coherent stores) are
-        // complete before it arrives; arrival is one relaxed agent-scope add
+        // grid barrier: this workgroup's outputs are complete before it
+        // arrives (the compute waves' stores retired before the workgroup
+        // barrier that ended the previous stage); an agent-scope release
+        // fence makes them visible to the other XCDs before the arrival, and
+        // an acquire fence after the wait makes theirs visible here
         int ok = 1;
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         __builtin_amdgcn_s_waitcnt(0);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         if (lane == 0) {
           const int grp = g % kGroups, ngroups = G < kGroups ? G : kGroups;
@@ -251,8 +255,12 @@ __global__ __launch_bounds__(kThreads, 1) void decode_step_kernel(const DStage* 
           }
         }
         ok = uni(__shfl(ok, 0));
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         if (!ok) {
+          // a step that times out leaves NaN logits (each workgroup its
+          // share), never the previous step's values
+          for (int i = g * 64 + lane; i < vocab; i += G * 64) logits[i] = 0x7FC0u;
           if (lane == 0) abort_flag = 1;
           __syncthreads();  // meets the compute waves' next stage-entry barrier: they read the flag and leave
           return;
@@ -763,7 +771,7 @@ extern "C" int mlxq_decode_step(const mlxq_decode_plan_t* plan, const void* x, v
   hipLaunchKernelGGL(kern, dim3(plan->grid), dim3(kThreads), plan->lds_bytes,
                      as_stream(stream), stage_table(plan->workspace, plan->stages), plan->stages, static_cast<const uint16_t*>(x),
                      static_cast<uint16_t*>(logits), static_cast<DHeader*>(plan->workspace), plan->max_k,
-                     plan->max_k, plan->hidden, plan->trace,
+                     plan->max_k, plan->hidden, plan->vocab, plan->trace,
                      static_cast<unsigned long long>(plan->timeout_ticks > 0 ? plan->timeout_ticks : 1));
   return check_launch("decode_step");
 }

@@ -115,17 +115,20 @@ def test_persistent_unsupported(torch_gpu):
 def test_persistent_barrier_timeout_path(torch_gpu, monkeypatch):
     """Failure handling forced from the host: a 1-tick barrier wait limit
     makes the grid barriers give up.  Every wave leaves the launch (the
-    bounded waits end it; nothing hangs), the plan reports the time-out, and a
-    fresh plan on the same weights computes the step correctly again."""
+    bounded waits end it; nothing hangs), the plan reports the time-out, the
+    logits hold NaN, and a fresh plan on the same weights computes the step
+    correctly again."""
     import torch
     cfg = StackConfig(**SMALL)
     st = DecodeStack(cfg, batch=1, seed=13, norm_noise=0.1)
     x = orc.f32_to_bf16(orc.normal(777, cfg.hidden, 0.0, 1.0)).reshape(1, cfg.hidden)
     st.x.copy_(dev(x, True))
     monkeypatch.setenv("MLXQ_DECODE_TIMEOUT_TICKS", "1")
+    st.logits.zero_()
     st.forward(1, persistent=True)
     torch.cuda.synchronize()
     assert st.persistent_plan().timed_out()
+    assert torch.isnan(st.logits.float()).any()  # a timed-out step leaves NaN logits, not stale ones
     monkeypatch.delenv("MLXQ_DECODE_TIMEOUT_TICKS")
     st._plan = None  # a new plan: the barrier state starts over
     st.forward(1, persistent=True)
