@@ -67,6 +67,14 @@ struct TileParams {
   int steps;  // K slices per workgroup (streaming form)
 };
 
+// First activation row of this workgroup's M block (blockIdx.z): a call with
+// more activation rows than one workgroup stages runs the blocks side by
+// side, each over the same weight rows.
+template <int MT>
+__device__ __forceinline__ int m_block0() {
+  return static_cast<int>(blockIdx.z) * 16 * MT;
+}
+
 constexpr int kMaxSplitsK = 16;  // most K splits of one call
 
 // Q4 codes of one dword (k0..k7, LSB first) -> bf16 (128 + k) pairs
@@ -151,7 +159,7 @@ __device__ __forceinline__ void tile_load_x(const TileParams& p, int split, Tile
   for (int i = 0; i < Tg::XP; i++) {  // rows past M read row M-1: they only feed output rows >= M
     const int row = Tg::T >= C ? tid / C + i * (Tg::T / C) : i / (C / Tg::T);
     const int col = Tg::T >= C ? tid % C : tid + Tg::T * (i % (C / Tg::T));
-    X.xg[i] = *reinterpret_cast<const u32x4*>(xs0 + min(row, p.M - 1) * p.K + col * 8);
+    X.xg[i] = *reinterpret_cast<const u32x4*>(xs0 + min(m_block0<MT>() + row, p.M - 1) * p.K + col * 8);
   }
 }
 
@@ -341,6 +349,7 @@ __device__ __forceinline__ void tile_finish(const TileParams& p, int tile, int s
   const int rg = wave % Tg::RG, kh = wave / Tg::RG;
   const int r16 = lane & 15, gq = lane >> 4;
   const int n0 = tile * 16 * Tg::RG + rg * 16;  // this wave's 16 weight rows
+  const int mb = m_block0<MT>();
 
   // K parts 1.. hand their sums to part 0 through LDS (added in part order)
   if constexpr (KH > 1) {
@@ -369,7 +378,7 @@ __device__ __forceinline__ void tile_finish(const TileParams& p, int tile, int s
     for (int mt = 0; mt < MT; mt++)
 #pragma unroll
       for (int v = 0; v < 4; v++) {
-        const int m = 16 * mt + 4 * gq + v;
+        const int m = mb + 16 * mt + 4 * gq + v;
         if (m < M) p.y[static_cast<int64_t>(m) * N + nn] = static_cast<uint16_t>(f32_to_bf16_bits(acc[mt][v] + bb));
       }
     return;
@@ -379,12 +388,13 @@ __device__ __forceinline__ void tile_finish(const TileParams& p, int tile, int s
   for (int mt = 0; mt < MT; mt++)
 #pragma unroll
     for (int v = 0; v < 4; v++) {
-      const int m = 16 * mt + 4 * gq + v;
+      const int m = mb + 16 * mt + 4 * gq + v;
       if (m < M) p.part[(static_cast<int64_t>(split) * M + m) * N + nn] = acc[mt][v];
     }
 }
 
-// One item per workgroup: blockIdx.x = tile of 16 RG rows, blockIdx.y = K slice.
+// One item per workgroup: blockIdx.x = tile of 16 RG rows, blockIdx.y = K
+// slice, blockIdx.z = M block.
 template <int BITS, int GS, int MT, int WV, int NCH, int KH>
 __global__ __launch_bounds__(64 * WV) void qmv_tile_kernel(const TileParams p) {
   using Tg = TileGeom<BITS, GS, MT, WV, NCH, KH>;
@@ -512,7 +522,7 @@ struct Cfg {
 };
 
 template <int BITS, int MT, int WV, int NCH, int KH>
-int run(const TileParams& a, int tiles, hipStream_t st, int* query) {
+int run(const TileParams& a, int tiles, int mblocks, hipStream_t st, int* query) {
   auto kern = qmv_tile_kernel<BITS, 64, MT, WV, NCH, KH>;
   if (query) {
     static int cached = -1;
@@ -525,36 +535,46 @@ int run(const TileParams& a, int tiles, hipStream_t st, int* query) {
     *query = cached;
     return MLXQ_OK;
   }
-  hipLaunchKernelGGL(kern, dim3(tiles, a.splits), dim3(64 * WV), 0, st, a);
+  hipLaunchKernelGGL(kern, dim3(tiles, a.splits, mblocks), dim3(64 * WV), 0, st, a);
   return check_launch("qmv_tile");
 }
 
 template <int BITS, int MT, int WV, int NCH, int KH>
-int run_stream(const TileParams& a, int tiles, hipStream_t st) {
-  hipLaunchKernelGGL((qmv_stream_kernel<BITS, 64, MT, WV, NCH, KH>), dim3(tiles, a.splits), dim3(64 * WV), 0, st, a);
+int run_stream(const TileParams& a, int tiles, int mblocks, hipStream_t st) {
+  hipLaunchKernelGGL((qmv_stream_kernel<BITS, 64, MT, WV, NCH, KH>), dim3(tiles, a.splits, mblocks), dim3(64 * WV), 0,
+                     st, a);
   return check_launch("qmv_stream");
 }
 
 // The streaming forms: (waves, Q4 chunks per wave and slice, K parts); Q8
-// takes twice the chunks, so a slice covers the same K either way.
+// takes twice the chunks, so a slice covers the same K either way.  Eight K
+// parts (one row group of 16 rows per workgroup, for short matrices) only
+// with 16 activation rows per workgroup: two such LDS buffers of 2048 k are
+// the most that fit.
 struct SCfg {
   int wv = 8, nch = 2, kh = 2;
 };
-bool scfg_known(const SCfg& c) {
+bool scfg_known(const SCfg& c, int mt) {
   if (c.wv == 8 && (c.kh == 1 || c.kh == 2)) return c.nch == 2 || c.nch == 4;
   if (c.wv == 8 && c.kh == 4) return c.nch == 2;
+  if (c.wv == 8 && c.kh == 8) return c.nch == 2 && mt == 1;
   if (c.wv == 4 && c.kh == 1) return c.nch == 2 || c.nch == 4;
   return false;
 }
 template <int BITS, int MT>
-int dispatch_stream_mt(const SCfg& c, const TileParams& a, int tiles, hipStream_t st) {
+int dispatch_stream_mt(const SCfg& c, const TileParams& a, int tiles, int mb, hipStream_t st) {
   constexpr int F = BITS == 4 ? 1 : 2;
   if (c.wv == 8 && c.kh == 2)
-    return c.nch == 2 ? run_stream<BITS, MT, 8, 2 * F, 2>(a, tiles, st) : run_stream<BITS, MT, 8, 4 * F, 2>(a, tiles, st);
-  if (c.wv == 8 && c.kh == 4) return run_stream<BITS, MT, 8, 2 * F, 4>(a, tiles, st);
+    return c.nch == 2 ? run_stream<BITS, MT, 8, 2 * F, 2>(a, tiles, mb, st)
+                      : run_stream<BITS, MT, 8, 4 * F, 2>(a, tiles, mb, st);
+  if (c.wv == 8 && c.kh == 4) return run_stream<BITS, MT, 8, 2 * F, 4>(a, tiles, mb, st);
+  if constexpr (MT == 1)
+    if (c.wv == 8 && c.kh == 8) return run_stream<BITS, MT, 8, 2 * F, 8>(a, tiles, mb, st);
   if (c.wv == 4)
-    return c.nch == 2 ? run_stream<BITS, MT, 4, 2 * F, 1>(a, tiles, st) : run_stream<BITS, MT, 4, 4 * F, 1>(a, tiles, st);
-  return c.nch == 2 ? run_stream<BITS, MT, 8, 2 * F, 1>(a, tiles, st) : run_stream<BITS, MT, 8, 4 * F, 1>(a, tiles, st);
+    return c.nch == 2 ? run_stream<BITS, MT, 4, 2 * F, 1>(a, tiles, mb, st)
+                      : run_stream<BITS, MT, 4, 4 * F, 1>(a, tiles, mb, st);
+  return c.nch == 2 ? run_stream<BITS, MT, 8, 2 * F, 1>(a, tiles, mb, st)
+                    : run_stream<BITS, MT, 8, 4 * F, 1>(a, tiles, mb, st);
 }
 // Where the streaming form is the default, from interleaved A/B timings
 // against the single-slice form at the Llama-3-8B shapes (weights streamed
@@ -584,32 +604,42 @@ bool stream_preferred(int64_t M, int64_t N, int64_t K, int bits, SCfg& c, int& s
   return false;
 }
 
-int dispatch_stream(int bits, int mt, const SCfg& c, const TileParams& a, int tiles, hipStream_t st) {
-  if (bits == 4) return mt == 1 ? dispatch_stream_mt<4, 1>(c, a, tiles, st) : dispatch_stream_mt<4, 2>(c, a, tiles, st);
-  return mt == 1 ? dispatch_stream_mt<8, 1>(c, a, tiles, st) : dispatch_stream_mt<8, 2>(c, a, tiles, st);
+int dispatch_stream(int bits, int mt, const SCfg& c, const TileParams& a, int tiles, int mb, hipStream_t st) {
+  if (bits == 4) return mt == 1 ? dispatch_stream_mt<4, 1>(c, a, tiles, mb, st) : dispatch_stream_mt<4, 2>(c, a, tiles, mb, st);
+  return mt == 1 ? dispatch_stream_mt<8, 1>(c, a, tiles, mb, st) : dispatch_stream_mt<8, 2>(c, a, tiles, mb, st);
 }
 
 // The instantiated (waves, chunks per wave, K parts) forms: slices of 16
 // chunks only with 8 waves and one K part (<= 16 activation pieces per
 // thread); K parts of 2 (4 or 8 chunks) and 4 (4 chunks) with 8 waves, so a
-// workgroup slice stays within 16 chunks.
-bool cfg_known(const Cfg& c) {
+// workgroup slice stays within 16 chunks.  Eight K parts (one row group of 16
+// rows) of 4 chunks, or 8 for Q8, with 16 activation rows per workgroup: a
+// slice of 4096 k, the whole K of a Llama-3-8B q/k/v/o row, in 128 KB of LDS.
+bool cfg_known(const Cfg& c, int bits) {
   if (c.kh == 1) return (c.wv == 4 && (c.nch == 4 || c.nch == 8)) || (c.wv == 8 && (c.nch == 4 || c.nch == 8 || c.nch == 16));
+  if (c.kh == 8) return c.wv == 8 && c.mt == 1 && (c.nch == 4 || (c.nch == 8 && bits == 8));
   return c.wv == 8 && ((c.kh == 2 && (c.nch == 4 || c.nch == 8)) || (c.kh == 4 && c.nch == 4));
 }
 
 template <int BITS, int MT>
-int run_wn(const Cfg& c, const TileParams& a, int tiles, hipStream_t st, int* q) {
-  if (c.kh == 2) return c.nch == 4 ? run<BITS, MT, 8, 4, 2>(a, tiles, st, q) : run<BITS, MT, 8, 8, 2>(a, tiles, st, q);
-  if (c.kh == 4) return run<BITS, MT, 8, 4, 4>(a, tiles, st, q);
-  if (c.wv == 4) return c.nch == 4 ? run<BITS, MT, 4, 4, 1>(a, tiles, st, q) : run<BITS, MT, 4, 8, 1>(a, tiles, st, q);
-  if (c.nch == 4) return run<BITS, MT, 8, 4, 1>(a, tiles, st, q);
-  return c.nch == 8 ? run<BITS, MT, 8, 8, 1>(a, tiles, st, q) : run<BITS, MT, 8, 16, 1>(a, tiles, st, q);
+int run_wn(const Cfg& c, const TileParams& a, int tiles, int mb, hipStream_t st, int* q) {
+  if (c.kh == 2) return c.nch == 4 ? run<BITS, MT, 8, 4, 2>(a, tiles, mb, st, q) : run<BITS, MT, 8, 8, 2>(a, tiles, mb, st, q);
+  if (c.kh == 4) return run<BITS, MT, 8, 4, 4>(a, tiles, mb, st, q);
+  if constexpr (MT == 1) {
+    if (c.kh == 8) {
+      if constexpr (BITS == 8)
+        if (c.nch == 8) return run<BITS, MT, 8, 8, 8>(a, tiles, mb, st, q);
+      return run<BITS, MT, 8, 4, 8>(a, tiles, mb, st, q);
+    }
+  }
+  if (c.wv == 4) return c.nch == 4 ? run<BITS, MT, 4, 4, 1>(a, tiles, mb, st, q) : run<BITS, MT, 4, 8, 1>(a, tiles, mb, st, q);
+  if (c.nch == 4) return run<BITS, MT, 8, 4, 1>(a, tiles, mb, st, q);
+  return c.nch == 8 ? run<BITS, MT, 8, 8, 1>(a, tiles, mb, st, q) : run<BITS, MT, 8, 16, 1>(a, tiles, mb, st, q);
 }
 
-int dispatch(int bits, const Cfg& c, const TileParams& a, int tiles, hipStream_t st, int* q) {
-  if (bits == 4) return c.mt == 1 ? run_wn<4, 1>(c, a, tiles, st, q) : run_wn<4, 2>(c, a, tiles, st, q);
-  return c.mt == 1 ? run_wn<8, 1>(c, a, tiles, st, q) : run_wn<8, 2>(c, a, tiles, st, q);
+int dispatch(int bits, const Cfg& c, const TileParams& a, int tiles, int mb, hipStream_t st, int* q) {
+  if (bits == 4) return c.mt == 1 ? run_wn<4, 1>(c, a, tiles, mb, st, q) : run_wn<4, 2>(c, a, tiles, mb, st, q);
+  return c.mt == 1 ? run_wn<8, 1>(c, a, tiles, mb, st, q) : run_wn<8, 2>(c, a, tiles, mb, st, q);
 }
 
 int cu_count() {
@@ -624,6 +654,27 @@ int64_t chunks_of(int64_t K, int bits) { return K * bits / 8 / 64; }
 }  // namespace tile
 
 using namespace tile;
+
+namespace {
+// Short matrices whose whole K one workgroup stages (8 waves as 8 K parts of
+// one 16-row group, 16 activation rows per M block): one workgroup per CU
+// (the LDS holds 16 x K activations), taken while tiles x M blocks fill at
+// most one round of CUs, so no K split and no second launch.  Measured at
+// the Llama-3-8B shapes (interleaved A/B, weights streamed from HBM): k/v
+// Q4 M = 6..32 6.6-8.2 -> 6.4-6.5 us, Q8 7.6-8.2 -> 7.1-7.2; q/o Q4 from M
+// = 8 (6.93 -> 6.69, M = 16 8.51 -> 6.84), Q8 from M = 12 (8.53 -> 8.25, M
+// = 16 9.54 -> 8.31); two M blocks of q/o take two rounds of CUs and are
+// slower than the 32-row forms.
+bool short_fullk(int64_t M, int64_t N, int64_t K, int bits, Cfg* c) {
+  if (N * K >= (int64_t(1) << 25) || M < (N <= 2048 ? 6 : bits == 4 ? 8 : 12)) return false;
+  const int64_t ch = chunks_of(K, bits);
+  const Cfg f{1, 8, static_cast<int>(ch / 8), 8};
+  if (ch % 8 || !cfg_known(f, bits)) return false;
+  if (ceil_div(N, 16) * ceil_div(M, 16) > cu_count()) return false;
+  if (c) *c = f;
+  return true;
+}
+}  // namespace
 
 bool qmv_tile_eligible(int64_t M, int64_t N, int64_t K, int group_size, int bits) {
   if (M < 1 || M > kQmvMaxM || N < 1 || group_size != 64) return false;
@@ -643,6 +694,7 @@ bool qmv_tile_preferred(int64_t M, int64_t N, int64_t K, int bits) {
   // M = 16, and on the other small projections from M = 24 (Q4) / 32 (Q8).
   const bool large = N * K >= (int64_t(1) << 25);
   if (M <= 4) return large && K < N && bits == 4 && M >= 3;
+  if (short_fullk(M, N, K, bits, nullptr)) return true;
   if (large) return M >= (bits == 4 ? 8 : 16);
   if (N <= 2048) return M >= 16;  // k/v: M = 16 Q4 8.28 -> 7.93 us, Q8 9.27 -> 8.06; Q8 M = 24 11.07 -> 8.93
   return M >= (bits == 4 ? 24 : 32);
@@ -689,13 +741,17 @@ int launch_qmv_tile(const uint16_t* x, int64_t M, const uint32_t* wq, const uint
       use = stream_preferred(M, N, K, bits, c, splits);
     }
     const int64_t per = c.nch * (bits == 4 ? 1 : 2) * c.kh;  // chunks per K slice
-    if (use && scfg_known(c) && ch % per == 0 && (ch / per) % splits == 0 && splits <= kMaxSplits &&
+    // one M block of up to 32 rows, or (eight K parts, or MLXQ_QMV_TILE_MB)
+    // blocks of 16
+    const int mt = M <= 16 || c.kh == 8 || ov.tile_mb ? 1 : 2;
+    if (use && scfg_known(c, mt) && ch % per == 0 && (ch / per) % splits == 0 && splits <= kMaxSplits &&
         (splits == 1 || splits <= fit)) {
       a.splits = splits;
       a.steps = static_cast<int>(ch / per / splits);
       a.part = splits > 1 ? static_cast<float*>(workspace) : nullptr;
       const int64_t tiles = ceil_div(N, 16 * (c.wv / c.kh));
-      if (int rc = dispatch_stream(bits, M <= 16 ? 1 : 2, c, a, static_cast<int>(tiles), st)) return rc;
+      const int mb = static_cast<int>(ceil_div(M, 16 * mt));
+      if (int rc = dispatch_stream(bits, mt, c, a, static_cast<int>(tiles), mb, st)) return rc;
       if (splits == 1) return MLXQ_OK;
       return launch_split_reduce(a.part, bias, y, M, N, splits, st);
     }
@@ -712,8 +768,9 @@ int launch_qmv_tile(const uint16_t* x, int64_t M, const uint32_t* wq, const uint
   // the others.
   const bool large = N * K >= (int64_t(1) << 25);
   Cfg pref;
-  pref.mt = M <= 16 ? 1 : 2;
-  if (large || (bits == 8 && M > 16 && N > 2048)) {
+  pref.mt = M <= 16 || overrides().tile_mb ? 1 : 2;
+  if (short_fullk(M, N, K, bits, &pref)) {
+  } else if (large || (bits == 8 && M > 16 && N > 2048)) {
     pref.wv = 8; pref.nch = 8; pref.kh = 2;
   } else if (N <= 2048 && bits == 4 && M > 16) {
     pref.wv = 4; pref.nch = 4; pref.kh = 1;
@@ -724,11 +781,12 @@ int launch_qmv_tile(const uint16_t* x, int64_t M, const uint32_t* wq, const uint
   if (fwv) pref.wv = fwv;
   if (fnch) pref.nch = fnch;
   if (fkh) pref.kh = fkh;
+  if (pref.kh == 8) pref.mt = 1;  // eight K parts: M blocks of 16 rows
   const Cfg order[] = {pref,           {pref.mt, 8, 16, 1}, {pref.mt, 8, 8, 1}, {pref.mt, 4, 8, 1},
                        {pref.mt, 4, 4, 1}, {pref.mt, 8, 4, 1}};
   const Cfg* pick = nullptr;
   for (const Cfg& c : order) {
-    if (!cfg_known(c)) continue;
+    if (!cfg_known(c, bits)) continue;
     if (ch % (c.nch * c.kh)) continue;
     const int64_t splits = ch / (c.nch * c.kh);
     if (splits > kMaxSplits || (splits > 1 && splits > fit)) continue;
@@ -744,7 +802,8 @@ int launch_qmv_tile(const uint16_t* x, int64_t M, const uint32_t* wq, const uint
   // slices) was measured slower at the Llama-3-8B shapes (Q8 M = 32 gate
   // 26.1 -> 26.9 us): its agent-coherent partial stores and serial tail cost
   // more than the launch it saves.
-  if (int rc = dispatch(bits, *pick, a, static_cast<int>(tiles), st, nullptr)) return rc;
+  const int mb = static_cast<int>(ceil_div(M, 16 * pick->mt));
+  if (int rc = dispatch(bits, *pick, a, static_cast<int>(tiles), mb, st, nullptr)) return rc;
   if (a.splits == 1) return MLXQ_OK;
   return launch_split_reduce(a.part, bias, y, M, N, a.splits, st);
 }

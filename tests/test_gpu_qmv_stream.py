@@ -39,6 +39,9 @@ CASES = [
     ("8,2,2,4", 4096),   # four splits of two steps
     ("8,2,2,4", 2048),   # four splits of one step
     ("4,4,1,4", 4096),
+    ("8,2,8,1", 2048),   # eight K parts: one step (M blocks of 16 above 16 rows)
+    ("8,2,8,1", 6144),   # three steps
+    ("8,2,8,2", 8192),   # two splits of two steps
 ]
 
 

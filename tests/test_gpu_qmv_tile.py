@@ -36,6 +36,51 @@ def test_tile_configs(torch_gpu, tile_all, bits, cfg, m):
 
 
 @pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("cfg", ["4,4", "8,8,2", "8,4,4"])
+@pytest.mark.parametrize("m", [17, 32])
+def test_tile_m_blocks(torch_gpu, tile_all, bits, cfg, m):
+    """Activation rows in M blocks of 16 (one workgroup per block and row
+    tile, over the same weight rows)."""
+    tile_all.setenv("MLXQ_QMV_TILE", cfg)
+    tile_all.setenv("MLXQ_QMV_TILE_MB", "1")
+    n, k = 200, 2048
+    wq, s, b = make_layer(42 + bits, n, k, 64, bits)
+    x = bf16_acts(52 + m, m, k)
+    assert rel_err(run(x, wq, s, b, 64, bits), orc.qmatmul_f64(x, wq, s, b, 64, bits)) <= TIGHT
+
+
+@pytest.mark.parametrize("bits,cfg", [(4, "8,4,8"), (8, "8,4,8"), (8, "8,8,8")])
+@pytest.mark.parametrize("k", [4096, 8192])
+@pytest.mark.parametrize("m", [5, 16, 17, 32])
+def test_tile_eight_k_parts(torch_gpu, tile_all, bits, cfg, k, m):
+    """Eight K parts of one 16-row group: a 4096-k slice (the whole K, or two
+    splits at K = 8192; 2048 for Q8 with 4 chunks per wave), M blocks of 16
+    above 16 rows."""
+    tile_all.setenv("MLXQ_QMV_TILE", cfg)
+    n = 200
+    wq, s, b = make_layer(44 + bits, n, k, 64, bits)
+    x = bf16_acts(54 + m, m, k)
+    assert rel_err(run(x, wq, s, b, 64, bits), orc.qmatmul_f64(x, wq, s, b, 64, bits)) <= TIGHT
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("proj,m", [("k", 6), ("k", 16), ("k", 32), ("q", 8), ("q", 12), ("q", 16), ("q", 32)])
+def test_tile_default_short(torch_gpu, monkeypatch, bits, proj, m):
+    """The short Llama-3-8B projections under the default dispatch (the
+    whole-K eight-part form where it fits one round of CUs), sampled rows
+    against the oracle."""
+    for v in ("MLXQ_QMV_TILE", "MLXQ_QMV_TILE_ALL", "MLXQ_QMV_TILE_MB", "MLXQ_QMV_TILE_STREAM"):
+        monkeypatch.delenv(v, raising=False)
+    n = {"k": 1024, "q": 4096}[proj]
+    k = 4096
+    wq, s, b = make_layer(46 + bits, n, k, 64, bits)
+    x = bf16_acts(56 + m, m, k)
+    y = run(x, wq, s, b, 64, bits)
+    rows = np.random.default_rng(57).choice(n, 256, replace=False)
+    assert rel_err(y[:, rows], orc.qmatmul_f64(x, wq[rows], s[rows], b[rows], 64, bits)) <= TIGHT
+
+
+@pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("m", [8, 32])
 def test_tile_bias_and_outliers(torch_gpu, tile_all, bits, m):
     n, k = 640, 4096
