@@ -11,7 +11,8 @@ its wall time: HBM GB/s of the whole job.
 Extra fields (same JSON line):
   roofline      dominant kernel of the step, HIP-event timed per launch
   kernels       per (bits, M) decode GEMV GB/s and % of 8 TB/s
-  prefill       config 3: qmm at M=2048, Q4, 4096->14336 and 14336->4096, TFLOP/s
+  prefill       config 3: qmatmul at M=2048, Q4, 4096->14336 and 14336->4096, TFLOP/s (default
+                route and the fused qmm kernel)
   gguf          config 4: block dequant of a 14336x4096 tensor, GB/s per type
   decode_stack  config 5: quantized Llama-3-8B decode step, tokens/s at batch 1 and 16
   cpu_baseline  the CPU restatement (oracle, OpenMP) on a bounded sample
@@ -318,26 +319,38 @@ def bench_prefill(torch, mlxq, iters=10):
         wq, s, b = mlxq.quantize(w.to(torch.bfloat16), 64, 4)
         x = torch.randn((2048, k), generator=g, device="cuda").to(torch.bfloat16)
         y = torch.empty((2048, n), device="cuda", dtype=torch.bfloat16)
-        fn = mlxq.bind_qmatmul(x, wq, s, b, 64, 4, out=y)
-        for _ in range(100):  # the first launches of a ~300 us kernel run below full clocks (~30 ms to settle)
-            fn()
-        torch.cuda.synchronize()
-        reps = []
-        for _ in range(5):  # median of 5 batches of `iters` launches
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
-            for _ in range(iters):
+        def timed(algo):
+            fn = mlxq.bind_qmatmul(x, wq, s, b, 64, 4, out=y, algo=algo)
+            for _ in range(100):  # the first launches of a ~300 us kernel run below full clocks (~30 ms to settle)
                 fn()
-            e1.record()
             torch.cuda.synchronize()
-            reps.append(e0.elapsed_time(e1) * 1e3 / iters)
-        us = sorted(reps)[len(reps) // 2]
+            reps = []
+            for _ in range(5):  # median of 5 batches of `iters` launches
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for _ in range(iters):
+                    fn()
+                e1.record()
+                torch.cuda.synchronize()
+                reps.append(e0.elapsed_time(e1) * 1e3 / iters)
+            return sorted(reps)[len(reps) // 2]
+
+        # the default route (mlxq_qmatmul): at M = 2048 the weight dequantized
+        # into the workspace + hipBLASLt's bf16 GEMM; beside it the fused
+        # LDS-dequant MFMA kernel (what the no-alloc entry point runs)
+        lib_route = mlxq.workspace_size(2048, n, k, 64, 4) >= n * k * 2
+        us = timed(mlxq.ALGO_AUTO)
+        us_fused = timed(mlxq.ALGO_QMM)
         tf = 2.0 * 2048 * n * k / (us * 1e-6) / 1e12
+        tf_fused = 2.0 * 2048 * n * k / (us_fused * 1e-6) / 1e12
         res[name] = {"us": round(us, 1), "TFLOP/s": round(tf, 1), "frac_mfma_bf16": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                     "route": "dequantize + hipBLASLt bf16 GEMM" if lib_route else "fused qmm_kernel",
                      "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
                                   "unit": "TFLOP/s", "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
-                                  "flops_per_launch": 2 * 2048 * n * k,
-                                  "mfma_busy_counter": PREFILL_MFMA_BUSY[name]}}
+                                  "flops_per_launch": 2 * 2048 * n * k},
+                     "fused_qmm": {"us": round(us_fused, 1), "TFLOP/s": round(tf_fused, 1),
+                                   "frac_mfma_bf16": round(tf_fused / MFMA_BF16_PEAK_TFLOPS, 4),
+                                   "mfma_busy_counter": PREFILL_MFMA_BUSY[name]}}
         # reference point, not part of the path: the library's plain bf16 GEMM
         # (torch -> hipBLASLt) of the same shape on already dequantized weights
         wd = w.to(torch.bfloat16)

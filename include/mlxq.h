@@ -56,7 +56,10 @@ typedef enum {
 typedef enum {
   MLXQ_ALGO_AUTO = 0, /* qmv for M <= 32, qmm above (what mlxq_qmatmul does) */
   MLXQ_ALGO_QMV = 1,  /* decode GEMV, any M <= 32                             */
-  MLXQ_ALGO_QMM = 2   /* LDS-dequant bf16 MFMA GEMM, any M                    */
+  MLXQ_ALGO_QMM = 2,  /* LDS-dequant bf16 MFMA GEMM, any M                    */
+  MLXQ_ALGO_QMM_LIB = 3 /* dequantize into the workspace, then hipBLASLt's bf16
+                           GEMM (needs mlxq_qmatmul_workspace_size bytes at a
+                           shape where MLXQ_ALGO_AUTO takes it; see there)      */
 } mlxq_algo;
 
 /* Message for the last failing call on this thread ("" if none). */
@@ -101,9 +104,13 @@ int mlxq_dequantize(const uint32_t* wq, const void* scales, const void* biases,
  * with too few 256 x 256 output tiles to fill the GPU (e.g. M = 2048,
  * 14336 -> 4096: 2 x M x N x 4 bytes), where the kernel splits K across
  * workgroups and a second kernel adds the f32 partial sums in slice order.
+ * At prefill shapes where it is measured faster (M >= 512, or M >= 2048
+ * when K > N) the size is instead that of the whole weight dequantized to
+ * bf16 (N x K x 2 bytes) plus 32 MiB for hipBLASLt: the call dequantizes
+ * into the workspace and runs hipBLASLt's bf16 GEMM (MLXQ_ALGO_QMM_LIB).
  * The workspace must be 256-byte aligned; its contents need no
  * initialisation and are scratch after a call.  With no or too small a
- * workspace the call still succeeds on an unsplit kernel. */
+ * workspace the call still succeeds on the fused / unsplit kernels. */
 int mlxq_qmatmul_workspace_size(int64_t M, int64_t N, int64_t K,
                                 int group_size, int bits, size_t* bytes);
 
@@ -130,7 +137,9 @@ int mlxq_qmatmul_algo(const void* x, int64_t M, const uint32_t* wq,
 /* mlxq_qmatmul for callers that cannot allocate or pass a workspace (code
  * under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc).  No counterpart in the reference.  Same kernels and results as
- * mlxq_qmatmul with a workspace of mlxq_qmatmul_workspace_size bytes, but
+ * mlxq_qmatmul with a workspace, except that M > 32 always takes the fused
+ * prefill kernel (MLXQ_ALGO_QMM; the library GEMM path needs a workspace of
+ * the whole dequantized weight and a hipBLASLt handle, which allocates), and
  * the split-K partial sums live in a fixed library scratch array in device
  * memory (mlxq_qmatmul_noalloc_max_scratch() bytes, 64 MiB, held by every
  * device the library runs on until the process ends); nothing is allocated.

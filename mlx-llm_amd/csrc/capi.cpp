@@ -60,6 +60,8 @@ const Overrides* read_overrides() {
   o->row_w = num("MLXQ_QMV_ROW_W");
   o->qmm_cfg = num("MLXQ_QMM_CFG");
   o->qmm_split = num("MLXQ_QMM_SPLIT");
+  o->qmm_lib = flag("MLXQ_QMM_LIB");
+  o->qmm_fused = flag("MLXQ_QMM_FUSED");
   return o;
 }
 

@@ -31,6 +31,7 @@ struct Overrides {
   int qmv_sub;              // MLXQ_QMV_SUB
   int row_r, row_w;         // MLXQ_QMV_ROW_R, MLXQ_QMV_ROW_W
   int qmm_cfg, qmm_split;   // MLXQ_QMM_CFG, MLXQ_QMM_SPLIT
+  bool qmm_lib, qmm_fused;  // MLXQ_QMM_LIB, MLXQ_QMM_FUSED
 };
 const Overrides& overrides();
 

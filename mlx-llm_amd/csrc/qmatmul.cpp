@@ -30,6 +30,52 @@ QmvPlan qmv_plan_for(int64_t M, int64_t N, int64_t K, int group_size, int bits) 
   return plan_qmv(std::min<int64_t>(std::max<int64_t>(M, 1), kQmvMaxM), N, K, group_size, bits);
 }
 
+// The kernel route of a call with more than 32 activation rows
+// (MLXQ_ALGO_AUTO), from graph-timed A/B runs at the Llama-3-8B shapes
+// (warm clocks, TFLOP/s fused kernel / library GEMM / 32-row decode chunks):
+//  * up to 64 rows, and down-like matrices (K > N) up to 128: the batched
+//    decode kernels over 32-row chunks (M = 64: gate 51.6 / 52.4 us fused /
+//    library vs 2 x 17.9, down 195 / 63 vs 2 x 20, q/o 64 / 30 vs 2 x 9.3,
+//    k/v 63 / 27 vs 2 x 6.5; down M = 128: 195 / 88 vs 4 x 20);
+//  * the library GEMM on the dequantized weight (qmm_lib.hip): gate/up-like
+//    (K < N) from M = 512 (669 -> 741 TFLOP/s; M = 2048 942 -> 1267), the
+//    square and short matrices (K = N, or N * K < 2^25) from 64 rows on
+//    (q/o M = 2048 716 -> 977; k/v 262 -> 470), large down-like ones up to
+//    384 rows (153 -> 395 at M = 256) and again from 1024 (Q4 839 -> 877) /
+//    2048 (Q8; 974 -> 1114);
+//  * the fused LDS-dequant kernel (qmm.hip) otherwise (down M = 512: 644 vs
+//    574).
+enum class Route { Fused, Lib, Chunks };
+
+Route prefill_route(int64_t M, int64_t N, int64_t K, int bits) {
+  const Overrides& ov = overrides();
+  if (ov.qmm_fused) return Route::Fused;
+  if (ov.qmm_lib) return Route::Lib;
+  if (N <= 16384 && (M <= 2 * kQmvMaxM || (K > N && M <= 4 * kQmvMaxM))) return Route::Chunks;
+  if (K < N) return M >= 512 ? Route::Lib : Route::Fused;
+  if (K > N && N * K >= (int64_t(1) << 25)) return M <= 384 || M >= (bits == 4 ? 1024 : 2048) ? Route::Lib : Route::Fused;
+  return Route::Lib;
+}
+
+// Workspace of the library's own kernels: split-K partials of the decode
+// kernels (also for the 32-row chunks of a longer call) and of the fused
+// prefill kernel.
+size_t fused_workspace_bytes(int64_t M, int64_t N, int64_t K, int group_size, int bits) {
+  const int64_t mq = std::min<int64_t>(M, kQmvMaxM);
+  size_t bytes = qmv_plan_for(mq, N, K, group_size, bits).workspace_bytes();
+  if (mq >= 2 && qmv_tile_eligible(mq, N, K, group_size, bits))
+    bytes = qmv_tile_workspace_bytes(mq, N);  // split-K partials (the M = 1 decode kernel needs none)
+  if (M > kQmvMaxM) {
+    const size_t qmm = K % 64 == 0 ? qmm_workspace_bytes(M, N, K) : 0;
+    bytes = prefill_route(M, N, K, bits) == Route::Chunks ? std::max(bytes, qmm) : qmm;
+  }
+  return bytes;
+}
+
+int qmatmul_dispatch(const void* x, int64_t M, const uint32_t* wq, const void* scales, const void* biases,
+                     const void* bias_vec, int64_t N, int64_t K, int group_size, int bits, void* y, void* workspace,
+                     size_t workspace_bytes, int algo, bool allow_lib, void* stream);
+
 }  // namespace
 
 extern "C" int mlxq_qmatmul_workspace_size(int64_t M, int64_t N, int64_t K, int group_size, int bits,
@@ -38,10 +84,9 @@ extern "C" int mlxq_qmatmul_workspace_size(int64_t M, int64_t N, int64_t K, int 
   int rc = check_shape(M, N, K, group_size, bits);
   if (rc) return rc;
   if (!bytes) return fail(MLXQ_ERR_INVALID, "qmatmul: null output pointer");
-  *bytes = qmv_plan_for(M, N, K, group_size, bits).workspace_bytes();
-  if (M >= 2 && M <= kQmvMaxM && qmv_tile_eligible(M, N, K, group_size, bits))
-    *bytes = qmv_tile_workspace_bytes(M, N);  // split-K partials (the M = 1 decode kernel needs none)
-  if (M > kQmvMaxM && K % 64 == 0) *bytes = qmm_workspace_bytes(M, N, K);  // prefill split-K partials
+  *bytes = fused_workspace_bytes(M, N, K, group_size, bits);
+  if (M > kQmvMaxM && prefill_route(M, N, K, bits) == Route::Lib)
+    *bytes = std::max(*bytes, qmm_lib_workspace_bytes(N, K));
   return MLXQ_OK;
 }
 
@@ -50,14 +95,49 @@ extern "C" int mlxq_qmatmul_algo(const void* x, int64_t M, const uint32_t* wq, c
                                  int bits, void* y, void* workspace, size_t workspace_bytes, int algo,
                                  void* stream) {
   clear_error();
+  return qmatmul_dispatch(x, M, wq, scales, biases, bias_vec, N, K, group_size, bits, y, workspace, workspace_bytes,
+                          algo, true, stream);
+}
+
+namespace {
+
+int qmatmul_dispatch(const void* x, int64_t M, const uint32_t* wq, const void* scales, const void* biases,
+                     const void* bias_vec, int64_t N, int64_t K, int group_size, int bits, void* y, void* workspace,
+                     size_t workspace_bytes, int algo, bool allow_lib, void* stream) {
   int rc = check_shape(M, N, K, group_size, bits);
   if (rc) return rc;
-  if (algo < MLXQ_ALGO_AUTO || algo > MLXQ_ALGO_QMM)
+  if (algo < MLXQ_ALGO_AUTO || algo > MLXQ_ALGO_QMM_LIB)
     return fail(MLXQ_ERR_INVALID, "qmatmul: unknown algo " + std::to_string(algo));
   if (M == 0) return MLXQ_OK;
   if (!x || !wq || !scales || !biases || !y) return fail(MLXQ_ERR_INVALID, "qmatmul: null pointer");
   if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(wq)) & 15u)
     return fail(MLXQ_ERR_INVALID, "qmatmul: x and wq must be 16-byte aligned");
+  if (algo == MLXQ_ALGO_QMM_LIB)
+    return launch_qmm_lib(static_cast<const uint16_t*>(x), M, wq, static_cast<const uint16_t*>(scales),
+                          static_cast<const uint16_t*>(biases), static_cast<const uint16_t*>(bias_vec), N, K,
+                          group_size, bits, static_cast<uint16_t*>(y), workspace, workspace_bytes,
+                          as_stream(stream));
+  if (algo == MLXQ_ALGO_AUTO && M > kQmvMaxM) {
+    const Route r = prefill_route(M, N, K, bits);
+    if (r == Route::Lib && allow_lib && workspace && workspace_bytes >= qmm_lib_workspace_bytes(N, K)) {
+      rc = launch_qmm_lib(static_cast<const uint16_t*>(x), M, wq, static_cast<const uint16_t*>(scales),
+                          static_cast<const uint16_t*>(biases), static_cast<const uint16_t*>(bias_vec), N, K,
+                          group_size, bits, static_cast<uint16_t*>(y), workspace, workspace_bytes,
+                          as_stream(stream));
+      if (rc != MLXQ_ERR_UNSUPPORTED) return rc;  // else (no library algorithm): the fused kernel
+      clear_error();
+    }
+    if (r == Route::Chunks && (!fused_workspace_bytes(kQmvMaxM, N, K, group_size, bits) ||
+                               (workspace && workspace_bytes >= fused_workspace_bytes(kQmvMaxM, N, K, group_size, bits)))) {
+      for (int64_t m0 = 0; m0 < M; m0 += kQmvMaxM) {
+        rc = qmatmul_dispatch(static_cast<const uint16_t*>(x) + m0 * K, std::min<int64_t>(kQmvMaxM, M - m0), wq,
+                              scales, biases, bias_vec, N, K, group_size, bits, static_cast<uint16_t*>(y) + m0 * N,
+                              workspace, workspace_bytes, MLXQ_ALGO_QMV, false, stream);
+        if (rc) return rc;
+      }
+      return MLXQ_OK;
+    }
+  }
   if (algo == MLXQ_ALGO_AUTO) algo = M <= kQmvMaxM ? MLXQ_ALGO_QMV : MLXQ_ALGO_QMM;
   if (algo == MLXQ_ALGO_QMM && K % 64) algo = MLXQ_ALGO_QMV;  // qmm steps K by 64
 
@@ -135,6 +215,8 @@ extern "C" int mlxq_qmatmul_algo(const void* x, int64_t M, const uint32_t* wq, c
   }
   return MLXQ_OK;
 }
+
+}  // namespace
 
 extern "C" int mlxq_qmatmul(const void* x, int64_t M, const uint32_t* wq, const void* scales, const void* biases,
                             const void* bias_vec, int64_t N, int64_t K, int group_size, int bits, void* y,
@@ -244,8 +326,9 @@ extern "C" int mlxq_qmatmul_noalloc(const void* x, int64_t M, const uint32_t* wq
                                     int bits, void* y, void* stream) {
   clear_error();
   size_t need = 0;
-  int rc = mlxq_qmatmul_workspace_size(M, N, K, group_size, bits, &need);
+  int rc = check_shape(M, N, K, group_size, bits);
   if (rc) return rc;
+  need = fused_workspace_bytes(M, N, K, group_size, bits);
   if (need > kScratchBytes)
     return fail(MLXQ_ERR_WORKSPACE, "qmatmul_noalloc: this shape needs " + std::to_string(need) +
                                         " bytes of scratch; the library's fixed scratch holds " +
@@ -258,6 +341,6 @@ extern "C" int mlxq_qmatmul_noalloc(const void* x, int64_t M, const uint32_t* wq
   // the same kernels as mlxq_qmatmul with a workspace of exactly `need`
   // bytes; every partial they read back is written earlier in the same
   // call, so the scratch needs no clearing
-  return mlxq_qmatmul_algo(x, M, wq, scales, biases, bias_vec, N, K, group_size, bits, y, ws, need, MLXQ_ALGO_AUTO,
-                           stream);
+  return qmatmul_dispatch(x, M, wq, scales, biases, bias_vec, N, K, group_size, bits, y, ws, need, MLXQ_ALGO_AUTO,
+                          false, stream);
 }

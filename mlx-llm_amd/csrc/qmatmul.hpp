@@ -100,6 +100,11 @@ int launch_split_reduce(const float* part, const uint16_t* bias, uint16_t* y, in
 constexpr int kQmmMaxSplits = 8;
 int qmm_split_k(int64_t M, int64_t N, int64_t K);
 size_t qmm_workspace_bytes(int64_t M, int64_t N, int64_t K);
+// prefill as dequantize into the workspace + hipBLASLt bf16 GEMM (qmm_lib.hip)
+size_t qmm_lib_workspace_bytes(int64_t N, int64_t K);
+int launch_qmm_lib(const uint16_t* x, int64_t M, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
+                   const uint16_t* bias, int64_t N, int64_t K, int group_size, int bits, uint16_t* y,
+                   void* workspace, size_t workspace_bytes, hipStream_t st);
 int launch_qmm(const uint16_t* x, int64_t M, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
                const uint16_t* bias, int64_t N, int64_t K, int group_size, int bits, uint16_t* y, void* workspace,
                size_t workspace_bytes, hipStream_t st);

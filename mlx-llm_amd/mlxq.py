@@ -22,7 +22,7 @@ LIB_PATH = Path(__file__).resolve().with_name("libmlxq.so")
 
 OK, ERR_INVALID, ERR_SHAPE, ERR_UNSUPPORTED, ERR_SHORT_BUFFER, ERR_WORKSPACE, ERR_DEVICE = range(7)
 F32, F16, BF16 = 0, 1, 2
-ALGO_AUTO, ALGO_QMV, ALGO_QMM = 0, 1, 2
+ALGO_AUTO, ALGO_QMV, ALGO_QMM, ALGO_QMM_LIB = 0, 1, 2, 3
 
 # GGUF type tags (dequant.rs:85-108)
 GGUF_TAGS = {

@@ -83,14 +83,29 @@ def test_quantize_and_qmatmul_argument_errors():
     assert mlxq.workspace_size(1, 4096, 4096, 64, 4) == 0
     assert mlxq.workspace_size(32, 4096, 4096, 64, 4) == 16 * 32 * 4096 * 4
     assert mlxq.workspace_size(32, 4096, 4096, 32, 4) == 0
-    assert mlxq.workspace_size(2048, 4096, 4096, 64, 4) == 2 * 2048 * 4096 * 4    # 128 tiles -> 2 slices
-    assert mlxq.workspace_size(2048, 4096, 14336, 64, 4) == 2 * 2048 * 4096 * 4
-    assert mlxq.workspace_size(1024, 4096, 14336, 64, 8) == 4 * 1024 * 4096 * 4   # 64 tiles -> 4 slices
-    assert mlxq.workspace_size(2048, 14336, 4096, 64, 4) == 0                     # 448 tiles: unsplit
-    assert mlxq.workspace_size(2048, 1024, 4096, 64, 4) == 0                      # 32 tiles: slices too short
+    # prefill routes: the library GEMM needs the whole weight as bf16 plus
+    # 32 MiB for hipBLASLt; 33..64 rows run as 32-row decode calls
+    lib = lambda n, k: n * k * 2 + (32 << 20)  # noqa: E731
+    assert mlxq.workspace_size(2048, 4096, 4096, 64, 4) == max(lib(4096, 4096), 2 * 2048 * 4096 * 4)
+    assert mlxq.workspace_size(2048, 4096, 14336, 64, 4) == lib(4096, 14336)
+    assert mlxq.workspace_size(1024, 4096, 14336, 64, 8) == 4 * 1024 * 4096 * 4   # fused: 64 tiles -> 4 slices
+    assert mlxq.workspace_size(2048, 14336, 4096, 64, 4) == lib(14336, 4096)
+    assert mlxq.workspace_size(2048, 1024, 4096, 64, 4) == lib(1024, 4096)
+    assert mlxq.workspace_size(64, 4096, 4096, 64, 4) == 16 * 32 * 4096 * 4      # decode chunks of 32
     assert L.mlxq_qmatmul_algo(p, 1, p, p, p, None, 64, 128, 64, 4, p, None, 0, 7, None) == mlxq.ERR_INVALID
     # M = 0 is a no-op
     assert L.mlxq_qmatmul(p, 0, p, p, p, None, 64, 128, 64, 4, p, None, 0, None) == mlxq.OK
+
+
+def test_workspace_sizes_fused_prefill(monkeypatch):
+    """MLXQ_QMM_FUSED=1: prefill always on the fused kernel, whose split-K
+    partials fill about one round of the 256 CUs when its 256 x 256 tiles
+    fill under 7/8 of them."""
+    monkeypatch.setenv("MLXQ_QMM_FUSED", "1")
+    assert mlxq.workspace_size(2048, 4096, 4096, 64, 4) == 2 * 2048 * 4096 * 4    # 128 tiles -> 2 slices
+    assert mlxq.workspace_size(2048, 4096, 14336, 64, 4) == 2 * 2048 * 4096 * 4
+    assert mlxq.workspace_size(2048, 14336, 4096, 64, 4) == 0                     # 448 tiles: unsplit
+    assert mlxq.workspace_size(2048, 1024, 4096, 64, 4) == 0                      # 32 tiles: slices too short
 
 
 def test_workspace_sizes_cover_every_decode_shape():

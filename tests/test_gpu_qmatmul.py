@@ -110,6 +110,7 @@ def test_qmm_split_k(torch_gpu, monkeypatch, bits, gs, splits, n):
     summed in slice order by the reduce kernel): the 4-wide reduce (N % 4 ==
     0) and the scalar one, a bias vector, M not a multiple of the tile."""
     monkeypatch.setenv("MLXQ_QMM_SPLIT", str(splits))
+    monkeypatch.setenv("MLXQ_QMM_FUSED", "1")
     m, k = 300, 1024
     assert mlxq.workspace_size(m, n, k, gs, bits) == splits * m * n * 4
     wq, s, b = make_layer(90 + bits + gs + n, n, k, gs, bits)

@@ -42,7 +42,9 @@ def test_noalloc_matches_workspace_path(torch_gpu, bits, n, k, m1, m2):
     bias = dev(orc.f32_to_bf16(np.random.default_rng(n).normal(0, 1, n).astype(np.float32)), bf16=True)
     for m in (m1, m2):
         x = dev(bf16_acts(0x7100 + m, m, k), bf16=True)
-        want = mlxq.qmatmul(x, wq, s, b, 64, bits, bias=bias)
+        # M > 32: the fused prefill kernel, which the no-alloc entry point
+        # always takes (mlxq_qmatmul may take the library GEMM there)
+        want = mlxq.qmatmul(x, wq, s, b, 64, bits, bias=bias, algo=mlxq.ALGO_QMM if m > 32 else mlxq.ALGO_AUTO)
         got = noalloc(x, wq, s, b, n, k, bits, bias)
         torch.cuda.synchronize()
         assert torch.equal(got.view(torch.int16), want.view(torch.int16)), m
