@@ -62,6 +62,7 @@ const Overrides* read_overrides() {
   o->qmm_split = num("MLXQ_QMM_SPLIT");
   o->qmm_lib = flag("MLXQ_QMM_LIB");
   o->qmm_fused = flag("MLXQ_QMM_FUSED");
+  o->qmm_lib_algo = num("MLXQ_QMM_LIB_ALGO");
   return o;
 }
 

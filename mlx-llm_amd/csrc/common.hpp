@@ -32,6 +32,7 @@ struct Overrides {
   int row_r, row_w;         // MLXQ_QMV_ROW_R, MLXQ_QMV_ROW_W
   int qmm_cfg, qmm_split;   // MLXQ_QMM_CFG, MLXQ_QMM_SPLIT
   bool qmm_lib, qmm_fused;  // MLXQ_QMM_LIB, MLXQ_QMM_FUSED
+  int qmm_lib_algo;         // MLXQ_QMM_LIB_ALGO
 };
 const Overrides& overrides();
 

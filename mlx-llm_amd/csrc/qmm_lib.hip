@@ -91,7 +91,7 @@ struct LtPlan {
 
 std::mutex g_mu;
 hipblasLtHandle_t g_handle[kMaxDev] = {};
-std::map<std::tuple<int, int64_t, int64_t, int64_t, bool>, LtPlan> g_plans;
+std::map<std::tuple<int, int64_t, int64_t, int64_t, bool, int>, LtPlan> g_plans;
 
 int lt_fail(const char* what, hipblasStatus_t st) {
   return fail(MLXQ_ERR_UNSUPPORTED, std::string("qmatmul (library GEMM): ") + what + " failed (status " +
@@ -102,7 +102,8 @@ int lt_fail(const char* what, hipblasStatus_t st) {
 // descriptors and the heuristic query allocate nothing on the device).
 int get_plan(int dev, int64_t M, int64_t N, int64_t K, bool bias, const LtPlan** out) {
   std::lock_guard<std::mutex> lk(g_mu);
-  auto key = std::make_tuple(dev, M, N, K, bias);
+  const int pick = overrides().qmm_lib_algo;  // MLXQ_QMM_LIB_ALGO: the heuristic's i-th algorithm (tuning)
+  auto key = std::make_tuple(dev, M, N, K, bias, pick);
   auto it = g_plans.find(key);
   if (it != g_plans.end()) {
     *out = &it->second;
@@ -135,13 +136,13 @@ int get_plan(int dev, int64_t M, int64_t N, int64_t K, bool bias, const LtPlan**
   if (st != HIPBLAS_STATUS_SUCCESS) return lt_fail("MatmulPreferenceCreate", st);
   const uint64_t maxws = kLtWorkspace;
   hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &maxws, sizeof(maxws));
-  hipblasLtMatmulHeuristicResult_t res[8];
+  hipblasLtMatmulHeuristicResult_t res[16];
   int n = 0;
-  st = hipblasLtMatmulAlgoGetHeuristic(g_handle[dev], p.desc, p.a, p.b, p.c, p.c, pref, 8, res, &n);
+  st = hipblasLtMatmulAlgoGetHeuristic(g_handle[dev], p.desc, p.a, p.b, p.c, p.c, pref, 16, res, &n);
   hipblasLtMatmulPreferenceDestroy(pref);
   if (st != HIPBLAS_STATUS_SUCCESS) return lt_fail("MatmulAlgoGetHeuristic", st);
-  for (int i = 0; i < n; i++) {
-    if (res[i].state == HIPBLAS_STATUS_SUCCESS && res[i].workspaceSize <= kLtWorkspace) {
+  for (int i = 0, valid = 0; i < n; i++) {
+    if (res[i].state == HIPBLAS_STATUS_SUCCESS && res[i].workspaceSize <= kLtWorkspace && valid++ >= pick) {
       p.algo = res[i].algo;
       p.ws = res[i].workspaceSize;
       p.ok = true;
