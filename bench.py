@@ -95,8 +95,10 @@ def main(argv=None) -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--quick", action="store_true", help="skip prefill / gguf / cpu legs")
-    ap.add_argument("--profile-shape", metavar="BITS,M,PROJ",
-                    help="only launch one sweep shape 40 times (for rocprofv3 counter runs), no JSON")
+    ap.add_argument("--profile-shape", metavar="BITS,M,PROJ[,ALGO]",
+                    help="only launch one sweep shape 40 times (for rocprofv3 counter runs), no JSON; ALGO "
+                         "auto (default: the route mlxq_qmatmul takes), qmm (the fused prefill kernel) or lib "
+                         "(dequantize + library GEMM)")
     ap.add_argument("--profile-libgemm", metavar="M,PROJ",
                     help="only run the library bf16 GEMM (torch -> hipBLASLt) of one shape 40 times "
                          "(MFMA counter calibration), no JSON")
@@ -132,13 +134,14 @@ def main(argv=None) -> int:
         torch.cuda.synchronize()
         return 0
     if a.profile_shape:
-        bits, m, name = a.profile_shape.split(",")
+        bits, m, name, *alg = a.profile_shape.split(",")
         bits, m = int(bits), int(m)
+        algo = {"auto": mlxq.ALGO_AUTO, "qmm": mlxq.ALGO_QMM, "lib": mlxq.ALGO_QMM_LIB}[alg[0] if alg else "auto"]
         k, n = {p[0]: (p[1], p[2]) for p in PROJ}[name]
         layers = make_layers(torch, mlxq, bits, 8, 0x5EED0000 + 100 * bits)
         x = torch.randn((m, k), device="cuda").to(torch.bfloat16)
         y = torch.empty((m, n), device="cuda", dtype=torch.bfloat16)
-        fns = [mlxq.bind_qmatmul(x, *L[name], GS, bits, out=y) for L in layers]
+        fns = [mlxq.bind_qmatmul(x, *L[name], GS, bits, out=y, algo=algo) for L in layers]
         for _ in range(5):
             for f in fns:
                 f()
