@@ -32,29 +32,28 @@ QmvPlan qmv_plan_for(int64_t M, int64_t N, int64_t K, int group_size, int bits) 
 
 // The kernel route of a call with more than 32 activation rows
 // (MLXQ_ALGO_AUTO), from graph-timed A/B runs at the Llama-3-8B shapes
-// (warm clocks, TFLOP/s fused kernel / library GEMM / 32-row decode chunks):
-//  * up to 64 rows, and down-like matrices (K > N) up to 128: the batched
-//    decode kernels over 32-row chunks (M = 64: gate 51.6 / 52.4 us fused /
-//    library vs 2 x 17.9, down 195 / 63 vs 2 x 20, q/o 64 / 30 vs 2 x 9.3,
-//    k/v 63 / 27 vs 2 x 6.5; down M = 128: 195 / 88 vs 4 x 20);
+// (warm clocks; µs, Q4, fused kernel / library GEMM / 32-row decode chunks):
+//  * up to 64 rows: the batched-decode kernels over 32-row chunks (M = 64:
+//    gate 51.7 / 52.4 / 2 x 17.5, q/o 26.6 / 29.6 / 2 x 9.3, k/v 25.5 / 27.1
+//    / 2 x 6.5; down 37.8 / 62.8 / 2 x 19.6);
 //  * the library GEMM on the dequantized weight (qmm_lib.hip): gate/up-like
-//    (K < N) from M = 512 (669 -> 741 TFLOP/s; M = 2048 942 -> 1267), the
-//    square and short matrices (K = N, or N * K < 2^25) from 64 rows on
-//    (q/o M = 2048 716 -> 977; k/v 262 -> 470), large down-like ones up to
-//    384 rows (153 -> 395 at M = 256) and again from 1024 (Q4 839 -> 877) /
-//    2048 (Q8; 974 -> 1114);
-//  * the fused LDS-dequant kernel (qmm.hip) otherwise (down M = 512: 644 vs
-//    574).
+//    (K < N) from M = 512 (90.8 -> 81.1; M = 2048 253 -> 190, 942 -> 1267
+//    TFLOP/s), square (q/o) from 1024 (62.3 -> 49.7), down-like from 1024 (Q4:
+//    141.8 -> 137.2) / 2048 (Q8; Q4 M = 2048 253 -> 210) and short matrices
+//    with K > N (k/v) from 2048 (42.3 -> 36.6);
+//  * the fused LDS-dequant kernel (qmm.hip) otherwise (e.g. down M = 256:
+//    56.7 vs 75.2 library; q/o M = 256: 30.8 vs 34.7).
 enum class Route { Fused, Lib, Chunks };
 
 Route prefill_route(int64_t M, int64_t N, int64_t K, int bits) {
   const Overrides& ov = overrides();
   if (ov.qmm_fused) return Route::Fused;
   if (ov.qmm_lib) return Route::Lib;
-  if (N <= 16384 && (M <= 2 * kQmvMaxM || (K > N && M <= 4 * kQmvMaxM))) return Route::Chunks;
+  if (N <= 16384 && M <= 2 * kQmvMaxM) return Route::Chunks;
+  const bool large = N * K >= (int64_t(1) << 25);
   if (K < N) return M >= 512 ? Route::Lib : Route::Fused;
-  if (K > N && N * K >= (int64_t(1) << 25)) return M <= 384 || M >= (bits == 4 ? 1024 : 2048) ? Route::Lib : Route::Fused;
-  return Route::Lib;
+  if (K > N) return M >= (large && bits == 4 ? 1024 : 2048) ? Route::Lib : Route::Fused;
+  return M >= 1024 ? Route::Lib : Route::Fused;
 }
 
 // Workspace of the library's own kernels: split-K partials of the decode

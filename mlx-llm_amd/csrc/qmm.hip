@@ -439,7 +439,7 @@ int launch_cfg(const uint16_t* x, int M, const uint32_t* wq, const uint16_t* s, 
   // Grids too small for either: 128 x 128 tiles, two workgroups per CU.
   const bool even_steps = (K / splits / BK) % 2 == 0;
   int cfg = 6;
-  if (splits > 1 || tiles256 * 8 >= cus * 7) cfg = even_steps ? 14 : 9;
+  if (tiles256 * splits * 8 >= cus * 7) cfg = even_steps ? 14 : 9;
   if (BITS == 4 && splits == 1 && N % 224 == 0 && (N / 224) * ceil_div(M, 256) * 8 >= cus * 7)
     cfg = even_steps ? 15 : 10;
   if (overrides().qmm_cfg) cfg = overrides().qmm_cfg;
@@ -475,7 +475,17 @@ int qmm_split_k(int64_t M, int64_t N, int64_t K) {
     if (tiles * sp > cus) break;
     if (tiles * sp * 8 >= cus * 7 && K % (128 * sp) == 0 && K / sp >= 16 * 64) return sp;
   }
-  return 1;
+  // grids that no split of 256 x 256 tiles fills (short matrices or few
+  // rows): 128 x 128 tiles (two workgroups per CU), K split as far as the
+  // CUs and the 16-step minimum allow (launch_cfg takes the 128 x 128 form
+  // whenever the split 256-wide grid would still leave CUs idle).  Measured
+  // (Q4, µs): q/o M = 128 63.6 -> 28.8, M = 512 65.7 -> 40.5; k/v M = 512
+  // 64.3 -> 27.3; down M = 128 195 -> 39.9, M = 256 197 -> 56.7
+  const int64_t t128 = ceil_div(N, 128) * ceil_div(M, 128);
+  int best = 1;
+  for (int sp = 2; sp <= kQmmMaxSplits; sp++)
+    if (t128 * sp <= 2 * cus && K % (128 * sp) == 0 && K / sp >= 16 * 64) best = sp;
+  return best;
 }
 
 size_t qmm_workspace_bytes(int64_t M, int64_t N, int64_t K) {

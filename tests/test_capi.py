@@ -87,6 +87,7 @@ def test_quantize_and_qmatmul_argument_errors():
     # 32 MiB for hipBLASLt; 33..64 rows run as 32-row decode calls
     lib = lambda n, k: n * k * 2 + (32 << 20)  # noqa: E731
     assert mlxq.workspace_size(2048, 4096, 4096, 64, 4) == max(lib(4096, 4096), 2 * 2048 * 4096 * 4)
+    assert mlxq.workspace_size(512, 4096, 4096, 64, 4) == 4 * 512 * 4096 * 4        # fused, 128-wide tiles, 4 slices
     assert mlxq.workspace_size(2048, 4096, 14336, 64, 4) == lib(4096, 14336)
     assert mlxq.workspace_size(1024, 4096, 14336, 64, 8) == 4 * 1024 * 4096 * 4   # fused: 64 tiles -> 4 slices
     assert mlxq.workspace_size(2048, 14336, 4096, 64, 4) == lib(14336, 4096)
@@ -105,7 +106,7 @@ def test_workspace_sizes_fused_prefill(monkeypatch):
     assert mlxq.workspace_size(2048, 4096, 4096, 64, 4) == 2 * 2048 * 4096 * 4    # 128 tiles -> 2 slices
     assert mlxq.workspace_size(2048, 4096, 14336, 64, 4) == 2 * 2048 * 4096 * 4
     assert mlxq.workspace_size(2048, 14336, 4096, 64, 4) == 0                     # 448 tiles: unsplit
-    assert mlxq.workspace_size(2048, 1024, 4096, 64, 4) == 0                      # 32 tiles: slices too short
+    assert mlxq.workspace_size(2048, 1024, 4096, 64, 4) == 4 * 2048 * 1024 * 4    # 128-wide tiles, 4 slices
 
 
 def test_workspace_sizes_cover_every_decode_shape():

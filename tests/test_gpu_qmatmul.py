@@ -350,3 +350,18 @@ def test_qmv_row_several_rows(torch_gpu, monkeypatch, bits, m, gs):
         bias = orc.f32_to_bf16(np.linspace(-1, 1, n, dtype=np.float32))
         ref = orc.qmatmul_f64(x, wq, s, b, gs, bits) + orc.bf16_to_f32(bias).astype(np.float64)[None, :]
         assert rel_err(run(x, wq, s, b, gs, bits, bias=bias), ref) <= TIGHT, (n, k)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("name,m", [("q_o", 128), ("q_o", 512), ("k_v", 256), ("down", 128), ("down", 256)])
+def test_qmm_small_grids_split_on_narrow_tiles(torch_gpu, bits, name, m):
+    """The fused prefill kernel at grids that no split of 256 x 256 tiles
+    fills: 128 x 128 tiles with K split (partials in the workspace); sampled
+    output columns against the oracle."""
+    k, n = LLAMA[name]
+    assert mlxq.workspace_size(m, n, k, 64, bits) > 0 or name == "down"
+    wq, s, b = make_layer(0x600 + m + bits, n, k, 64, bits)
+    x = bf16_acts(0x601 + m, m, k)
+    y = run(x, wq, s, b, 64, bits, mlxq.ALGO_QMM)
+    cols = np.sort(np.random.default_rng(m).choice(n, 128, replace=False))
+    assert rel_err(y[:, cols], orc.qmatmul_f64(x, wq[cols], s[cols], b[cols], 64, bits)) <= TIGHT

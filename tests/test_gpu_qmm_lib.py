@@ -51,16 +51,17 @@ def test_lib_bias_and_outliers(torch_gpu, lib_all, bits):
 @pytest.mark.parametrize("bits", [4, 8])
 def test_lib_matches_fused_kernel(torch_gpu, lib_all, bits):
     """Same dequantized values as the fused kernel: the outputs agree to
-    bf16 output rounding of the two summation orders."""
+    bf16 output rounding of the two summation orders (one bf16 ulp of an
+    output apart at most: <= 4e-3 of the largest)."""
     n, k, m = 1024, 4096, 256
     wq, s, b = make_layer(320 + bits, n, k, 64, bits)
     x = bf16_acts(321, m, k)
     lib = run(x, wq, s, b, 64, bits, mlxq.ALGO_QMM_LIB)
     fused = run(x, wq, s, b, 64, bits, mlxq.ALGO_QMM)
-    assert np.max(np.abs(lib - fused)) / np.max(np.abs(fused)) <= 2e-3
+    assert np.max(np.abs(lib - fused)) / np.max(np.abs(fused)) <= TIGHT
 
 
-@pytest.mark.parametrize("name,m", [("gate_up", 512), ("q_o", 512), ("down", 2048)])
+@pytest.mark.parametrize("name,m", [("gate_up", 512), ("q_o", 1024), ("down", 2048), ("k_v", 2048)])
 def test_lib_default_llama(torch_gpu, monkeypatch, name, m):
     """The default dispatch at shapes where it takes the library GEMM;
     seeded sample of 64 output columns (weight rows) against the oracle."""
@@ -122,11 +123,10 @@ def test_lib_graph_replay_bit_exact(torch_gpu, lib_all):
 
 
 @pytest.mark.parametrize("bits", [4, 8])
-@pytest.mark.parametrize("m,n,k", [(33, 200, 1024), (64, 640, 4096), (100, 256, 8192), (128, 96, 2048)])
+@pytest.mark.parametrize("m,n,k", [(33, 200, 1024), (64, 640, 4096), (48, 256, 8192), (64, 96, 2048)])
 def test_prefill_short_calls_in_decode_chunks(torch_gpu, monkeypatch, bits, m, n, k):
-    """33..64 rows (and up to 128 when K > N) run as 32-row calls of the
-    batched-decode kernels under the default dispatch (with a bias: each
-    chunk adds it)."""
+    """33..64 rows run as 32-row calls of the batched-decode kernels under
+    the default dispatch (with a bias: each chunk adds it)."""
     for v in ("MLXQ_QMM_LIB", "MLXQ_QMM_FUSED"):
         monkeypatch.delenv(v, raising=False)
     wq, s, b = make_layer(360 + bits, n, k, 64, bits)
