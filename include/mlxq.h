@@ -100,14 +100,16 @@ int mlxq_dequantize(const uint32_t* wq, const void* scales, const void* biases,
 /* ------------------------------------------------------------------ */
 
 /* Bytes of device workspace mlxq_qmatmul may use for this shape: nonzero
- * for batched decode (2 <= M <= 32, group size 64) and for prefill shapes
- * with too few 256 x 256 output tiles to fill the GPU (e.g. M = 2048,
- * 14336 -> 4096: 2 x M x N x 4 bytes), where the kernel splits K across
- * workgroups and a second kernel adds the f32 partial sums in slice order.
- * At prefill shapes where it is measured faster (M >= 512, or M >= 2048
- * when K > N) the size is instead that of the whole weight dequantized to
- * bf16 (N x K x 2 bytes) plus 32 MiB for hipBLASLt: the call dequantizes
- * into the workspace and runs hipBLASLt's bf16 GEMM (MLXQ_ALGO_QMM_LIB).
+ * for batched decode (2 <= M <= 32, group size 64; also calls of 33..64
+ * rows, run as 32-row decode calls) and for prefill shapes with too few
+ * output tiles to fill the GPU (e.g. M = 512, 4096 -> 4096: 4 x M x N x 4
+ * bytes), where the kernel splits K across workgroups and a second kernel
+ * adds the f32 partial sums in slice order.  At prefill shapes where it is
+ * measured faster (gate/up-like from M = 512, square from 1024, down-like
+ * from 1024 / 2048 (Q4 / Q8), k/v-like from 2048) the size is instead that
+ * of the whole weight dequantized to bf16 (N x K x 2 bytes) plus 32 MiB for
+ * hipBLASLt: the call dequantizes into the workspace and runs hipBLASLt's
+ * bf16 GEMM (MLXQ_ALGO_QMM_LIB).
  * The workspace must be 256-byte aligned; its contents need no
  * initialisation and are scratch after a call.  With no or too small a
  * workspace the call still succeeds on the fused / unsplit kernels. */
