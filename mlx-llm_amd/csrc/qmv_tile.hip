@@ -428,31 +428,52 @@ __global__ __launch_bounds__(64 * WV) void qmv_stream_kernel(const TileParams p)
   __shared__ __align__(16) uint16_t sx[2][Tg::MR * Tg::SXS];
   __shared__ f32x4 red[KH > 1 ? (KH - 1) * Tg::RG * MT * 64 : 1];
   const int steps = p.steps, s0 = blockIdx.y * steps, tile = blockIdx.x;
+  // Every load below is issued on every path (a slice past the run re-reads
+  // the last one): the memory counter then holds the same loads wherever
+  // control flow joins, so each wait names exactly the loads it needs.  A
+  // load issued only on some paths made the compiler wait at the join as
+  // if it were absent, i.e. for the just-issued prefetch of slice s + 2 too.
+  const int last = s0 + steps - 1;
   TileX<BITS, GS, MT, WV, NCH, KH> X0, X1;
   TileW<BITS, GS, MT, WV, NCH, KH> W0, W1;
   tile_load_x(p, s0, X0);
   tile_load_w(p, tile, s0, W0);
-  if (steps > 1) {
-    tile_load_x(p, s0 + 1, X1);
-    tile_load_w(p, tile, s0 + 1, W1);
-  }
+  tile_load_x(p, min(s0 + 1, last), X1);
+  tile_load_w(p, tile, min(s0 + 1, last), W1);
   __builtin_amdgcn_sched_barrier(0);
   tile_stage(X0, xs[0], sx[0]);
   f32x4 acc[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; mt++) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
   // slice s: codes W0 / buffer 0 (s even), W1 / buffer 1 (s odd); each
-  // register set and buffer is refilled as soon as its slice is used
-  for (int s = 0; s < steps; s += 2) {
-    if (s + 2 < steps) tile_load_x(p, s0 + s + 2, X0);
+  // register set and buffer is refilled as soon as its slice is used.
+  // Steady state while slices s + 2 and s + 3 exist; then a tail of 1..3.
+  int s = 0;
+  for (; s + 3 < steps; s += 2) {
+    tile_load_x(p, s0 + s + 2, X0);
     tile_accum(acc, W0, xs[0], sx[0]);
-    if (s + 2 < steps) tile_load_w(p, tile, s0 + s + 2, W0);
-    if (s + 1 >= steps) break;
+    tile_load_w(p, tile, s0 + s + 2, W0);
     tile_stage(X1, xs[1], sx[1], s == 0);
-    if (s + 3 < steps) tile_load_x(p, s0 + s + 3, X1);
+    tile_load_x(p, s0 + s + 3, X1);
     tile_accum(acc, W1, xs[1], sx[1]);
-    if (s + 3 < steps) tile_load_w(p, tile, s0 + s + 3, W1);
-    if (s + 2 < steps) tile_stage(X0, xs[0], sx[0], false);
+    tile_load_w(p, tile, s0 + s + 3, W1);
+    tile_stage(X0, xs[0], sx[0], false);
+  }
+  const int rest = steps - s;  // 1 only when steps == 1
+  if (rest == 3) {
+    tile_load_x(p, s0 + s + 2, X0);
+    tile_accum(acc, W0, xs[0], sx[0]);
+    tile_load_w(p, tile, s0 + s + 2, W0);
+    tile_stage(X1, xs[1], sx[1], s == 0);
+    tile_accum(acc, W1, xs[1], sx[1]);
+    tile_stage(X0, xs[0], sx[0], false);
+    tile_accum(acc, W0, xs[0], sx[0]);
+  } else if (rest == 2) {
+    tile_accum(acc, W0, xs[0], sx[0]);
+    tile_stage(X1, xs[1], sx[1], s == 0);
+    tile_accum(acc, W1, xs[1], sx[1]);
+  } else {
+    tile_accum(acc, W0, xs[0], sx[0]);
   }
   tile_finish<BITS, GS, MT, WV, NCH, KH>(p, tile, blockIdx.y, acc, red);
 }
