@@ -606,7 +606,8 @@ int dispatch_stream_mt(const SCfg& c, const TileParams& a, int tiles, int mb, hi
 // matrices (q/o, k/v) stay on the single-slice form (parity or slower).
 bool stream_preferred(int64_t M, int64_t N, int64_t K, int bits, SCfg& c, int& splits) {
   const bool large = N * K >= (int64_t(1) << 25);
-  if (!large || M < 8) return false;
+  // gate/up-like from M = 3 (M = 4: Q4 13.20 -> 12.40 us, Q8 19.10 -> 18.47)
+  if (!large || M < (K < N ? 3 : 8)) return false;
   if (K < N) {
     c = M > 16 && bits == 8 ? SCfg{8, 2, 2} : SCfg{8, 4, 2};
     splits = 1;
@@ -711,12 +712,12 @@ bool qmv_tile_preferred(int64_t M, int64_t N, int64_t K, int bits) {
   // Measured against the block kernel (qmv.hip) and the vector-ALU kernel
   // (qmv_dot) at the Llama-3-8B projection shapes: the tile kernel wins on
   // the large projections from M = 8 (Q4) / 16 (Q8),
-  // on Q4 gate/up already from M = 3, on short matrices (N <= 2048) from
+  // on gate/up already from M = 3 (Q4) / 4 (Q8), on short matrices (N <= 2048) from
   // M = 16, and on the other small projections from M = 24 (Q4) / 32 (Q8).
   const bool large = N * K >= (int64_t(1) << 25);
-  if (M <= 4) return large && K < N && bits == 4 && M >= 3;
+  if (M <= 4) return large && K < N && M >= (bits == 4 ? 3 : 4);
   if (short_fullk(M, N, K, bits, nullptr)) return true;
-  if (large) return M >= (bits == 4 ? 8 : 16);
+  if (large) return K < N || M >= (bits == 4 ? 8 : 16);  // gate/up-like: the streaming form (Q8 M = 8 20.4 -> 19.0)
   if (N <= 2048) return M >= 16;  // k/v: M = 16 Q4 8.28 -> 7.93 us, Q8 9.27 -> 8.06; Q8 M = 24 11.07 -> 8.93
   return M >= (bits == 4 ? 24 : 32);
 }
