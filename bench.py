@@ -95,6 +95,8 @@ def main(argv=None) -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--quick", action="store_true", help="skip prefill / gguf / cpu legs")
+    ap.add_argument("--leg", choices=["prefill", "gguf", "decode_stack"],
+                    help="only run one secondary leg and print its JSON (tuning), no sweep")
     ap.add_argument("--profile-shape", metavar="BITS,M,PROJ[,ALGO]",
                     help="only launch one sweep shape 40 times (for rocprofv3 counter runs), no JSON; ALGO "
                          "auto (default: the route mlxq_qmatmul takes), qmm (the fused prefill kernel) or lib "
@@ -146,6 +148,12 @@ def main(argv=None) -> int:
             for f in fns:
                 f()
         torch.cuda.synchronize()
+        return 0
+
+    if a.leg:
+        legs = {"prefill": lambda: bench_prefill(torch, mlxq), "gguf": lambda: bench_gguf(torch, mlxq),
+                "decode_stack": lambda: bench_stack(torch)}
+        print(json.dumps({a.leg: legs[a.leg]()}), flush=True)
         return 0
 
     torch.manual_seed(0)

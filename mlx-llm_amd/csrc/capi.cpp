@@ -48,6 +48,7 @@ const Overrides* read_overrides() {
   o->qmv_stream = flag("MLXQ_QMV_STREAM");
   o->qmv_narrow = flag("MLXQ_QMV_NARROW");
   o->tile_mb = flag("MLXQ_QMV_TILE_MB");
+  o->qmv_no_tile_fused = flag("MLXQ_QMV_NO_TILE_FUSED");
   if (const char* e = getenv("MLXQ_QMV_TILE")) sscanf(e, "%d,%d,%d", &o->tile_wv, &o->tile_nch, &o->tile_kh);
   if (const char* e = getenv("MLXQ_QMV_TILE_STREAM")) {
     o->stream_set = true;

@@ -269,6 +269,10 @@ extern "C" int mlxq_qmatmul_fused(const void* x, int64_t M, int64_t K, const voi
   f.swiglu = swiglu != 0;
   f.group_size = group_size;
   f.bits = bits;
+  // 5..32 rows: the whole-K tile form where it covers the shape (every form
+  // but SwiGLU); MLXQ_QMV_LEGACY=1 or MLXQ_QMV_NO_TILE_FUSED=1 skips it
+  if (M > kQmvDotMaxM && qmv_tile_fused_eligible(f) && !overrides().qmv_legacy && !overrides().qmv_no_tile_fused)
+    return launch_qmv_tile_fused(f, as_stream(stream));
   if (M > kQmvDotMaxM) {  // matrix-core form: plain, residual and multi-projection only
     if (f.norm_w || f.swiglu || f.rep > 1 || M > kQmvMaxM)
       return fail(MLXQ_ERR_UNSUPPORTED, "qmatmul_fused: for M > " + std::to_string(kQmvDotMaxM) +

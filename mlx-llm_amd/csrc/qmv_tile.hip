@@ -65,7 +65,41 @@ struct TileParams {
   int M, N, K;
   int splits;
   int steps;  // K slices per workgroup (streaming form)
+  // fused forms (whole-K form only, no K split): residual epilogue
+  // y = bf16(res + bf16(acc + bias)); GQA head repeat by remapping the
+  // activation loads; up to three weight matrices of the same activations,
+  // each its own run of tiles (segment) of blockIdx.x
+  const uint16_t* res;     // [M, N] or null
+  int x_stride;            // activation row stride (elements)
+  int rep_hd8, rep;        // head repeat: piece k8 reads (k8 / (rep_hd8 rep)) rep_hd8 + k8 % rep_hd8
+  float rcp_hd8, rcp_grp;
 };
+
+// One weight matrix of a fused launch; its tiles end at tile_end (exclusive).
+struct TileSeg {
+  const uint32_t* wq;
+  const uint16_t* s;
+  const uint16_t* b;
+  const uint16_t* bias;
+  const uint16_t* res;
+  uint16_t* y;
+  int N;
+  int tile_end;
+};
+struct TileFused {
+  TileParams p;  // x, M, K and the fused-form fields; the matrix fields come from seg
+  int nseg;
+  TileSeg seg[3];
+};
+
+// n / d for 0 <= n < 2^24, d >= 1, given rcp = 1/d: the f32 quotient is
+// within one of the true one; one correction each way makes it exact.
+__device__ __forceinline__ int div_rcp(int n, int d, float rcp) {
+  int q = static_cast<int>(static_cast<float>(n) * rcp);
+  q -= q * d > n;
+  q += (q + 1) * d <= n;
+  return q;
+}
 
 // First activation row of this workgroup's M block (blockIdx.z): a call with
 // more activation rows than one workgroup stages runs the blocks side by
@@ -149,7 +183,7 @@ struct TileW {
 // The activation loads of the workgroup's slice: piece i of this thread is
 // 16-byte slot tid + T i of the slice's rows of C slots; its row and column
 // follow from tid at compile-time steps.
-template <int BITS, int GS, int MT, int WV, int NCH, int KH>
+template <int BITS, int GS, int MT, int WV, int NCH, int KH, bool FUSED = false>
 __device__ __forceinline__ void tile_load_x(const TileParams& p, int split, TileX<BITS, GS, MT, WV, NCH, KH>& X) {
   using Tg = TileGeom<BITS, GS, MT, WV, NCH, KH>;
   const int tid = threadIdx.x;
@@ -159,7 +193,17 @@ __device__ __forceinline__ void tile_load_x(const TileParams& p, int split, Tile
   for (int i = 0; i < Tg::XP; i++) {  // rows past M read row M-1: they only feed output rows >= M
     const int row = Tg::T >= C ? tid / C + i * (Tg::T / C) : i / (C / Tg::T);
     const int col = Tg::T >= C ? tid % C : tid + Tg::T * (i % (C / Tg::T));
-    X.xg[i] = *reinterpret_cast<const u32x4*>(xs0 + min(m_block0<MT>() + row, p.M - 1) * p.K + col * 8);
+    int src = col;
+    if constexpr (FUSED) {
+      if (p.rep > 1) {  // query head hq reads KV head hq / rep (whole-K form: col is the piece of the row)
+        const int grp = p.rep_hd8 * p.rep;
+        const int hq = div_rcp(col, grp, p.rcp_grp);
+        const int r = col - hq * grp;
+        src = hq * p.rep_hd8 + (r - div_rcp(r, p.rep_hd8, p.rcp_hd8) * p.rep_hd8);
+      }
+    }
+    X.xg[i] = *reinterpret_cast<const u32x4*>(xs0 + min(m_block0<MT>() + row, p.M - 1) * (FUSED ? p.x_stride : p.K) +
+                                              src * 8);
   }
 }
 
@@ -379,7 +423,11 @@ __device__ __forceinline__ void tile_finish(const TileParams& p, int tile, int s
 #pragma unroll
       for (int v = 0; v < 4; v++) {
         const int m = mb + 16 * mt + 4 * gq + v;
-        if (m < M) p.y[static_cast<int64_t>(m) * N + nn] = static_cast<uint16_t>(f32_to_bf16_bits(acc[mt][v] + bb));
+        if (m >= M) continue;
+        const int64_t o = static_cast<int64_t>(m) * N + nn;
+        uint32_t r = f32_to_bf16_bits(acc[mt][v] + bb);
+        if (p.res) r = f32_to_bf16_bits(bf16_bits_to_f32(p.res[o]) + bf16_bits_to_f32(r));  // residual: bf16(r + bf16(v))
+        p.y[o] = static_cast<uint16_t>(r);
       }
     return;
   }
@@ -412,6 +460,40 @@ __global__ __launch_bounds__(64 * WV) void qmv_tile_kernel(const TileParams p) {
   for (int mt = 0; mt < MT; mt++) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
   tile_accum(acc, W, xs, sx);
   tile_finish<BITS, GS, MT, WV, NCH, KH>(p, blockIdx.x, blockIdx.y, acc, red);
+}
+
+// Fused forms on the whole-K single-slice kernel: blockIdx.x picks the
+// segment (weight matrix) and its tile, blockIdx.z the M block; no K split.
+template <int BITS, int GS, int MT, int WV, int NCH, int KH>
+__global__ __launch_bounds__(64 * WV) void qmv_tile_fused_kernel(const TileFused f) {
+  using Tg = TileGeom<BITS, GS, MT, WV, NCH, KH>;
+  __shared__ u32x4 xs[Tg::MR * Tg::ROW16];
+  __shared__ __align__(16) uint16_t sx[Tg::MR * Tg::SXS];
+  __shared__ f32x4 red[KH > 1 ? (KH - 1) * Tg::RG * MT * 64 : 1];
+  int sg = 0;
+  const int t = blockIdx.x;
+  while (sg + 1 < f.nseg && t >= f.seg[sg].tile_end) sg++;
+  const TileSeg& S = f.seg[sg];
+  TileParams p = f.p;
+  p.wq = S.wq;
+  p.s = S.s;
+  p.b = S.b;
+  p.bias = S.bias;
+  p.res = S.res;
+  p.y = S.y;
+  p.N = S.N;
+  const int tile = t - (sg ? f.seg[sg - 1].tile_end : 0);
+  TileX<BITS, GS, MT, WV, NCH, KH> X;
+  TileW<BITS, GS, MT, WV, NCH, KH> W;
+  tile_load_x<BITS, GS, MT, WV, NCH, KH, true>(p, 0, X);
+  tile_load_w(p, tile, 0, W);
+  __builtin_amdgcn_sched_barrier(0);  // every load is issued before the first wait
+  tile_stage(X, xs, sx);
+  f32x4 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; mt++) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  tile_accum(acc, W, xs, sx);
+  tile_finish<BITS, GS, MT, WV, NCH, KH>(p, tile, 0, acc, red);
 }
 
 // Streaming form: a workgroup owns its 16 RG weight rows over `steps`
@@ -828,6 +910,71 @@ int launch_qmv_tile(const uint16_t* x, int64_t M, const uint32_t* wq, const uint
   if (int rc = dispatch(bits, *pick, a, static_cast<int>(tiles), mb, st, nullptr)) return rc;
   if (a.splits == 1) return MLXQ_OK;
   return launch_split_reduce(a.part, bias, y, M, N, a.splits, st);
+}
+
+namespace tile {
+
+template <int BITS>
+int run_fused(const Cfg& c, const TileFused& f, int tiles, int mb, hipStream_t st) {
+  if (c.nch == 4) {
+    hipLaunchKernelGGL((qmv_tile_fused_kernel<BITS, 64, 1, 8, 4, 8>), dim3(tiles, 1, mb), dim3(512), 0, st, f);
+  } else {
+    if constexpr (BITS == 8)
+      hipLaunchKernelGGL((qmv_tile_fused_kernel<BITS, 64, 1, 8, 8, 8>), dim3(tiles, 1, mb), dim3(512), 0, st, f);
+  }
+  return check_launch("qmv_tile_fused");
+}
+
+}  // namespace tile
+
+// The whole-K form carries the fused decode forms for 5..32 activation rows:
+// group size 64, K one slice of 8 waves x 4 chunks (Q4 K = 4096, Q8 K = 2048
+// or 4096), up to three projections, a head repeat, residuals;
+// no SwiGLU (gate/up go through plain calls there).
+bool qmv_tile_fused_eligible(const QmvFused& f) {
+  if (f.M < 5 || f.M > kQmvMaxM || f.group_size != 64 || f.swiglu || f.nproj < 1 || f.nproj > 3) return false;
+  const int64_t ch = chunks_of(f.K, f.bits);
+  if (ch % 8) return false;
+  const Cfg c{1, 8, static_cast<int>(ch / 8), 8};
+  if (!cfg_known(c, f.bits)) return false;
+  // No RMSNorm: every workgroup would normalise the same activations again
+  // (measured with the norm while staging: qkv at M = 16 26 us against 4.5 +
+  // 13.5 for the norm kernel and the fused projections; a 128256-row
+  // lm_head 379 us)
+  if (f.norm_w) return false;
+  int64_t tiles = 0;
+  for (int i = 0; i < f.nproj; i++) tiles += ceil_div(f.proj[i].N, 16);
+  if (tiles * ceil_div(f.M, 16) > 2 * cu_count()) return false;  // one workgroup per CU: at most two rounds
+  for (int i = 0; i < f.nproj; i++)
+    if (f.proj[i].N < 1 || f.proj[i].N > (int64_t(1) << 24)) return false;
+  return f.x_stride * f.M < (int64_t(1) << 31) && f.K * f.M < (int64_t(1) << 31);
+}
+
+int launch_qmv_tile_fused(const QmvFused& f, hipStream_t st) {
+  if (!qmv_tile_fused_eligible(f)) return fail(MLXQ_ERR_UNSUPPORTED, "qmv_tile_fused: shape not supported");
+  TileFused a{};
+  a.p.x = f.x;
+  a.p.M = static_cast<int>(f.M);
+  a.p.K = static_cast<int>(f.K);
+  a.p.splits = 1;
+  a.p.steps = 1;
+  a.p.x_stride = static_cast<int>(f.x_stride);
+  a.p.rep = f.rep > 1 ? f.rep : 1;
+  a.p.rep_hd8 = f.rep > 1 ? f.rep_hd / 8 : 1;
+  if (f.rep > 1 && f.rep_hd % 8) return fail(MLXQ_ERR_UNSUPPORTED, "qmv_tile_fused: head size not a multiple of 8");
+  a.p.rcp_hd8 = 1.0f / static_cast<float>(a.p.rep_hd8);
+  a.p.rcp_grp = 1.0f / static_cast<float>(a.p.rep_hd8 * a.p.rep);
+  a.nseg = f.nproj;
+  int tiles = 0;
+  for (int i = 0; i < f.nproj; i++) {
+    const QmvProj& P = f.proj[i];
+    tiles += static_cast<int>(ceil_div(P.N, 16));
+    a.seg[i] = TileSeg{P.wq, P.s, P.b, P.bias, P.res, P.y, static_cast<int>(P.N), tiles};
+  }
+  const int64_t ch = chunks_of(f.K, f.bits);
+  const Cfg c{1, 8, static_cast<int>(ch / 8), 8};
+  const int mb = static_cast<int>(ceil_div(f.M, 16));
+  return f.bits == 4 ? run_fused<4>(c, a, tiles, mb, st) : run_fused<8>(c, a, tiles, mb, st);
 }
 
 }  // namespace mlxq

@@ -190,3 +190,76 @@ def test_batch1_forms_both_kernels(torch_gpu, monkeypatch, path, bits):
     dd["y"], dd["residual"] = out_like(1, 1000), dev(r2, True)
     mlxq.qmatmul_fused(dev(a, True), [dd], gs, bits)
     check(dd["y"], orc.add(r2, orc.qlinear_bf16(a, hd_, gs, bits)))
+
+
+@pytest.mark.parametrize("bits,k", [(4, 4096), (8, 4096), (8, 2048)])
+@pytest.mark.parametrize("m", [5, 16, 17, 32])
+def test_tile_norm_qkv_batched(torch_gpu, bits, k, m):
+    """5..32 rows on the whole-K tile form: three projections of the same
+    activations (ragged N), a bias on one, after the norm kernel (the fused
+    norm form is not taken above 4 rows: every workgroup would normalise the
+    same rows again)."""
+    x = bf16_acts(50 + m, m, k)
+    w = orc.f32_to_bf16(orc.normal(51, k, 1.0, 0.1))
+    shapes = [1000, 256, 200]
+    host_w, projs = [], []
+    bias = orc.f32_to_bf16(orc.normal(52, 256, 0.0, 1.0))
+    for i, n in enumerate(shapes):
+        hw, dw = qlayer(53 + i + bits, n, k, 64, bits)
+        host_w.append(hw)
+        dw["y"] = out_like(m, n)
+        if i == 1:
+            dw["bias"] = dev(bias, True)
+        projs.append(dw)
+    with pytest.raises(mlxq.Unsupported):
+        mlxq.qmatmul_fused(dev(x, True), projs, 64, bits, norm_weight=dev(w, True), eps=1e-5)
+    mlxq.qmatmul_fused(mlxq.rms_norm(dev(x, True), dev(w, True), 1e-5), projs, 64, bits)
+    xn = orc.rms_norm(x, w, 1e-5)
+    for i, (hw, p) in enumerate(zip(host_w, projs)):
+        want = orc.qlinear_bf16(xn, hw, 64, bits)
+        if i == 1:
+            want = orc.f32_to_bf16(orc.bf16_to_f32(want) + orc.bf16_to_f32(bias)[None, :])
+        check(p["y"], want)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("m", [5, 16, 32])
+def test_tile_repeat_o_residual_batched(torch_gpu, bits, m):
+    """5..32 rows on the whole-K tile form: GQA head repeat by remapped
+    activation loads, o projection, residual epilogue."""
+    kvh, hd, groups = 8, 128, 4
+    k = kvh * hd * groups
+    v = bf16_acts(60 + m, m, kvh * hd)
+    r = bf16_acts(61 + m, m, 4096)
+    hw, dw = qlayer(62 + bits, 4096, k, 64, bits)
+    dw["y"] = out_like(m, 4096)
+    dw["residual"] = dev(r, True)
+    mlxq.qmatmul_fused(dev(v, True), [dw], 64, bits, repeat=(kvh, hd, groups))
+    want = orc.add(r, orc.qlinear_bf16(orc.repeat_kv(v, kvh, hd, groups), hw, 64, bits))
+    check(dw["y"], want)
+
+
+def test_tile_fused_matches_legacy_form(torch_gpu, monkeypatch):
+    """The tile form and the streaming matrix-core form (MLXQ_QMV_LEGACY=1)
+    agree on a residual multi-projection call (both round at the same points)."""
+    import torch
+
+    m, k = 16, 4096
+    x = bf16_acts(70, m, k)
+    r = bf16_acts(71, m, 1024)
+    outs = []
+    for legacy in (False, True):
+        if legacy:
+            monkeypatch.setenv("MLXQ_QMV_LEGACY", "1")
+        projs = []
+        for i, n in enumerate([1024, 512]):
+            _, dw = qlayer(72 + i, n, k, 64, 4)
+            dw["y"] = out_like(m, n)
+            if i == 0:
+                dw["residual"] = dev(r, True)
+            projs.append(dw)
+        mlxq.qmatmul_fused(dev(x, True), projs, 64, 4)
+        torch.cuda.synchronize()
+        outs.append([orc.bf16_to_f32(host(p["y"])) for p in projs])
+    for a, b in zip(*outs):
+        assert np.max(np.abs(a - b)) / np.max(np.abs(b)) <= 8e-3
