@@ -690,8 +690,12 @@ bool stream_preferred(int64_t M, int64_t N, int64_t K, int bits, SCfg& c, int& s
   const bool large = N * K >= (int64_t(1) << 25);
   // gate/up-like from M = 3 (M = 4: Q4 13.20 -> 12.40 us, Q8 19.10 -> 18.47)
   if (!large || M < (K < N ? 3 : 8)) return false;
+  // (re-measured with every load issued on every path: Q4 M = 32 gate 17.33
+  // -> 16.58 on {8, 2, 2}, Q8 M = 16 19.34 -> 18.41 on {4, 4, 1}, Q4 M = 16
+  // down 15.94 -> 15.56 on {4, 4, 1} with 4 splits)
   if (K < N) {
-    c = M > 16 && bits == 8 ? SCfg{8, 2, 2} : SCfg{8, 4, 2};
+    if (bits == 4) c = M > 16 || M <= 4 ? SCfg{8, 2, 2} : SCfg{8, 4, 2};
+    else c = M > 16 ? SCfg{8, 2, 2} : M > 4 ? SCfg{4, 4, 1} : SCfg{8, 4, 2};
     splits = 1;
     return true;
   }
@@ -700,7 +704,7 @@ bool stream_preferred(int64_t M, int64_t N, int64_t K, int bits, SCfg& c, int& s
     splits = 4;
     return true;
   }
-  if (bits == 8 && M == 16) {
+  if (M == 16) {
     c = SCfg{4, 4, 1};
     splits = 4;
     return true;
