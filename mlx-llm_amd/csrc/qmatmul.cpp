@@ -229,8 +229,9 @@ extern "C" int mlxq_qmatmul_fused(const void* x, int64_t M, int64_t K, const voi
                                   int swiglu, int group_size, int bits, void* stream) {
   clear_error();
   if (!proj || nproj < 1 || nproj > 3) return fail(MLXQ_ERR_INVALID, "qmatmul_fused: 1 to 3 projections");
-  if (swiglu && (nproj != 2 || !norm_weight))
-    return fail(MLXQ_ERR_UNSUPPORTED, "qmatmul_fused: SwiGLU needs gate/up and a norm weight");
+  if (swiglu && nproj != 2) return fail(MLXQ_ERR_UNSUPPORTED, "qmatmul_fused: SwiGLU needs gate and up");
+  if (swiglu && !norm_weight && M <= kQmvDotMaxM)
+    return fail(MLXQ_ERR_UNSUPPORTED, "qmatmul_fused: SwiGLU without a norm needs more than 4 rows");
   if (norm_weight && groups > 1) return fail(MLXQ_ERR_UNSUPPORTED, "qmatmul_fused: norm and head repeat together");
   for (int i = 0; i < nproj; i++) {
     int rc = check_shape(M, proj[i].N, K, group_size, bits);
@@ -273,6 +274,9 @@ extern "C" int mlxq_qmatmul_fused(const void* x, int64_t M, int64_t K, const voi
   // but SwiGLU); MLXQ_QMV_LEGACY=1 or MLXQ_QMV_NO_TILE_FUSED=1 skips it
   if (M > kQmvDotMaxM && qmv_tile_fused_eligible(f) && !overrides().qmv_legacy && !overrides().qmv_no_tile_fused)
     return launch_qmv_tile_fused(f, as_stream(stream));
+  // 5..32 rows, SwiGLU without a norm: gate/up pairs on the streaming form
+  if (M > kQmvDotMaxM && qmv_tile_swiglu_eligible(f) && !overrides().qmv_legacy && !overrides().qmv_no_tile_fused)
+    return launch_qmv_tile_swiglu(f, as_stream(stream));
   if (M > kQmvDotMaxM) {  // matrix-core form: plain, residual and multi-projection only
     if (f.norm_w || f.swiglu || f.rep > 1 || M > kQmvMaxM)
       return fail(MLXQ_ERR_UNSUPPORTED, "qmatmul_fused: for M > " + std::to_string(kQmvDotMaxM) +

@@ -85,6 +85,9 @@ bool qmv_tile_eligible(int64_t M, int64_t N, int64_t K, int group_size, int bits
 // whole-K tile form: 5 <= M <= 32, K one workgroup slice, no norm or SwiGLU
 bool qmv_tile_fused_eligible(const QmvFused& f);
 int launch_qmv_tile_fused(const QmvFused& f, hipStream_t st);
+// SwiGLU of gate/up (no norm) on the streaming tile form, 5 <= M <= 32
+bool qmv_tile_swiglu_eligible(const QmvFused& f);
+int launch_qmv_tile_swiglu(const QmvFused& f, hipStream_t st);
 size_t qmv_tile_workspace_bytes(int64_t M, int64_t N);
 bool qmv_tile_preferred(int64_t M, int64_t N, int64_t K, int bits);
 bool qmv_dot_preferred(int64_t M, int64_t N, int64_t K, int bits);  // M <= 4: vector-ALU kernel

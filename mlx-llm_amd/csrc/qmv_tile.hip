@@ -70,6 +70,14 @@ struct TileParams {
   // activation loads; up to three weight matrices of the same activations,
   // each its own run of tiles (segment) of blockIdx.x
   const uint16_t* res;     // [M, N] or null
+  // SwiGLU (streaming form): even row groups read the gate matrix (wq, s, b,
+  // bias), odd ones the up matrix (wq2, s2, b2, bias2) for the same outputs;
+  // y = bf16(bf16(g * bf16(sigmoid(g))) * u) of the bf16 projections
+  const uint32_t* wq2;
+  const uint16_t* s2;
+  const uint16_t* b2;
+  const uint16_t* bias2;
+  int swiglu;
   int x_stride;            // activation row stride (elements)
   int rep_hd8, rep;        // head repeat: piece k8 reads (k8 / (rep_hd8 rep)) rep_hd8 + k8 % rep_hd8
   float rcp_hd8, rcp_grp;
@@ -223,10 +231,14 @@ __device__ __forceinline__ void tile_load_w(const TileParams& p, int tile, int s
   const int G = K / GS;
   const int64_t row_u4 = static_cast<int64_t>(K) * BITS / 128;
   const int c0 = (split * KH + kh) * NCH;  // first chunk of the wave's part
-  const int n = min(tile * 16 * Tg::RG + rg * 16 + r16, p.N - 1);  // rows past N repeat row N-1 (results dropped)
-  load_param_words<Tg::NGW>(p.s + static_cast<int64_t>(n) * G + c0 * Bk::KC / GS, W.sw);
-  load_param_words<Tg::NGW>(p.b + static_cast<int64_t>(n) * G + c0 * Bk::KC / GS, W.bw);
-  const u32x4* wrow = reinterpret_cast<const u32x4*>(p.wq) + n * row_u4 + gq;
+  // rows past N repeat row N-1 (results dropped); SwiGLU: row group rg
+  // reads matrix rg & 1 at output block rg / 2
+  const bool up = p.swiglu && (rg & 1);
+  const int n = p.swiglu ? min(tile * 8 * Tg::RG + (rg >> 1) * 16 + r16, p.N - 1)
+                         : min(tile * 16 * Tg::RG + rg * 16 + r16, p.N - 1);
+  load_param_words<Tg::NGW>((up ? p.s2 : p.s) + static_cast<int64_t>(n) * G + c0 * Bk::KC / GS, W.sw);
+  load_param_words<Tg::NGW>((up ? p.b2 : p.b) + static_cast<int64_t>(n) * G + c0 * Bk::KC / GS, W.bw);
+  const u32x4* wrow = reinterpret_cast<const u32x4*>(up ? p.wq2 : p.wq) + n * row_u4 + gq;
 #pragma unroll
   for (int c = 0; c < NCH; c++) W.w[c] = wrow[static_cast<int64_t>(c0 + c) * 4];
 }
@@ -441,6 +453,60 @@ __device__ __forceinline__ void tile_finish(const TileParams& p, int tile, int s
     }
 }
 
+// SwiGLU end of a streaming item (one K split): K parts add up in LDS as in
+// tile_finish, then each up row group hands its sums to the gate row group
+// of the same outputs, which stores y = bf16(bf16(g * bf16(sigmoid(g))) * u)
+// with g, u the bf16 projection outputs (llama.rs:1040-1045 at MLX's
+// rounding points).  Every wave reaches both barriers.
+template <int BITS, int GS, int MT, int WV, int NCH, int KH>
+__device__ __forceinline__ void tile_finish_swiglu(const TileParams& p, int tile, f32x4 (&acc)[MT], f32x4* red,
+                                                   f32x4* hand) {
+  using Tg = TileGeom<BITS, GS, MT, WV, NCH, KH>;
+  static_assert(Tg::RG % 2 == 0, "SwiGLU: gate and up row groups in pairs");
+  const int M = p.M, N = p.N;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rg = wave % Tg::RG, kh = wave / Tg::RG;
+  const int r16 = lane & 15, gq = lane >> 4;
+  if constexpr (KH > 1) {
+    if (kh > 0)
+#pragma unroll
+      for (int mt = 0; mt < MT; mt++) red[(((kh - 1) * Tg::RG + rg) * MT + mt) * 64 + lane] = acc[mt];
+    __syncthreads();
+    if (kh == 0)
+#pragma unroll
+      for (int h = 1; h < KH; h++)
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+          const f32x4 o = red[(((h - 1) * Tg::RG + rg) * MT + mt) * 64 + lane];
+#pragma unroll
+          for (int v = 0; v < 4; v++) acc[mt][v] += o[v];
+        }
+  }
+  if (kh == 0 && (rg & 1))
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) hand[((rg >> 1) * MT + mt) * 64 + lane] = acc[mt];
+  __syncthreads();
+  if (kh != 0 || (rg & 1)) return;
+  const int nn = tile * 8 * Tg::RG + (rg >> 1) * 16 + r16;
+  if (nn >= N) return;
+  const float bg = p.bias ? bf16_bits_to_f32(p.bias[nn]) : 0.f, bu = p.bias2 ? bf16_bits_to_f32(p.bias2[nn]) : 0.f;
+#pragma unroll
+  for (int mt = 0; mt < MT; mt++) {
+    const f32x4 u4 = hand[((rg >> 1) * MT + mt) * 64 + lane];
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      const int m = m_block0<MT>() + 16 * mt + 4 * gq + v;
+      if (m >= M) continue;
+      const float g = bf16_bits_to_f32(f32_to_bf16_bits(acc[mt][v] + bg));
+      const float u = bf16_bits_to_f32(f32_to_bf16_bits(u4[v] + bu));
+      const float sig = bf16_bits_to_f32(f32_to_bf16_bits(1.0f / (1.0f + expf(-g))));
+      const float a = bf16_bits_to_f32(f32_to_bf16_bits(g * sig));
+      p.y[static_cast<int64_t>(m) * N + nn] = static_cast<uint16_t>(f32_to_bf16_bits(a * u));
+    }
+  }
+}
+
 // One item per workgroup: blockIdx.x = tile of 16 RG rows, blockIdx.y = K
 // slice, blockIdx.z = M block.
 template <int BITS, int GS, int MT, int WV, int NCH, int KH>
@@ -503,12 +569,14 @@ __global__ __launch_bounds__(64 * WV) void qmv_tile_fused_kernel(const TileFused
 // is staged into the other buffer: the memory stream of the workgroup keeps
 // going under its arithmetic instead of alternating with it, and a whole
 // projection needs no second pass over partial sums.
-template <int BITS, int GS, int MT, int WV, int NCH, int KH>
+// SW: the SwiGLU form (gate / up row groups in pairs, tile_finish_swiglu).
+template <int BITS, int GS, int MT, int WV, int NCH, int KH, bool SW = false>
 __global__ __launch_bounds__(64 * WV) void qmv_stream_kernel(const TileParams p) {
   using Tg = TileGeom<BITS, GS, MT, WV, NCH, KH>;
   __shared__ u32x4 xs[2][Tg::MR * Tg::ROW16];
   __shared__ __align__(16) uint16_t sx[2][Tg::MR * Tg::SXS];
   __shared__ f32x4 red[KH > 1 ? (KH - 1) * Tg::RG * MT * 64 : 1];
+  __shared__ f32x4 hand[SW ? Tg::RG / 2 * MT * 64 : 1];
   const int steps = p.steps, s0 = blockIdx.y * steps, tile = blockIdx.x;
   // Every load below is issued on every path (a slice past the run re-reads
   // the last one): the memory counter then holds the same loads wherever
@@ -557,7 +625,10 @@ __global__ __launch_bounds__(64 * WV) void qmv_stream_kernel(const TileParams p)
   } else {
     tile_accum(acc, W0, xs[0], sx[0]);
   }
-  tile_finish<BITS, GS, MT, WV, NCH, KH>(p, tile, blockIdx.y, acc, red);
+  if constexpr (SW)
+    tile_finish_swiglu<BITS, GS, MT, WV, NCH, KH>(p, tile, acc, red, hand);
+  else
+    tile_finish<BITS, GS, MT, WV, NCH, KH>(p, tile, blockIdx.y, acc, red);
 }
 
 // y[m, n] = bf16(sum over splits of part[s, m, n] (in split order) + bias[n])
@@ -642,10 +713,10 @@ int run(const TileParams& a, int tiles, int mblocks, hipStream_t st, int* query)
   return check_launch("qmv_tile");
 }
 
-template <int BITS, int MT, int WV, int NCH, int KH>
+template <int BITS, int MT, int WV, int NCH, int KH, bool SW = false>
 int run_stream(const TileParams& a, int tiles, int mblocks, hipStream_t st) {
-  hipLaunchKernelGGL((qmv_stream_kernel<BITS, 64, MT, WV, NCH, KH>), dim3(tiles, a.splits, mblocks), dim3(64 * WV), 0,
-                     st, a);
+  hipLaunchKernelGGL((qmv_stream_kernel<BITS, 64, MT, WV, NCH, KH, SW>), dim3(tiles, a.splits, mblocks),
+                     dim3(64 * WV), 0, st, a);
   return check_launch("qmv_stream");
 }
 
@@ -930,6 +1001,67 @@ int run_fused(const Cfg& c, const TileFused& f, int tiles, int mb, hipStream_t s
 }
 
 }  // namespace tile
+
+namespace tile {
+
+template <int BITS, int MT>
+int run_swiglu(const SCfg& c, const TileParams& a, int tiles, int mb, hipStream_t st) {
+  constexpr int F = BITS == 4 ? 1 : 2;
+  if (c.wv == 8 && c.kh == 2)
+    return c.nch == 2 ? run_stream<BITS, MT, 8, 2 * F, 2, true>(a, tiles, mb, st)
+                      : run_stream<BITS, MT, 8, 4 * F, 2, true>(a, tiles, mb, st);
+  return run_stream<BITS, MT, 4, 4 * F, 1, true>(a, tiles, mb, st);  // {4, 4, 1}
+}
+
+}  // namespace tile
+
+// SwiGLU of two projections (gate, up) of the same activations in one
+// streaming launch, for 5..32 rows: the configurations stream_preferred
+// takes for gate/up-like shapes (one K split), gate and up row groups
+// paired in each workgroup.
+bool qmv_tile_swiglu_eligible(const QmvFused& f) {
+  if (!f.swiglu || f.norm_w || f.rep > 1 || f.nproj != 2 || f.M < 5 || f.M > kQmvMaxM || f.group_size != 64)
+    return false;
+  if (f.proj[0].N != f.proj[1].N || f.proj[0].res || f.proj[1].res || f.x_stride != f.K) return false;
+  const int64_t N = f.proj[0].N, K = f.K;
+  if (!qmv_tile_eligible(f.M, N, K, 64, f.bits)) return false;
+  SCfg c;
+  int splits = 1;
+  if (!stream_preferred(f.M, N, K, f.bits, c, splits) || splits != 1) return false;
+  const bool known = (c.wv == 8 && c.kh == 2 && (c.nch == 2 || c.nch == 4)) || (c.wv == 4 && c.kh == 1 && c.nch == 4);
+  const int64_t per = c.nch * (f.bits == 4 ? 1 : 2) * c.kh;
+  return known && chunks_of(K, f.bits) % per == 0;
+}
+
+int launch_qmv_tile_swiglu(const QmvFused& f, hipStream_t st) {
+  if (!qmv_tile_swiglu_eligible(f)) return fail(MLXQ_ERR_UNSUPPORTED, "qmv_tile_swiglu: shape not supported");
+  const int64_t N = f.proj[0].N, K = f.K;
+  SCfg c;
+  int splits = 1;
+  stream_preferred(f.M, N, K, f.bits, c, splits);
+  TileParams a{};
+  a.x = f.x;
+  a.M = static_cast<int>(f.M);
+  a.N = static_cast<int>(N);
+  a.K = static_cast<int>(K);
+  a.wq = f.proj[0].wq;
+  a.s = f.proj[0].s;
+  a.b = f.proj[0].b;
+  a.bias = f.proj[0].bias;
+  a.wq2 = f.proj[1].wq;
+  a.s2 = f.proj[1].s;
+  a.b2 = f.proj[1].b;
+  a.bias2 = f.proj[1].bias;
+  a.y = f.proj[0].y;
+  a.swiglu = 1;
+  a.splits = 1;
+  const int64_t per = c.nch * (f.bits == 4 ? 1 : 2) * c.kh;
+  a.steps = static_cast<int>(chunks_of(K, f.bits) / per);
+  const int tiles = static_cast<int>(ceil_div(N, 8 * (c.wv / c.kh)));  // 16 outputs per gate/up pair of row groups
+  const int mt = f.M <= 16 ? 1 : 2;
+  if (f.bits == 4) return mt == 1 ? run_swiglu<4, 1>(c, a, tiles, 1, st) : run_swiglu<4, 2>(c, a, tiles, 1, st);
+  return mt == 1 ? run_swiglu<8, 1>(c, a, tiles, 1, st) : run_swiglu<8, 2>(c, a, tiles, 1, st);
+}
 
 // The whole-K form carries the fused decode forms for 5..32 activation rows:
 // group size 64, K one slice of 8 waves x 4 chunks (Q4 K = 4096, Q8 K = 2048

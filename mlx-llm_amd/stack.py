@@ -211,13 +211,18 @@ class DecodeStack:
 
             def mlp_in(P=P, L=L, split=split):
                 mlxq.rms_norm(h, L.ln2, c.eps, out=n)
-                if "mlp" in split:
+
+                def plain():
                     lin(n, P["gate"], g)
                     lin(n, P["up"], u)
+                    mlxq.silu_mul(g, u, out=a)
+
+                if "mlp" in split:  # gate/up pairs and SwiGLU in one streaming launch where covered
+                    fz(n, [self._proj(P["gate"], a), self._proj(P["up"], u)], plain, swiglu=True)
                 else:
                     fz(n, [self._proj(P["gate"], g), self._proj(P["up"], u)],
                        lambda: (lin(n, P["gate"], g), lin(n, P["up"], u)))
-                mlxq.silu_mul(g, u, out=a)
+                    mlxq.silu_mul(g, u, out=a)
 
             def down(P=P, xn=xn):
                 lin(a, P["down"], d)

@@ -263,3 +263,28 @@ def test_tile_fused_matches_legacy_form(torch_gpu, monkeypatch):
         outs.append([orc.bf16_to_f32(host(p["y"])) for p in projs])
     for a, b in zip(*outs):
         assert np.max(np.abs(a - b)) / np.max(np.abs(b)) <= 8e-3
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("m", [5, 16, 17, 32])
+@pytest.mark.parametrize("n", [14336, 8200])
+def test_tile_swiglu_batched(torch_gpu, bits, m, n):
+    """5..32 rows: gate and up row groups paired in one streaming launch,
+    y = silu(gate) * up at MLX's rounding points (no norm: the caller ran it);
+    ragged N, a bias on the gate."""
+    k = 4096
+    x = bf16_acts(80 + m, m, k)
+    hg, dg = qlayer(81 + bits, n, k, 64, bits)
+    hu, du = qlayer(82 + bits, n, k, 64, bits)
+    bias = orc.f32_to_bf16(orc.normal(83, n, 0.0, 1.0))
+    dg["y"], du["y"], dg["bias"] = out_like(m, n), out_like(m, n), dev(bias, True)
+    mlxq.qmatmul_fused(dev(x, True), [dg, du], 64, bits, swiglu=True)
+    g = orc.f32_to_bf16(orc.bf16_to_f32(orc.qlinear_bf16(x, hg, 64, bits)) + orc.bf16_to_f32(bias)[None, :])
+    check(dg["y"], orc.silu_mul(g, orc.qlinear_bf16(x, hu, 64, bits)))
+
+
+def test_swiglu_without_norm_needs_more_rows(torch_gpu):
+    hw, dw = qlayer(90, 256, 512, 64, 4)
+    dw["y"] = out_like(4, 256)
+    with pytest.raises(mlxq.Unsupported):
+        mlxq.qmatmul_fused(dev(bf16_acts(91, 4, 512), True), [dw, dict(dw)], 64, 4, swiglu=True)
