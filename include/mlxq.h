@@ -180,13 +180,18 @@ typedef struct {
  * and then, for nproj <= 3 projections of the same x' (q, k, v at
  * llama.rs:806-812), y_i = x' W_i^T (+ bias_i) (+ residual_i: the residual
  * add of llama.rs:729-733, rounded as add(r, bf16(x' W^T))).
- * swiglu != 0 (requires norm_weight and nproj == 2): y_0 = silu(x' W_0^T) *
- * (x' W_1^T) with the rounding of mlxq_silu_mul (llama.rs:1040-1045).
+ * swiglu != 0 (nproj == 2): y_0 = silu(x' W_0^T) * (x' W_1^T) with the
+ * rounding of mlxq_silu_mul (llama.rs:1040-1045).
  * Results equal the unfused sequence of mlxq_rms_norm / mlxq_repeat_kv /
  * mlxq_qmatmul / mlxq_add / mlxq_silu_mul up to f32 summation order.
- * Covers the decode kernel's shapes (1 <= M <= 4, K*bits/8 % 64 == 0);
- * other shapes return MLXQ_ERR_UNSUPPORTED before any launch, and the
- * caller issues the unfused calls.  No workspace, no allocation. */
+ * Covers: 1 <= M <= 4 (K*bits/8 % 64 == 0), every form, SwiGLU only with a
+ * norm; 5 <= M <= 32, group size 64: multi-projection / head repeat /
+ * residual forms where K is one tile slice (Q4 K = 4096, Q8 K = 2048 or
+ * 4096), SwiGLU without a norm on gate/up-like shapes (N * K >= 2^25,
+ * K < N), the residual / multi-projection forms otherwise.  Other shapes
+ * and forms (e.g. a norm above 4 rows) return MLXQ_ERR_UNSUPPORTED before
+ * any launch, and the caller issues the unfused calls.  No workspace, no
+ * allocation. */
 int mlxq_qmatmul_fused(const void* x, int64_t M, int64_t K,
                        const void* norm_weight, float eps, int kv_heads,
                        int head_dim, int groups, const mlxq_projection* proj,
