@@ -299,6 +299,15 @@ int mlxq_silu_mul(const void* gate, const void* up, int64_t n, void* y,
  * (src/models/llama.rs:729-733): y = bf16(a + b), n % 8 == 0. */
 int mlxq_add(const void* a, const void* b, int64_t n, void* y, void* stream);
 
+/* The residual add that ends a layer followed by the RMSNorm that starts
+ * the next one (src/models/llama.rs:729-733 then :698, or the final norm
+ * at :596), in one launch: sum = bf16(a + b) as mlxq_add, y =
+ * rms_norm(sum, weight, eps) as mlxq_rms_norm.  a, b, sum, y: [rows, dim]
+ * bf16, dim % 8 == 0. */
+int mlxq_add_rms_norm(const void* a, const void* b, const void* weight,
+                      int64_t rows, int64_t dim, float eps, void* sum,
+                      void* y, void* stream);
+
 /* Replaces repeat_kv (src/primitives/attention.rs:45-55) for one position:
  * x [rows, kv_heads, head_dim] -> y [rows, kv_heads*groups, head_dim], output
  * head h = KV head h / groups.  head_dim % 8 == 0. */

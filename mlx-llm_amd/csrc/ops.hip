@@ -86,6 +86,59 @@ __global__ void silu_mul_kernel(const uint4* __restrict__ g, const uint4* __rest
   }
 }
 
+// The residual add of a layer's end and the RMSNorm that starts the next
+// layer (or the final norm) in one pass: one workgroup per row writes
+// s = bf16(a + b) and y = rms_norm(s), each rounded as add_kernel /
+// rms_norm_kernel round it.
+__global__ __launch_bounds__(kNormThreads) void add_rms_norm_kernel(const uint16_t* __restrict__ a,
+                                                                    const uint16_t* __restrict__ b,
+                                                                    const uint16_t* __restrict__ w, int D, float eps,
+                                                                    uint16_t* __restrict__ s,
+                                                                    uint16_t* __restrict__ y) {
+  __shared__ float part[kNormThreads / 64];
+  const int64_t off = static_cast<int64_t>(blockIdx.x) * D;
+  const uint4* ar = reinterpret_cast<const uint4*>(a + off);
+  const uint4* br = reinterpret_cast<const uint4*>(b + off);
+  uint4* sr = reinterpret_cast<uint4*>(s + off);
+  uint4* yr = reinterpret_cast<uint4*>(y + off);
+  const uint4* wv = reinterpret_cast<const uint4*>(w);
+  const int pieces = D / 8;
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < pieces; i += kNormThreads) {
+    const uint4 p = ar[i], q = br[i];
+    const uint32_t pa[4] = {p.x, p.y, p.z, p.w}, qb[4] = {q.x, q.y, q.z, q.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      o[j] = pack2(lo_f(pa[j]) + lo_f(qb[j]), hi_f(pa[j]) + hi_f(qb[j]));
+      const float u = lo_f(o[j]), v = hi_f(o[j]);
+      ss = fmaf(u, u, ss);
+      ss = fmaf(v, v, ss);
+    }
+    sr[i] = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int i = 0; i < kNormThreads / 64; i++) tot += part[i];
+  const float inv = 1.0f / sqrtf(tot / static_cast<float>(D) + eps);
+  for (int i = threadIdx.x; i < pieces; i += kNormThreads) {
+    const uint4 p = ar[i], q = br[i], g = wv[i];
+    const uint32_t pa[4] = {p.x, p.y, p.z, p.w}, qb[4] = {q.x, q.y, q.z, q.w}, gw[4] = {g.x, g.y, g.z, g.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const uint32_t sv = pack2(lo_f(pa[j]) + lo_f(qb[j]), hi_f(pa[j]) + hi_f(qb[j]));
+      const float n0 = bf16_bits_to_f32(f32_to_bf16_bits(lo_f(sv) * inv));
+      const float n1 = bf16_bits_to_f32(f32_to_bf16_bits(hi_f(sv) * inv));
+      o[j] = pack2(lo_f(gw[j]) * n0, hi_f(gw[j]) * n1);
+    }
+    yr[i] = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
 __global__ void add_kernel(const uint4* __restrict__ a, const uint4* __restrict__ b, int64_t n8,
                            uint4* __restrict__ y) {
   for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n8;
@@ -133,6 +186,24 @@ extern "C" int mlxq_rms_norm(const void* x, const void* weight, int64_t rows, in
                      static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(weight), static_cast<int>(dim),
                      eps, static_cast<uint16_t*>(y));
   return check_launch("rms_norm");
+}
+
+extern "C" int mlxq_add_rms_norm(const void* a, const void* b, const void* weight, int64_t rows, int64_t dim,
+                                 float eps, void* sum, void* y, void* stream) {
+  clear_error();
+  if (rows < 0 || dim <= 0) return fail(MLXQ_ERR_INVALID, "add_rms_norm: bad shape");
+  if (dim % 8) return fail(MLXQ_ERR_SHAPE, "add_rms_norm: dim must be a multiple of 8");
+  if (!(eps >= 0.f)) return fail(MLXQ_ERR_INVALID, "add_rms_norm: eps must be >= 0");
+  if (rows == 0) return MLXQ_OK;
+  if (!a || !b || !weight || !sum || !y) return fail(MLXQ_ERR_INVALID, "add_rms_norm: null pointer");
+  if (misaligned(a) || misaligned(b) || misaligned(weight) || misaligned(sum) || misaligned(y))
+    return fail(MLXQ_ERR_INVALID, "add_rms_norm: pointers must be 16-byte aligned");
+  if (rows > INT32_MAX || dim > INT32_MAX) return fail(MLXQ_ERR_INVALID, "add_rms_norm: too large");
+  hipLaunchKernelGGL(add_rms_norm_kernel, dim3(static_cast<unsigned>(rows)), dim3(kNormThreads), 0,
+                     as_stream(stream), static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b),
+                     static_cast<const uint16_t*>(weight), static_cast<int>(dim), eps, static_cast<uint16_t*>(sum),
+                     static_cast<uint16_t*>(y));
+  return check_launch("add_rms_norm");
 }
 
 extern "C" int mlxq_silu_mul(const void* gate, const void* up, int64_t n, void* y, void* stream) {

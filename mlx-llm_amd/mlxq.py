@@ -52,6 +52,7 @@ SIGNATURES = {
     "mlxq_rms_norm": (ctypes.c_int, [_vp, _vp, _i64, _i64, ctypes.c_float, _vp, _vp]),
     "mlxq_silu_mul": (ctypes.c_int, [_vp, _vp, _i64, _vp, _vp]),
     "mlxq_add": (ctypes.c_int, [_vp, _vp, _i64, _vp, _vp]),
+    "mlxq_add_rms_norm": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, ctypes.c_float, _vp, _vp, _vp]),
     "mlxq_repeat_kv": (ctypes.c_int, [_vp, _i64, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp, _vp]),
     "mlxq_gguf_requantize": (ctypes.c_int, [_u32, _vp, _i64, _i64, _i64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                             _vp, _vp, _vp, _vp]),
@@ -286,6 +287,17 @@ def rms_norm(x, weight, eps: float, out=None):
     y = out if out is not None else torch.empty_like(x)
     check(lib().mlxq_rms_norm(_ptr(x), _ptr(weight), x.numel() // d, d, eps, _ptr(y), _stream()))
     return y
+
+
+def add_rms_norm(a, b, weight, eps: float, sum_out=None, out=None):
+    """sum = a + b (bf16, as add), y = rms_norm(sum) (as rms_norm), one launch."""
+    torch = _torch()
+    d = a.shape[-1]
+    s = sum_out if sum_out is not None else torch.empty_like(a)
+    y = out if out is not None else torch.empty_like(a)
+    check(lib().mlxq_add_rms_norm(_ptr(a), _ptr(b), _ptr(weight), a.numel() // d, d, eps, _ptr(s), _ptr(y),
+                                  _stream()))
+    return s, y
 
 
 def silu_mul(gate, up, out=None):

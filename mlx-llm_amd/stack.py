@@ -192,7 +192,12 @@ class DecodeStack:
         # 3.01 -> 2.85 ms per step); q/k/v and o keep the fused forms (plain
         # calls there: 3.24 / 2.98 ms)
         split = {"mlp", "down"} if b > 4 else set()
-        for j, i in enumerate(range(len(self.layers)) if layers is None else layers):
+        order = list(range(len(self.layers)) if layers is None else layers)
+        # b > 4: the residual add that ends a layer and the norm that starts
+        # the next (or the final norm) run as one launch; `normed` says that
+        # n already holds the next norm's output
+        normed = [False]
+        for j, i in enumerate(order):
             L = self.layers[i]
             P = L.proj
             xn = (self.xa if j % 2 == 0 else self.xb)[:b]
@@ -201,7 +206,8 @@ class DecodeStack:
             # the norm / head repeat / SwiGLU run as their own kernels and the
             # projections still share launches with their residual adds
             def qkv(x=x, P=P, L=L):
-                mlxq.rms_norm(x, L.ln1, c.eps, out=n)
+                if not normed[0]:
+                    mlxq.rms_norm(x, L.ln1, c.eps, out=n)
                 fz(n, [self._proj(P["q"], q), self._proj(P["k"], k), self._proj(P["v"], v)],
                    lambda: (lin(n, P["q"], q), lin(n, P["k"], k), lin(n, P["v"], v)))
 
@@ -224,17 +230,24 @@ class DecodeStack:
                        lambda: (lin(n, P["gate"], g), lin(n, P["up"], u)))
                     mlxq.silu_mul(g, u, out=a)
 
-            def down(P=P, xn=xn):
+            nxt = self.layers[order[j + 1]].ln1 if j + 1 < len(order) else (self.norm if head else None)
+
+            def down(P=P, xn=xn, nxt=nxt):
                 lin(a, P["down"], d)
-                mlxq.add(h, d, out=xn)
+                if nxt is not None:
+                    mlxq.add_rms_norm(h, d, nxt, c.eps, sum_out=xn, out=n)
+                else:
+                    mlxq.add(h, d, out=xn)
 
             fz(x, [self._proj(P["q"], q), self._proj(P["k"], k), self._proj(P["v"], v)], qkv,
                norm_weight=L.ln1, eps=c.eps)
+            normed[0] = False
             fz(v, [self._proj(P["o"], h, res=x)], oproj, repeat=(c.kv_heads, c.head_dim, c.groups))
             fz(h, [self._proj(P["gate"], a), self._proj(P["up"], u)], mlp_in, norm_weight=L.ln2, eps=c.eps,
                swiglu=True)
             if "down" in split:
                 down()
+                normed[0] = nxt is not None
             else:
                 fz(a, [self._proj(P["down"], xn, res=h)], down)
             x = xn
@@ -242,7 +255,8 @@ class DecodeStack:
             return x
 
         def head_ops(x=x):
-            mlxq.rms_norm(x, self.norm, c.eps, out=n)
+            if not normed[0]:
+                mlxq.rms_norm(x, self.norm, c.eps, out=n)
             lin(n, self.lm_head, self.logits[:b])
 
         fz(x, [self._proj(self.lm_head, self.logits[:b])], head_ops, norm_weight=self.norm, eps=c.eps)

@@ -31,6 +31,22 @@ def test_rms_norm(torch_gpu, rows, dim):
     _ulp_close(got, want)
 
 
+@pytest.mark.parametrize("rows,dim", [(1, 4096), (16, 4096), (3, 14336), (2, 8)])
+def test_add_rms_norm(torch_gpu, rows, dim):
+    """One launch of the residual add and the next norm: the sum bit-exact
+    with the oracle's add, the norm as rms_norm of that sum, and both
+    bit-identical to the separate add and rms_norm kernels."""
+    a = orc.f32_to_bf16(orc.normal(500 + rows, rows * dim, 0.0, 2.0)).reshape(rows, dim)
+    b = orc.f32_to_bf16(orc.normal(501 + rows, rows * dim, 0.0, 1.0)).reshape(rows, dim)
+    w = orc.f32_to_bf16(orc.normal(502 + dim, dim, 1.0, 0.2))
+    s, y = mlxq.add_rms_norm(dev(a, True), dev(b, True), dev(w, True), 1e-5)
+    want_s = orc.add(a, b)
+    assert np.array_equal(host(s), want_s)
+    _ulp_close(host(y), orc.rms_norm(want_s, w, 1e-5))
+    s2 = mlxq.add(dev(a, True), dev(b, True))
+    assert np.array_equal(host(y), host(mlxq.rms_norm(s2, dev(w, True), 1e-5)))
+
+
 def test_silu_mul(torch_gpu):
     n = 16 * 14336
     g = orc.f32_to_bf16(orc.normal(300, n, 0.0, 3.0))
