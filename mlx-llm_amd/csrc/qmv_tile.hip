@@ -77,7 +77,6 @@ struct TileParams {
   const uint16_t* s2;
   const uint16_t* b2;
   const uint16_t* bias2;
-  int swiglu;
   int x_stride;            // activation row stride (elements)
   int rep_hd8, rep;        // head repeat: piece k8 reads (k8 / (rep_hd8 rep)) rep_hd8 + k8 % rep_hd8
   float rcp_hd8, rcp_grp;
@@ -218,7 +217,7 @@ __device__ __forceinline__ void tile_load_x(const TileParams& p, int split, Tile
 // The group parameters, then the codes chunk by chunk (the math on chunk c
 // waits only for chunks <= c), of this lane's weight row over this wave's
 // part of the slice.
-template <int BITS, int GS, int MT, int WV, int NCH, int KH>
+template <int BITS, int GS, int MT, int WV, int NCH, int KH, bool SW = false>
 __device__ __forceinline__ void tile_load_w(const TileParams& p, int tile, int split,
                                             TileW<BITS, GS, MT, WV, NCH, KH>& W) {
   using Tg = TileGeom<BITS, GS, MT, WV, NCH, KH>;
@@ -233,9 +232,9 @@ __device__ __forceinline__ void tile_load_w(const TileParams& p, int tile, int s
   const int c0 = (split * KH + kh) * NCH;  // first chunk of the wave's part
   // rows past N repeat row N-1 (results dropped); SwiGLU: row group rg
   // reads matrix rg & 1 at output block rg / 2
-  const bool up = p.swiglu && (rg & 1);
-  const int n = p.swiglu ? min(tile * 8 * Tg::RG + (rg >> 1) * 16 + r16, p.N - 1)
-                         : min(tile * 16 * Tg::RG + rg * 16 + r16, p.N - 1);
+  const bool up = SW && (rg & 1);
+  const int n = SW ? min(tile * 8 * Tg::RG + (rg >> 1) * 16 + r16, p.N - 1)
+                   : min(tile * 16 * Tg::RG + rg * 16 + r16, p.N - 1);
   load_param_words<Tg::NGW>((up ? p.s2 : p.s) + static_cast<int64_t>(n) * G + c0 * Bk::KC / GS, W.sw);
   load_param_words<Tg::NGW>((up ? p.b2 : p.b) + static_cast<int64_t>(n) * G + c0 * Bk::KC / GS, W.bw);
   const u32x4* wrow = reinterpret_cast<const u32x4*>(up ? p.wq2 : p.wq) + n * row_u4 + gq;
@@ -396,7 +395,7 @@ __device__ __forceinline__ void tile_accum(f32x4 (&acc)[MT], const TileW<BITS, G
 // The end of a workgroup item: K parts 1.. hand their sums to part 0 through
 // LDS (added in part order), then y (one K split) or the split's f32 partial
 // tile.
-template <int BITS, int GS, int MT, int WV, int NCH, int KH>
+template <int BITS, int GS, int MT, int WV, int NCH, int KH, bool RES = false>
 __device__ __forceinline__ void tile_finish(const TileParams& p, int tile, int split, f32x4 (&acc)[MT], f32x4* red) {
   using Tg = TileGeom<BITS, GS, MT, WV, NCH, KH>;
   const int M = p.M, N = p.N;
@@ -438,7 +437,7 @@ __device__ __forceinline__ void tile_finish(const TileParams& p, int tile, int s
         if (m >= M) continue;
         const int64_t o = static_cast<int64_t>(m) * N + nn;
         uint32_t r = f32_to_bf16_bits(acc[mt][v] + bb);
-        if (p.res) r = f32_to_bf16_bits(bf16_bits_to_f32(p.res[o]) + bf16_bits_to_f32(r));  // residual: bf16(r + bf16(v))
+        if (RES && p.res) r = f32_to_bf16_bits(bf16_bits_to_f32(p.res[o]) + bf16_bits_to_f32(r));  // residual: bf16(r + bf16(v))
         p.y[o] = static_cast<uint16_t>(r);
       }
     return;
@@ -559,7 +558,7 @@ __global__ __launch_bounds__(64 * WV) void qmv_tile_fused_kernel(const TileFused
 #pragma unroll
   for (int mt = 0; mt < MT; mt++) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
   tile_accum(acc, W, xs, sx);
-  tile_finish<BITS, GS, MT, WV, NCH, KH>(p, tile, 0, acc, red);
+  tile_finish<BITS, GS, MT, WV, NCH, KH, true>(p, tile, 0, acc, red);
 }
 
 // Streaming form: a workgroup owns its 16 RG weight rows over `steps`
@@ -587,9 +586,9 @@ __global__ __launch_bounds__(64 * WV) void qmv_stream_kernel(const TileParams p)
   TileX<BITS, GS, MT, WV, NCH, KH> X0, X1;
   TileW<BITS, GS, MT, WV, NCH, KH> W0, W1;
   tile_load_x(p, s0, X0);
-  tile_load_w(p, tile, s0, W0);
+  tile_load_w<BITS, GS, MT, WV, NCH, KH, SW>(p, tile, s0, W0);
   tile_load_x(p, min(s0 + 1, last), X1);
-  tile_load_w(p, tile, min(s0 + 1, last), W1);
+  tile_load_w<BITS, GS, MT, WV, NCH, KH, SW>(p, tile, min(s0 + 1, last), W1);
   __builtin_amdgcn_sched_barrier(0);
   tile_stage(X0, xs[0], sx[0]);
   f32x4 acc[MT];
@@ -602,18 +601,18 @@ __global__ __launch_bounds__(64 * WV) void qmv_stream_kernel(const TileParams p)
   for (; s + 3 < steps; s += 2) {
     tile_load_x(p, s0 + s + 2, X0);
     tile_accum(acc, W0, xs[0], sx[0]);
-    tile_load_w(p, tile, s0 + s + 2, W0);
+    tile_load_w<BITS, GS, MT, WV, NCH, KH, SW>(p, tile, s0 + s + 2, W0);
     tile_stage(X1, xs[1], sx[1], s == 0);
     tile_load_x(p, s0 + s + 3, X1);
     tile_accum(acc, W1, xs[1], sx[1]);
-    tile_load_w(p, tile, s0 + s + 3, W1);
+    tile_load_w<BITS, GS, MT, WV, NCH, KH, SW>(p, tile, s0 + s + 3, W1);
     tile_stage(X0, xs[0], sx[0], false);
   }
   const int rest = steps - s;  // 1 only when steps == 1
   if (rest == 3) {
     tile_load_x(p, s0 + s + 2, X0);
     tile_accum(acc, W0, xs[0], sx[0]);
-    tile_load_w(p, tile, s0 + s + 2, W0);
+    tile_load_w<BITS, GS, MT, WV, NCH, KH, SW>(p, tile, s0 + s + 2, W0);
     tile_stage(X1, xs[1], sx[1], s == 0);
     tile_accum(acc, W1, xs[1], sx[1]);
     tile_stage(X0, xs[0], sx[0], false);
@@ -1053,7 +1052,6 @@ int launch_qmv_tile_swiglu(const QmvFused& f, hipStream_t st) {
   a.b2 = f.proj[1].b;
   a.bias2 = f.proj[1].bias;
   a.y = f.proj[0].y;
-  a.swiglu = 1;
   a.splits = 1;
   const int64_t per = c.nch * (f.bits == 4 ? 1 : 2) * c.kh;
   a.steps = static_cast<int>(chunks_of(K, f.bits) / per);
