@@ -397,9 +397,18 @@ int launch_ni(RowParams& a, int64_t M, int R, int W, hipStream_t st) {
 // Fused forms at M = 1 (the batch-1 decode chain), K*bits/8 of 1, 2 or 4 KB.
 template <int BITS, int NI, int F>
 int launch_fused_r(RowParams& a, int R, hipStream_t st) {
+  // 8 waves per workgroup for the norm / SwiGLU / head-repeat forms: half
+  // the workgroups stage (and normalise) the activations (config-5 batch-1
+  // step 1.263 -> 1.245 and 1.232 -> 1.219 ms on two boxes); MLXQ_QMV_ROW_W=4 or 8 forces either
+  const bool w8 = overrides().row_w ? overrides().row_w == 8 : F != 0;
   if constexpr (F & kSwiGLU) {
+    if (w8) return launch_rw<BITS, NI, 2, 8, 1, F>(a, set_tiles(a, 2, 8, true), st);
     return launch_rw<BITS, NI, 2, 4, 1, F>(a, set_tiles(a, 2, 4, true), st);
   } else {
+    if (w8) {
+      if (R >= 2) return launch_rw<BITS, NI, 2, 8, 1, F>(a, set_tiles(a, 2, 8, false), st);
+      return launch_rw<BITS, NI, 1, 8, 1, F>(a, set_tiles(a, 1, 8, false), st);
+    }
     if (R >= 2) return launch_rw<BITS, NI, 2, 4, 1, F>(a, set_tiles(a, 2, 4, false), st);
     return launch_rw<BITS, NI, 1, 4, 1, F>(a, set_tiles(a, 1, 4, false), st);
   }
