@@ -869,13 +869,13 @@ bool qmv_tile_preferred(int64_t M, int64_t N, int64_t K, int bits) {
   // (qmv_dot) at the Llama-3-8B projection shapes: the tile kernel wins on
   // the large projections from M = 8 (Q4) / 16 (Q8),
   // on gate/up already from M = 3 (Q4) / 4 (Q8), on short matrices (N <= 2048) from
-  // M = 16, and on the other small projections from M = 24 (Q4) / 32 (Q8).
+  // M = 16, and on the other small projections above 16 rows.
   const bool large = N * K >= (int64_t(1) << 25);
   if (M <= 4) return large && K < N && M >= (bits == 4 ? 3 : 4);
   if (short_fullk(M, N, K, bits, nullptr)) return true;
   if (large) return K < N || M >= (bits == 4 ? 8 : 16);  // gate/up-like: the streaming form (Q8 M = 8 20.4 -> 19.0)
   if (N <= 2048) return M >= 16;  // k/v: M = 16 Q4 8.28 -> 7.93 us, Q8 9.27 -> 8.06; Q8 M = 24 11.07 -> 8.93
-  return M >= (bits == 4 ? 24 : 32);
+  return M > 16;  // q/o-like: Q4 M = 20 10.16 -> 9.21 us, Q8 M = 24 11.36 -> 10.42 against the block kernel
 }
 
 bool qmv_dot_preferred(int64_t M, int64_t N, int64_t K, int bits) {
