@@ -198,6 +198,26 @@ int mlxq_qmatmul_fused(const void* x, int64_t M, int64_t K,
                        int nproj, int swiglu, int group_size, int bits,
                        void* stream);
 
+/* The end of a decoder layer and the start of the next
+ * (src/models/llama.rs:729-733 residual add after down_proj, then :698
+ * input_layernorm of the next layer):
+ *   sum_out = bf16(residual + bf16(x W^T (+ bias_vec))),
+ *   y       = rms_norm(sum_out, norm_weight, eps)   (as mlxq_rms_norm).
+ * Results equal mlxq_qmatmul followed by mlxq_add_rms_norm bit for bit.  At
+ * 5 <= M <= 32 where mlxq_qmatmul splits K, the split sum, the residual and
+ * the norm run in one second launch (one workgroup per row) instead of two;
+ * other shapes run the unfused calls.  workspace / workspace_bytes as for
+ * mlxq_qmatmul (mlxq_qmatmul_workspace_size).  residual, norm_weight,
+ * sum_out and y are bf16 ([M, N], [N], [M, N], [M, N]), 16-byte aligned;
+ * N % 8 == 0; sum_out may not alias residual. */
+int mlxq_qmatmul_add_rms_norm(const void* x, int64_t M, const uint32_t* wq,
+                              const void* scales, const void* biases,
+                              const void* bias_vec, int64_t N, int64_t K,
+                              int group_size, int bits, const void* residual,
+                              const void* norm_weight, float eps,
+                              void* sum_out, void* y, void* workspace,
+                              size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------ */
 /* Whole batch-1 decode step in one persistent launch                  */
 /* ------------------------------------------------------------------ */

@@ -289,6 +289,49 @@ extern "C" int mlxq_qmatmul_fused(const void* x, int64_t M, int64_t K, const voi
   return launch_qmv_dot_fused(f, as_stream(stream));
 }
 
+// Down projection + residual add + the next layer's RMSNorm (llama.rs:729-733
+// then :698): at 5..32 rows on the tile kernels the split-K sum, the residual
+// and the norm share the second launch; elsewhere the unfused calls.
+extern "C" int mlxq_qmatmul_add_rms_norm(const void* x, int64_t M, const uint32_t* wq, const void* scales,
+                                         const void* biases, const void* bias_vec, int64_t N, int64_t K,
+                                         int group_size, int bits, const void* residual, const void* norm_weight,
+                                         float eps, void* sum_out, void* y, void* workspace, size_t workspace_bytes,
+                                         void* stream) {
+  clear_error();
+  int rc = check_shape(M, N, K, group_size, bits);
+  if (rc) return rc;
+  if (M == 0) return MLXQ_OK;
+  if (!residual || !norm_weight || !sum_out || !y) return fail(MLXQ_ERR_INVALID, "qmatmul_add_rms_norm: null pointer");
+  auto mis = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15u) != 0; };
+  if (mis(residual) || mis(norm_weight) || mis(sum_out) || mis(y))
+    return fail(MLXQ_ERR_INVALID, "qmatmul_add_rms_norm: pointers must be 16-byte aligned");
+  if (N % 8) return fail(MLXQ_ERR_SHAPE, "qmatmul_add_rms_norm: N must be a multiple of 8");
+  if (!(eps >= 0.f)) return fail(MLXQ_ERR_INVALID, "qmatmul_add_rms_norm: eps must be >= 0");
+  const Overrides& ov = overrides();
+  const uint16_t* res = static_cast<const uint16_t*>(residual);
+  uint16_t* so = static_cast<uint16_t*>(sum_out);
+  if (M > kQmvDotMaxM && M <= kQmvMaxM && qmv_tile_eligible(M, N, K, group_size, bits) &&
+      (qmv_tile_preferred(M, N, K, bits) || ov.qmv_tile_all) && !ov.qmv_legacy && !ov.qmv_stream &&
+      !ov.qmv_no_tile_fused && x && wq && scales && biases) {
+    AddNormEpilogue ep{res, static_cast<const uint16_t*>(norm_weight), eps, so, static_cast<uint16_t*>(y), false};
+    rc = launch_qmv_tile(static_cast<const uint16_t*>(x), M, wq, static_cast<const uint16_t*>(scales),
+                         static_cast<const uint16_t*>(biases), static_cast<const uint16_t*>(bias_vec), N, K,
+                         group_size, bits, so, workspace, workspace_bytes, as_stream(stream), &ep);
+    if (rc == MLXQ_OK && ep.applied) return MLXQ_OK;
+    if (rc == MLXQ_OK) {  // one K slice: the projection is in sum_out
+      if ((rc = mlxq_add(res, so, M * N, so, stream))) return rc;
+      return mlxq_rms_norm(so, norm_weight, M, N, eps, y, stream);
+    }
+    if (rc != MLXQ_ERR_UNSUPPORTED) return rc;
+    clear_error();
+  }
+  rc = qmatmul_dispatch(x, M, wq, scales, biases, bias_vec, N, K, group_size, bits, so, workspace, workspace_bytes,
+                        MLXQ_ALGO_AUTO, true, stream);
+  if (rc) return rc;
+  if ((rc = mlxq_add(res, so, M * N, so, stream))) return rc;  // element-wise, in place
+  return mlxq_rms_norm(so, norm_weight, M, N, eps, y, stream);
+}
+
 // ---------------------------------------------------------------- no-alloc
 
 namespace {

@@ -91,10 +91,24 @@ int launch_qmv_tile_swiglu(const QmvFused& f, hipStream_t st);
 size_t qmv_tile_workspace_bytes(int64_t M, int64_t N);
 bool qmv_tile_preferred(int64_t M, int64_t N, int64_t K, int bits);
 bool qmv_dot_preferred(int64_t M, int64_t N, int64_t K, int bits);  // M <= 4: vector-ALU kernel
+// The decode chain's down projection with the residual add and the next
+// RMSNorm in the second kernel of a split-K launch: instead of y, sum_out =
+// bf16(res + bf16(sum + bias)) and y_norm = rms_norm(sum_out) (one workgroup
+// per row).  applied: the launch took it (split K); else y was written.
+struct AddNormEpilogue {
+  const uint16_t* res;
+  const uint16_t* norm_w;
+  float eps;
+  uint16_t* sum_out;
+  uint16_t* y_norm;
+  bool applied;
+};
 int launch_qmv_tile(const uint16_t* x, int64_t M, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
                     const uint16_t* bias, int64_t N, int64_t K, int group_size, int bits, uint16_t* y,
-                    void* workspace, size_t workspace_bytes, hipStream_t st);
+                    void* workspace, size_t workspace_bytes, hipStream_t st, AddNormEpilogue* ep = nullptr);
 
+int launch_split_add_norm(const float* part, const uint16_t* bias, int64_t M, int64_t N, int splits,
+                          const AddNormEpilogue& ep, hipStream_t st);
 // y = bf16(sum over the splits of part[split][M][N], in split order, + bias):
 // the second kernel of every split-K launch.
 int launch_split_reduce(const float* part, const uint16_t* bias, uint16_t* y, int64_t M, int64_t N, int splits,

@@ -49,6 +49,8 @@ SIGNATURES = {
     "mlxq_qmatmul_fused": (ctypes.c_int, [_vp, _i64, _i64, _vp, ctypes.c_float, ctypes.c_int, ctypes.c_int,
                                           ctypes.c_int, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                           ctypes.c_int, _vp]),
+    "mlxq_qmatmul_add_rms_norm": (ctypes.c_int, [_vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, ctypes.c_int,
+                                                 ctypes.c_int, _vp, _vp, ctypes.c_float, _vp, _vp, _vp, _sz, _vp]),
     "mlxq_rms_norm": (ctypes.c_int, [_vp, _vp, _i64, _i64, ctypes.c_float, _vp, _vp]),
     "mlxq_silu_mul": (ctypes.c_int, [_vp, _vp, _i64, _vp, _vp]),
     "mlxq_add": (ctypes.c_int, [_vp, _vp, _i64, _vp, _vp]),
@@ -297,6 +299,25 @@ def add_rms_norm(a, b, weight, eps: float, sum_out=None, out=None):
     y = out if out is not None else torch.empty_like(a)
     check(lib().mlxq_add_rms_norm(_ptr(a), _ptr(b), _ptr(weight), a.numel() // d, d, eps, _ptr(s), _ptr(y),
                                   _stream()))
+    return s, y
+
+
+def qmatmul_add_rms_norm(x, wq, scales, biases, residual, weight, eps: float, group_size: int = 64, bits: int = 4,
+                         bias=None, sum_out=None, out=None):
+    """sum = residual + qmatmul(x) (bf16, as add), y = rms_norm(sum); the
+    split-K sum, the add and the norm share one launch where K is split."""
+    torch = _torch()
+    k = x.shape[-1]
+    n = wq.shape[0]
+    x2 = x.reshape(-1, k)
+    m = x2.shape[0]
+    s = sum_out if sum_out is not None else torch.empty((m, n), dtype=torch.bfloat16, device=x.device)
+    y = out if out is not None else torch.empty((m, n), dtype=torch.bfloat16, device=x.device)
+    nbytes = workspace_size(m, n, k, group_size, bits)
+    ws = workspace(nbytes, x.device) if nbytes else None
+    check(lib().mlxq_qmatmul_add_rms_norm(_ptr(x2), m, _ptr(wq), _ptr(scales), _ptr(biases), _ptr(bias), n, k,
+                                          group_size, bits, _ptr(residual), _ptr(weight), eps, _ptr(s), _ptr(y),
+                                          _ptr(ws), 0 if ws is None else ws.numel(), _stream()))
     return s, y
 
 

@@ -233,10 +233,12 @@ class DecodeStack:
             nxt = self.layers[order[j + 1]].ln1 if j + 1 < len(order) else (self.norm if head else None)
 
             def down(P=P, xn=xn, nxt=nxt):
-                lin(a, P["down"], d)
-                if nxt is not None:
-                    mlxq.add_rms_norm(h, d, nxt, c.eps, sum_out=xn, out=n)
+                if nxt is not None:  # down + residual + the next norm (split-K sum, add and norm in one launch)
+                    pd = P["down"]
+                    mlxq.qmatmul_add_rms_norm(a, pd.wq, pd.scales, pd.biases, h, nxt, c.eps, gs, bits,
+                                              sum_out=xn, out=n)
                 else:
+                    lin(a, P["down"], d)
                     mlxq.add(h, d, out=xn)
 
             fz(x, [self._proj(P["q"], q), self._proj(P["k"], k), self._proj(P["v"], v)], qkv,

@@ -76,3 +76,38 @@ def test_ops_reject_bad_shapes(torch_gpu):
         mlxq.add(x, x)  # 12 is not a multiple of 8
     with pytest.raises(mlxq.MlxqError):
         mlxq.rms_norm(x.view(1, 12), x, 1e-5)
+
+
+@pytest.mark.parametrize("bits,m,k,n,with_bias", [
+    (4, 16, 14336, 4096, False),  # split K: the sum, add and norm in the second launch
+    (4, 32, 14336, 4096, True),
+    (8, 16, 14336, 4096, False),
+    (8, 32, 14336, 4096, True),
+    (4, 24, 4096, 4096, False),   # one K slice: the projection, then add and norm
+    (4, 2, 14336, 4096, False),   # batch 2: the unfused calls
+    (8, 40, 2048, 1024, True),    # prefill rows
+])
+def test_qmatmul_add_rms_norm(torch_gpu, bits, m, k, n, with_bias):
+    """Down projection + residual + next norm (llama.rs:729-733, :698) in one
+    call: bit-identical to mlxq_qmatmul followed by mlxq_add_rms_norm, and
+    the sum within twice the qmatmul bar of the f64 oracle."""
+    from helpers import bf16_acts, rel_err
+    from test_gpu_qmatmul import TIGHT, make_layer
+    wq, s, b = make_layer(600 + bits + m, n, k, 64, bits)
+    x = bf16_acts(601 + m, m, k)
+    r = orc.f32_to_bf16(orc.normal(602 + m, m * n, 0.0, 1.0)).reshape(m, n)
+    w = orc.f32_to_bf16(orc.normal(603, n, 1.0, 0.2))
+    bias = orc.f32_to_bf16(orc.normal(604, n, 0.0, 1.0)) if with_bias else None
+    xd, wd, sd, bd, rd, gw = dev(x, True), dev(wq), dev(s, True), dev(b, True), dev(r, True), dev(w, True)
+    biasd = dev(bias, True) if with_bias else None
+    print(f"qmatmul_add_rms_norm bits={bits} m={m} k={k} n={n} bias={with_bias}", flush=True)
+    s_got, y_got = mlxq.qmatmul_add_rms_norm(xd, wd, sd, bd, rd, gw, 1e-5, 64, bits, bias=biasd)
+    d = mlxq.qmatmul(xd, wd, sd, bd, 64, bits, bias=biasd)
+    s_want, y_want = mlxq.add_rms_norm(rd, d, gw, 1e-5)
+    assert np.array_equal(host(s_got), host(s_want))
+    assert np.array_equal(host(y_got), host(y_want))
+    ref = orc.qmatmul_f64(x, wq, s, b, 64, bits) + orc.bf16_to_f32(r).astype(np.float64)
+    if with_bias:
+        ref += orc.bf16_to_f32(bias)[None, :].astype(np.float64)
+    # two bf16 roundings (the projection's output, then the sum): twice the bar
+    assert rel_err(orc.bf16_to_f32(host(s_got)), ref) <= 2 * TIGHT
