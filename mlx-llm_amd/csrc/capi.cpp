@@ -50,6 +50,7 @@ const Overrides* read_overrides() {
   o->tile_mb = flag("MLXQ_QMV_TILE_MB");
   o->qmv_no_tile_fused = flag("MLXQ_QMV_NO_TILE_FUSED");
   if (const char* e = getenv("MLXQ_QMV_TILE")) sscanf(e, "%d,%d,%d", &o->tile_wv, &o->tile_nch, &o->tile_kh);
+  if (const char* e = getenv("MLXQ_QMV_TILE_FUSED_RG")) o->tile_fused_rg = atoi(e);
   if (const char* e = getenv("MLXQ_QMV_TILE_STREAM")) {
     o->stream_set = true;
     sscanf(e, "%d,%d,%d,%d", &o->stream_wv, &o->stream_nch, &o->stream_kh, &o->stream_splits);

@@ -1095,7 +1095,10 @@ namespace tile {
 
 template <int BITS>
 int run_fused(const Cfg& c, const TileFused& f, int tiles, int mb, hipStream_t st) {
-  if (c.nch == 4) {
+  if (c.kh == 4) {  // two row groups x four K parts (32 rows per workgroup)
+    hipLaunchKernelGGL((qmv_tile_fused_kernel<BITS, 64, 1, 8, BITS == 4 ? 8 : 16, 4>), dim3(tiles, 1, mb), dim3(512), 0,
+                       st, f);
+  } else if (c.nch == 4) {
     hipLaunchKernelGGL((qmv_tile_fused_kernel<BITS, 64, 1, 8, 4, 8>), dim3(tiles, 1, mb), dim3(512), 0, st, f);
   } else {
     if constexpr (BITS == 8)
@@ -1204,15 +1207,22 @@ int launch_qmv_tile_fused(const QmvFused& f, hipStream_t st) {
   a.p.rcp_hd8 = 1.0f / static_cast<float>(a.p.rep_hd8);
   a.p.rcp_grp = 1.0f / static_cast<float>(a.p.rep_hd8 * a.p.rep);
   a.nseg = f.nproj;
+  const int64_t ch = chunks_of(f.K, f.bits);
+  const int mb = static_cast<int>(ceil_div(f.M, 16));
+  // 16-row tiles past one round of CUs: 32 rows per workgroup (two row
+  // groups x four K parts) in one round instead
+  int64_t tiles16 = 0;
+  for (int i = 0; i < f.nproj; i++) tiles16 += ceil_div(f.proj[i].N, 16);
+  const bool rg2 = tiles16 * mb > cu_count() && ch % 4 == 0 && ch / 4 == (f.bits == 4 ? 8 : 16) &&
+                   overrides().tile_fused_rg != 1;
+  const Cfg c = rg2 ? Cfg{1, 8, static_cast<int>(ch / 4), 4} : Cfg{1, 8, static_cast<int>(ch / 8), 8};
+  const int rows = rg2 ? 32 : 16;
   int tiles = 0;
   for (int i = 0; i < f.nproj; i++) {
     const QmvProj& P = f.proj[i];
-    tiles += static_cast<int>(ceil_div(P.N, 16));
+    tiles += static_cast<int>(ceil_div(P.N, rows));
     a.seg[i] = TileSeg{P.wq, P.s, P.b, P.bias, P.res, P.y, static_cast<int>(P.N), tiles};
   }
-  const int64_t ch = chunks_of(f.K, f.bits);
-  const Cfg c{1, 8, static_cast<int>(ch / 8), 8};
-  const int mb = static_cast<int>(ceil_div(f.M, 16));
   return f.bits == 4 ? run_fused<4>(c, a, tiles, mb, st) : run_fused<8>(c, a, tiles, mb, st);
 }
 
