@@ -893,13 +893,18 @@ int dispatch_stream(int bits, int mt, const SCfg& c, const TileParams& a, int ti
 bool cfg_known(const Cfg& c, int bits) {
   if (c.kh == 1) return (c.wv == 4 && (c.nch == 4 || c.nch == 8)) || (c.wv == 8 && (c.nch == 4 || c.nch == 8 || c.nch == 16));
   if (c.kh == 8) return c.wv == 8 && c.mt == 1 && (c.nch == 4 || (c.nch == 8 && bits == 8));
+  if (c.kh == 4 && c.mt == 1 && c.wv == 8 && c.nch == (bits == 4 ? 8 : 16)) return true;  // whole-K, 32 rows
   return c.wv == 8 && ((c.kh == 2 && (c.nch == 4 || c.nch == 8)) || (c.kh == 4 && c.nch == 4));
 }
 
 template <int BITS, int MT>
 int run_wn(const Cfg& c, const TileParams& a, int tiles, int mb, hipStream_t st, int* q) {
   if (c.kh == 2) return c.nch == 4 ? run<BITS, MT, 8, 4, 2>(a, tiles, mb, st, q) : run<BITS, MT, 8, 8, 2>(a, tiles, mb, st, q);
-  if (c.kh == 4) return run<BITS, MT, 8, 4, 4>(a, tiles, mb, st, q);
+  if (c.kh == 4) {
+    if constexpr (MT == 1)
+      if (c.nch == (BITS == 4 ? 8 : 16)) return run<BITS, MT, 8, BITS == 4 ? 8 : 16, 4>(a, tiles, mb, st, q);
+    return run<BITS, MT, 8, 4, 4>(a, tiles, mb, st, q);
+  }
   if constexpr (MT == 1) {
     if (c.kh == 8) {
       if constexpr (BITS == 8)
@@ -945,7 +950,17 @@ bool short_fullk(int64_t M, int64_t N, int64_t K, int bits, Cfg* c) {
   const int64_t ch = chunks_of(K, bits);
   const Cfg f{1, 8, static_cast<int>(ch / 8), 8};
   if (ch % 8 || !cfg_known(f, bits)) return false;
-  if (ceil_div(N, 16) * ceil_div(M, 16) > cu_count()) return false;
+  if (ceil_div(N, 16) * ceil_div(M, 16) > cu_count()) {
+    // past one round: 32 rows per workgroup (two row groups x four K parts)
+    // in one round, Q4 (q/o at M = 17 / 24 / 32: 9.02 / 9.29 / 9.39 -> 7.98 /
+    // 8.01 / 8.05 us; Q8 10.16 -> 10.41 at M = 17, 10.76 -> 10.49 at 32)
+    const Cfg f2{1, 8, static_cast<int>(ch / 4), 4};
+    if (bits != 4 || overrides().tile_fused_rg == 1 || !cfg_known(f2, bits) ||
+        ceil_div(N, 32) * ceil_div(M, 16) > cu_count())
+      return false;
+    if (c) *c = f2;
+    return true;
+  }
   if (c) *c = f;
   return true;
 }
