@@ -163,7 +163,9 @@ int qmatmul_dispatch(const void* x, int64_t M, const uint32_t* wq, const void* s
   const Overrides& ov = overrides();
   // M = 2: also on the taller matrices except Q4 gate/up-like ones (Q8 gate
   // 17.0 -> 14.4 us, Q8 q 7.0 -> 6.3, Q4 q 6.0 -> 5.7; Q4 gate stays on qmv_dot)
-  const bool row_m2 = M == 2 && !(bits == 4 && K < N && N * K >= (int64_t(1) << 25));
+  const bool gate_like = K < N && N * K >= (int64_t(1) << 25);
+  // M = 3: Q8 gate/up-like ones too (19.42 -> 16.82 us; the other shapes at parity or slower)
+  const bool row_m2 = (M == 2 && !(bits == 4 && gate_like)) || (M == 3 && bits == 8 && gate_like);
   if (qmv_row_eligible(M, N, K, group_size, bits) && (M == 1 || row_m2 || N <= 2048 || ov.qmv_row_all) &&
       !ov.qmv_no_row && !ov.qmv_mfma)
     return launch_qmv_row(xp, M, wq, sp, bp, bias, N, K, group_size, bits, yp, st);

@@ -51,7 +51,7 @@ def test_qmv_small(torch_gpu, bits, gs, m):
 
 @pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("name", list(LLAMA))
-@pytest.mark.parametrize("m", [1, 4, 16, 32])
+@pytest.mark.parametrize("m", [1, 3, 4, 16, 32])
 def test_qmv_llama_shapes(torch_gpu, bits, name, m):
     k, n = LLAMA[name]
     wq, s, b = make_layer(0x5EED0000 + k + n + bits, n, k, 64, bits)
