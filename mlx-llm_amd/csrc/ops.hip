@@ -67,6 +67,61 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const uint16_t* 
   }
 }
 
+// The same computation with the row's pieces (i = t, t + 256, ...; at most
+// PT per thread) loaded once, all before any arithmetic, and kept in
+// registers for the second pass: one memory round trip instead of three.
+template <int PT>
+__global__ __launch_bounds__(kNormThreads) void rms_norm_reg_kernel(const uint16_t* __restrict__ x,
+                                                                    const uint16_t* __restrict__ w, int D, float eps,
+                                                                    uint16_t* __restrict__ y) {
+  __shared__ float part[kNormThreads / 64];
+  const int row = blockIdx.x;
+  const uint4* xr = reinterpret_cast<const uint4*>(x + static_cast<int64_t>(row) * D);
+  uint4* yr = reinterpret_cast<uint4*>(y + static_cast<int64_t>(row) * D);
+  const uint4* wv = reinterpret_cast<const uint4*>(w);
+  const int pieces = D / 8;
+  uint4 v[PT], g[PT];
+#pragma unroll
+  for (int k = 0; k < PT; k++) {
+    const int i = min(static_cast<int>(threadIdx.x) + kNormThreads * k, pieces - 1);  // clamped, no branch
+    v[k] = xr[i];
+    g[k] = wv[i];
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < PT; k++) {
+    if (static_cast<int>(threadIdx.x) + kNormThreads * k >= pieces) break;
+    const uint32_t a[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const float p = lo_f(a[j]), q = hi_f(a[j]);
+      ss = fmaf(p, p, ss);
+      ss = fmaf(q, q, ss);
+    }
+  }
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int i = 0; i < kNormThreads / 64; i++) tot += part[i];
+  const float inv = 1.0f / sqrtf(tot / static_cast<float>(D) + eps);
+#pragma unroll
+  for (int k = 0; k < PT; k++) {
+    const int i = static_cast<int>(threadIdx.x) + kNormThreads * k;
+    if (i >= pieces) break;
+    const uint32_t a[4] = {v[k].x, v[k].y, v[k].z, v[k].w}, b[4] = {g[k].x, g[k].y, g[k].z, g[k].w};
+    uint32_t o[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const float n0 = bf16_bits_to_f32(f32_to_bf16_bits(lo_f(a[j]) * inv));
+      const float n1 = bf16_bits_to_f32(f32_to_bf16_bits(hi_f(a[j]) * inv));
+      o[j] = pack2(lo_f(b[j]) * n0, hi_f(b[j]) * n1);
+    }
+    yr[i] = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
 __device__ __forceinline__ float silu_bf16(float g) {
   const float s = bf16_bits_to_f32(f32_to_bf16_bits(1.0f / (1.0f + expf(-g))));
   return bf16_bits_to_f32(f32_to_bf16_bits(g * s));
@@ -182,7 +237,14 @@ extern "C" int mlxq_rms_norm(const void* x, const void* weight, int64_t rows, in
   if (misaligned(x) || misaligned(weight) || misaligned(y))
     return fail(MLXQ_ERR_INVALID, "rms_norm: pointers must be 16-byte aligned");
   if (rows > INT32_MAX) return fail(MLXQ_ERR_INVALID, "rms_norm: too many rows");
-  hipLaunchKernelGGL(rms_norm_kernel, dim3(static_cast<unsigned>(rows)), dim3(kNormThreads), 0, as_stream(stream),
+  // rows of up to 16384: the register-resident form (same results)
+  const int64_t pt = ceil_div(dim / 8, int64_t(kNormThreads));
+  auto kern = pt <= 1 ? rms_norm_reg_kernel<1>
+              : pt <= 2 ? rms_norm_reg_kernel<2>
+              : pt <= 4 ? rms_norm_reg_kernel<4>
+              : pt <= 8 ? rms_norm_reg_kernel<8>
+                        : rms_norm_kernel;
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(rows)), dim3(kNormThreads), 0, as_stream(stream),
                      static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(weight), static_cast<int>(dim),
                      eps, static_cast<uint16_t*>(y));
   return check_launch("rms_norm");

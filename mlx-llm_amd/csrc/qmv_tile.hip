@@ -693,12 +693,15 @@ __global__ __launch_bounds__(256) void split_reduce4_kernel(const float4* __rest
 // The split sum as split_reduce4_kernel (split order, then the bias, then
 // bf16), then the residual add and RMSNorm of mlxq_add_rms_norm on the row
 // (same per-thread pieces and reduction order): one workgroup per row.
+template <int PT>
 __global__ __launch_bounds__(256) void split_add_norm_kernel(const float* __restrict__ part,
                                                              const uint16_t* __restrict__ bias,
                                                              const uint16_t* __restrict__ res,
                                                              const uint16_t* __restrict__ w, int64_t MN, int N,
                                                              int splits, float eps, uint16_t* __restrict__ s,
                                                              uint16_t* __restrict__ y) {
+  // PT pieces of 8 per thread at most (pieces i = t, t + 256, ...), all
+  // loaded before any arithmetic and kept in registers between the passes
   __shared__ float wpart[4];
   const int64_t off = static_cast<int64_t>(blockIdx.x) * N;
   const uint4* rr = reinterpret_cast<const uint4*>(res + off);
@@ -706,34 +709,48 @@ __global__ __launch_bounds__(256) void split_add_norm_kernel(const float* __rest
   uint4* yr = reinterpret_cast<uint4*>(y + off);
   const uint4* wv = reinterpret_cast<const uint4*>(w);
   const int pieces = N / 8;
-  float ss = 0.f;
-  for (int i = threadIdx.x; i < pieces; i += 256) {
+  float4 lo[PT], hi[PT];
+  uint4 r[PT], g[PT];
+#pragma unroll
+  for (int k = 0; k < PT; k++) {
+    const int i = min(static_cast<int>(threadIdx.x) + 256 * k, pieces - 1);  // clamped: no branch around the loads
     const float4* p0 = reinterpret_cast<const float4*>(part + off) + 2 * i;
-    float4 lo = p0[0], hi = p0[1];
-    for (int sp = 1; sp < splits; sp++) {
+    lo[k] = p0[0];
+    hi[k] = p0[1];
+    r[k] = rr[i];
+    g[k] = wv[i];
+  }
+  for (int sp = 1; sp < splits; sp++)
+#pragma unroll
+    for (int k = 0; k < PT; k++) {
+      const int i = min(static_cast<int>(threadIdx.x) + 256 * k, pieces - 1);
       const float4* pp = reinterpret_cast<const float4*>(part + sp * MN + off) + 2 * i;
       const float4 u = pp[0], v = pp[1];
-      lo.x += u.x; lo.y += u.y; lo.z += u.z; lo.w += u.w;
-      hi.x += v.x; hi.y += v.y; hi.z += v.z; hi.w += v.w;
+      lo[k].x += u.x; lo[k].y += u.y; lo[k].z += u.z; lo[k].w += u.w;
+      hi[k].x += v.x; hi[k].y += v.y; hi[k].z += v.z; hi[k].w += v.w;
     }
-    float d[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+  float ss = 0.f;
+  uint32_t o[PT][4];
+#pragma unroll
+  for (int k = 0; k < PT; k++) {
+    const int i = static_cast<int>(threadIdx.x) + 256 * k;
+    if (i >= pieces) break;
+    float d[8] = {lo[k].x, lo[k].y, lo[k].z, lo[k].w, hi[k].x, hi[k].y, hi[k].z, hi[k].w};
     if (bias)
 #pragma unroll
       for (int e = 0; e < 8; e++) d[e] += bf16_bits_to_f32(bias[8 * i + e]);
-    const uint4 r = rr[i];
-    const uint32_t ra[4] = {r.x, r.y, r.z, r.w};
-    uint32_t o[4];
+    const uint32_t ra[4] = {r[k].x, r[k].y, r[k].z, r[k].w};
 #pragma unroll
     for (int j = 0; j < 4; j++) {
       const float d0 = bf16_bits_to_f32(f32_to_bf16_bits(d[2 * j]));
       const float d1 = bf16_bits_to_f32(f32_to_bf16_bits(d[2 * j + 1]));
-      o[j] = f32_to_bf16_bits(bf16_bits_to_f32(ra[j] & 0xFFFFu) + d0) |
-             (f32_to_bf16_bits(bf16_bits_to_f32(ra[j] >> 16) + d1) << 16);
-      const float u = bf16_bits_to_f32(o[j] & 0xFFFFu), v = bf16_bits_to_f32(o[j] >> 16);
+      o[k][j] = f32_to_bf16_bits(bf16_bits_to_f32(ra[j] & 0xFFFFu) + d0) |
+                (f32_to_bf16_bits(bf16_bits_to_f32(ra[j] >> 16) + d1) << 16);
+      const float u = bf16_bits_to_f32(o[k][j] & 0xFFFFu), v = bf16_bits_to_f32(o[k][j] >> 16);
       ss = fmaf(u, u, ss);
       ss = fmaf(v, v, ss);
     }
-    sr[i] = make_uint4(o[0], o[1], o[2], o[3]);
+    sr[i] = make_uint4(o[k][0], o[k][1], o[k][2], o[k][3]);
   }
   ss = wave_sum(ss);
   if ((threadIdx.x & 63) == 0) wpart[threadIdx.x >> 6] = ss;
@@ -742,18 +759,20 @@ __global__ __launch_bounds__(256) void split_add_norm_kernel(const float* __rest
 #pragma unroll
   for (int i = 0; i < 4; i++) tot += wpart[i];
   const float inv = 1.0f / sqrtf(tot / static_cast<float>(N) + eps);
-  for (int i = threadIdx.x; i < pieces; i += 256) {
-    const uint4 sv4 = sr[i], g = wv[i];  // this thread's own sums from the loop above
-    const uint32_t sv[4] = {sv4.x, sv4.y, sv4.z, sv4.w}, gw[4] = {g.x, g.y, g.z, g.w};
-    uint32_t o[4];
+#pragma unroll
+  for (int k = 0; k < PT; k++) {
+    const int i = static_cast<int>(threadIdx.x) + 256 * k;
+    if (i >= pieces) break;
+    const uint32_t gw[4] = {g[k].x, g[k].y, g[k].z, g[k].w};
+    uint32_t q[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-      const float n0 = bf16_bits_to_f32(f32_to_bf16_bits(bf16_bits_to_f32(sv[j] & 0xFFFFu) * inv));
-      const float n1 = bf16_bits_to_f32(f32_to_bf16_bits(bf16_bits_to_f32(sv[j] >> 16) * inv));
-      o[j] = f32_to_bf16_bits(bf16_bits_to_f32(gw[j] & 0xFFFFu) * n0) |
+      const float n0 = bf16_bits_to_f32(f32_to_bf16_bits(bf16_bits_to_f32(o[k][j] & 0xFFFFu) * inv));
+      const float n1 = bf16_bits_to_f32(f32_to_bf16_bits(bf16_bits_to_f32(o[k][j] >> 16) * inv));
+      q[j] = f32_to_bf16_bits(bf16_bits_to_f32(gw[j] & 0xFFFFu) * n0) |
              (f32_to_bf16_bits(bf16_bits_to_f32(gw[j] >> 16) * n1) << 16);
     }
-    yr[i] = make_uint4(o[0], o[1], o[2], o[3]);
+    yr[i] = make_uint4(q[0], q[1], q[2], q[3]);
   }
 }
 
@@ -761,8 +780,15 @@ __global__ __launch_bounds__(256) void split_add_norm_kernel(const float* __rest
 
 int launch_split_add_norm(const float* part, const uint16_t* bias, int64_t M, int64_t N, int splits,
                           const AddNormEpilogue& ep, hipStream_t st) {
-  hipLaunchKernelGGL(tile::split_add_norm_kernel, dim3(static_cast<unsigned>(M)), dim3(256), 0, st, part, bias,
-                     ep.res, ep.norm_w, M * N, static_cast<int>(N), splits, ep.eps, ep.sum_out, ep.y_norm);
+  // pieces of 8 per thread (the same assignment as mlxq_add_rms_norm)
+  const int64_t pt = ceil_div(N / 8, int64_t(256));
+  auto kern = pt <= 1 ? tile::split_add_norm_kernel<1>
+              : pt <= 2 ? tile::split_add_norm_kernel<2>
+              : pt <= 4 ? tile::split_add_norm_kernel<4>
+                        : tile::split_add_norm_kernel<8>;
+  if (pt > 8) return fail(MLXQ_ERR_UNSUPPORTED, "split_add_norm: rows longer than 16384");
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(M)), dim3(256), 0, st, part, bias, ep.res, ep.norm_w, M * N,
+                     static_cast<int>(N), splits, ep.eps, ep.sum_out, ep.y_norm);
   return check_launch("split_add_norm");
 }
 
@@ -1043,7 +1069,7 @@ int launch_qmv_tile(const uint16_t* x, int64_t M, const uint32_t* wq, const uint
       const int mb = static_cast<int>(ceil_div(M, 16 * mt));
       if (int rc = dispatch_stream(bits, mt, c, a, static_cast<int>(tiles), mb, st)) return rc;
       if (splits == 1) return MLXQ_OK;
-      if (ep && N % 8 == 0) {
+      if (ep && N % 8 == 0 && N <= 16384) {
         ep->applied = true;
         return launch_split_add_norm(a.part, bias, M, N, splits, *ep, st);
       }
@@ -1099,7 +1125,7 @@ int launch_qmv_tile(const uint16_t* x, int64_t M, const uint32_t* wq, const uint
   const int mb = static_cast<int>(ceil_div(M, 16 * pick->mt));
   if (int rc = dispatch(bits, *pick, a, static_cast<int>(tiles), mb, st, nullptr)) return rc;
   if (a.splits == 1) return MLXQ_OK;
-  if (ep && N % 8 == 0) {
+  if (ep && N % 8 == 0 && N <= 16384) {
     ep->applied = true;
     return launch_split_add_norm(a.part, bias, M, N, a.splits, *ep, st);
   }

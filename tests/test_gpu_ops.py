@@ -22,7 +22,7 @@ def _ulp_close(got, want, frac=1e-3):
     assert np.all(np.abs(g - w)[diff] <= np.abs(w)[diff] * 2 ** -7 + 1e-30)
 
 
-@pytest.mark.parametrize("rows,dim", [(1, 4096), (16, 4096), (3, 14336), (2, 8)])
+@pytest.mark.parametrize("rows,dim", [(1, 4096), (16, 4096), (3, 14336), (2, 8), (2, 32768)])
 def test_rms_norm(torch_gpu, rows, dim):
     x = orc.f32_to_bf16(orc.normal(100 + rows, rows * dim, 0.0, 2.0)).reshape(rows, dim)
     w = orc.f32_to_bf16(orc.normal(200 + dim, dim, 1.0, 0.2))
@@ -83,6 +83,8 @@ def test_ops_reject_bad_shapes(torch_gpu):
     (4, 32, 14336, 4096, True),
     (8, 16, 14336, 4096, False),
     (8, 32, 14336, 4096, True),
+    (4, 16, 14336, 1024, True),   # a split-K single-slice form, one piece of 8 per thread
+    (4, 20, 16384, 8192, False),  # four pieces per thread
     (4, 24, 4096, 4096, False),   # one K slice: the projection, then add and norm
     (4, 2, 14336, 4096, False),   # batch 2: the unfused calls
     (8, 40, 2048, 1024, True),    # prefill rows
