@@ -28,6 +28,7 @@ from pathlib import Path
 
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / "mlx-llm_amd"))
+import seeded  # noqa: E402  (SplitMix64 / Box-Muller inputs; torch is imported lazily)
 
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, published
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, published
@@ -57,13 +58,13 @@ def qbytes(m, n, k, bits, gs=GS):
 
 
 def make_layers(torch, mlxq, bits, layers, seed):
-    g = torch.Generator(device="cuda")
+    """W ~ N(0, 0.02) f32 from the seeded SplitMix64 stream of each tensor
+    (seed + 1000 * layer + projection), cast to bf16, quantized on device."""
     out = []
     for li in range(layers):
         layer = {}
         for pi, (name, k, n) in enumerate(PROJ):
-            g.manual_seed(seed + 1000 * li + pi)
-            w = (torch.randn((n, k), generator=g, device="cuda", dtype=torch.float32) * 0.02).to(torch.bfloat16)
+            w = seeded.normal(seed + 1000 * li + pi, n * k, 0.0, 0.02, device="cuda").view(n, k).to(torch.bfloat16)
             layer[name] = mlxq.quantize(w, GS, bits)
             del w
         out.append(layer)
@@ -128,8 +129,8 @@ def main(argv=None) -> int:
         m, name = a.profile_libgemm.split(",")
         m = int(m)
         k, n = {p[0]: (p[1], p[2]) for p in PROJ}[name]
-        x = torch.randn((m, k), device="cuda").to(torch.bfloat16)
-        w = (torch.randn((n, k), device="cuda") * 0.02).to(torch.bfloat16)
+        x = seeded.normal(0x5EED0500 + k, m * k, device="cuda").view(m, k).to(torch.bfloat16)
+        w = seeded.normal(0x5EED0600 + k, n * k, 0.0, 0.02, device="cuda").view(n, k).to(torch.bfloat16)
         y = torch.empty((m, n), device="cuda", dtype=torch.bfloat16)
         for _ in range(40):
             torch.matmul(x, w.t(), out=y)
@@ -141,7 +142,7 @@ def main(argv=None) -> int:
         algo = {"auto": mlxq.ALGO_AUTO, "qmm": mlxq.ALGO_QMM, "lib": mlxq.ALGO_QMM_LIB}[alg[0] if alg else "auto"]
         k, n = {p[0]: (p[1], p[2]) for p in PROJ}[name]
         layers = make_layers(torch, mlxq, bits, 8, 0x5EED0000 + 100 * bits)
-        x = torch.randn((m, k), device="cuda").to(torch.bfloat16)
+        x = seeded.normal(0x5EED1000 + m, m * k, device="cuda").view(m, k).to(torch.bfloat16)
         y = torch.empty((m, n), device="cuda", dtype=torch.bfloat16)
         fns = [mlxq.bind_qmatmul(x, *L[name], GS, bits, out=y, algo=algo) for L in layers]
         for _ in range(5):
@@ -160,9 +161,7 @@ def main(argv=None) -> int:
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     dev = torch.device("cuda:0")
     weights = {bits: make_layers(torch, mlxq, bits, LAYERS, 0x5EED0000 + 100 * bits) for bits in BITS}
-    g = torch.Generator(device="cuda")
-    g.manual_seed(0x5EED1000)
-    xs = {(m, k): torch.randn((m, k), generator=g, device=dev).to(torch.bfloat16)
+    xs = {(m, k): seeded.normal(0x5EED1000 + 100000 * m + k, m * k, device=dev).view(m, k).to(torch.bfloat16)
           for m in MS for k in {p[1] for p in PROJ}}
     ys = {(m, n): torch.empty((m, n), device=dev, dtype=torch.bfloat16) for m in MS for n in {p[2] for p in PROJ}}
     # workspace sized for the largest shape up front (no allocation in the timed region)
@@ -296,7 +295,7 @@ def main(argv=None) -> int:
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": a.steps,
         "warmup": a.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16 activations, u4/u8 codes, f32 accumulate",
-        "data": "synthetic: seeded N(0,0.02) bf16 weights quantized on device, N(0,1) bf16 activations",
+        "data": "synthetic: N(0,0.02) weights (SplitMix64 + Box-Muller per tensor, f32 -> bf16) quantized on device, N(0,1) bf16 activations",
         "eager_ms_per_step": round(eager_ms, 4),
         "timing": "value = step bytes / wall time of HIP-graph replays of the step (barrier + synchronize "
                   "around the timed replays); eager_ms_per_step = the same launches issued one by one",
@@ -321,14 +320,13 @@ def main(argv=None) -> int:
 def bench_prefill(torch, mlxq, iters=10):
     """Config 3: M=2048 bf16 x Q4 g64 weights, gate/up (4096->14336) and down (14336->4096)."""
     res = {}
-    g = torch.Generator(device="cuda")
     for name, k, n in (("gate_up", 4096, 14336), ("down", 14336, 4096)):
-        g.manual_seed(0x5EED0300 + k)
-        w = (torch.randn((n, k), generator=g, device="cuda") * 0.02)
-        cols = torch.randperm(k, generator=torch.Generator().manual_seed(k))[: (k + 999) // 1000]
-        w[:, cols] *= 20  # 0.1% outlier input channels
+        w = seeded.normal(0x5EED0300 + k, n * k, 0.0, 0.02, device="cuda").view(n, k)
+        # ceil(0.001 K) outlier input channels, chosen by the seeded stream, x20
+        cols = seeded.choice(0x5EED0700 + k, k, (k + 999) // 1000)
+        w[:, cols] *= 20
         wq, s, b = mlxq.quantize(w.to(torch.bfloat16), 64, 4)
-        x = torch.randn((2048, k), generator=g, device="cuda").to(torch.bfloat16)
+        x = seeded.normal(0x5EED0400 + k, 2048 * k, device="cuda").view(2048, k).to(torch.bfloat16)
         y = torch.empty((2048, n), device="cuda", dtype=torch.bfloat16)
         def timed(algo):
             fn = mlxq.bind_qmatmul(x, wq, s, b, 64, 4, out=y, algo=algo)
@@ -464,9 +462,7 @@ def bench_stack(torch, steps=20, batches=(1, 16)):
 
     cfg = llama3_8b()
     st = DecodeStack(cfg, batch=max(batches), seed=5)
-    g = torch.Generator(device="cuda")
-    g.manual_seed(0x5EED0500)
-    st.x.copy_(torch.randn(st.x.shape, generator=g, device="cuda").to(torch.bfloat16))
+    st.x.copy_(seeded.normal(0x5EED0800, st.x.numel(), device="cuda").view(st.x.shape).to(torch.bfloat16))
     wbytes = st.weight_bytes()
     res = {"model": "Llama-3-8B shapes, random init, 32 layers, Q4 g64 (lm_head Q4)",
            "weight_bytes_per_step": wbytes,

@@ -22,6 +22,7 @@ from __future__ import annotations
 from dataclasses import dataclass, field
 
 import mlxq
+import seeded
 
 PROJ = ("q", "k", "v", "o", "gate", "up", "down")
 
@@ -88,12 +89,12 @@ class DecodeStack:
     def __init__(self, cfg: StackConfig, batch: int = 1, seed: int = 0, device="cuda", norm_noise: float = 0.0):
         import torch
         self.cfg, self.batch, self.device = cfg, batch, torch.device(device)
-        g = torch.Generator(device=self.device)
 
         def qlin(name, idx):
             n, k = cfg.proj_shape(name)
-            g.manual_seed(seed * 1_000_003 + idx)
-            w = (torch.randn((n, k), generator=g, device=self.device) * 0.02).to(torch.bfloat16)
+            # N(0, 0.02) f32 from the tensor's SplitMix64 stream, cast to bf16
+            w = seeded.normal(0x5EED0000 + seed * 1_000_003 + idx, n * k, 0.0, 0.02, device=self.device)
+            w = w.view(n, k).to(torch.bfloat16)
             wq, s, b = mlxq.quantize(w, cfg.group_size, cfg.bits)
             del w
             return QLinear(wq, s, b, n, k)
@@ -101,8 +102,8 @@ class DecodeStack:
         def norm_w(idx):
             w = torch.ones(cfg.hidden, device=self.device)
             if norm_noise:
-                g.manual_seed(seed * 1_000_003 + idx)
-                w = w + norm_noise * torch.randn(cfg.hidden, generator=g, device=self.device)
+                w = w + seeded.normal(0x5EED0000 + seed * 1_000_003 + idx, cfg.hidden, 0.0, norm_noise,
+                                      device=self.device)
             return w.to(torch.bfloat16)
 
         self.layers = []
