@@ -26,14 +26,22 @@ constexpr int kThreads = 256;
 constexpr int kVec = 8;                          // outputs per thread per pass
 constexpr int kChunkElems = kThreads * kVec;     // 2048 elements per chunk
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16_rne(float lo, float hi) {
+  const bf16x2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
 template <bool BF16OUT>
 __device__ __forceinline__ void store_vec(void* out, int64_t e, const float (&v)[kVec]) {
   if constexpr (BF16OUT) {
+    // v_cvt_pk_bf16_f32: round to nearest even, two values per instruction
+    // (the same bits as f32_to_bf16_bits except NaN payloads)
     uint4 p;
-    p.x = f32_to_bf16_bits(v[0]) | (f32_to_bf16_bits(v[1]) << 16);
-    p.y = f32_to_bf16_bits(v[2]) | (f32_to_bf16_bits(v[3]) << 16);
-    p.z = f32_to_bf16_bits(v[4]) | (f32_to_bf16_bits(v[5]) << 16);
-    p.w = f32_to_bf16_bits(v[6]) | (f32_to_bf16_bits(v[7]) << 16);
+    p.x = pack_bf16_rne(v[0], v[1]);
+    p.y = pack_bf16_rne(v[2], v[3]);
+    p.z = pack_bf16_rne(v[4], v[5]);
+    p.w = pack_bf16_rne(v[6], v[7]);
     *reinterpret_cast<uint4*>(static_cast<uint16_t*>(out) + e) = p;
   } else {
     float4* o = reinterpret_cast<float4*>(static_cast<float*>(out) + e);
