@@ -18,6 +18,9 @@
 namespace mlxq {
 namespace {
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+
 constexpr int kThreads = 256;
 
 template <int DT>
@@ -109,11 +112,16 @@ __global__ __launch_bounds__(kThreads) void affine_dequantize_kernel(const uint3
     o[0] = make_float4(r[0], r[1], r[2], r[3]);
     o[1] = make_float4(r[4], r[5], r[6], r[7]);
   } else {
+    // v_cvt_pk_bf16_f32: two values per instruction, round to nearest even
+    auto pk = [](float lo, float hi) {
+      const bf16x2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+      return __builtin_bit_cast(uint32_t, v);
+    };
     uint4 p;
-    p.x = f32_to_bf16_bits(r[0]) | (f32_to_bf16_bits(r[1]) << 16);
-    p.y = f32_to_bf16_bits(r[2]) | (f32_to_bf16_bits(r[3]) << 16);
-    p.z = f32_to_bf16_bits(r[4]) | (f32_to_bf16_bits(r[5]) << 16);
-    p.w = f32_to_bf16_bits(r[6]) | (f32_to_bf16_bits(r[7]) << 16);
+    p.x = pk(r[0], r[1]);
+    p.y = pk(r[2], r[3]);
+    p.z = pk(r[4], r[5]);
+    p.w = pk(r[6], r[7]);
     reinterpret_cast<uint4*>(static_cast<uint16_t*>(out) + lane * 8)[0] = p;
   }
 }
