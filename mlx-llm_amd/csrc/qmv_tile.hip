@@ -80,6 +80,7 @@ struct TileParams {
   int x_stride;            // activation row stride (elements)
   int rep_hd8, rep;        // head repeat: piece k8 reads (k8 / (rep_hd8 rep)) rep_hd8 + k8 % rep_hd8
   float rcp_hd8, rcp_grp;
+  int rep_sh_hd8, rep_sh_grp;  // log2 of rep_hd8 and rep_hd8 rep when both are powers of two, else -1
 };
 
 // One weight matrix of a fused launch; its tiles end at tile_end (exclusive).
@@ -205,10 +206,14 @@ __device__ __forceinline__ void tile_load_x(const TileParams& p, int split, Tile
     int src = col;
     if constexpr (FUSED) {
       if (p.rep > 1) {  // query head hq reads KV head hq / rep (whole-K form: col is the piece of the row)
-        const int grp = p.rep_hd8 * p.rep;
-        const int hq = div_rcp(col, grp, p.rcp_grp);
-        const int r = col - hq * grp;
-        src = hq * p.rep_hd8 + (r - div_rcp(r, p.rep_hd8, p.rcp_hd8) * p.rep_hd8);
+        if (p.rep_sh_grp >= 0) {  // powers of two (Llama: 16 pieces per head, 4 query heads per KV head)
+          src = ((col >> p.rep_sh_grp) << p.rep_sh_hd8) + (col & (p.rep_hd8 - 1));
+        } else {
+          const int grp = p.rep_hd8 * p.rep;
+          const int hq = div_rcp(col, grp, p.rcp_grp);
+          const int r = col - hq * grp;
+          src = hq * p.rep_hd8 + (r - div_rcp(r, p.rep_hd8, p.rcp_hd8) * p.rep_hd8);
+        }
       }
     }
     X.xg[i] = *reinterpret_cast<const u32x4*>(xs0 + min(m_block0<MT>() + row, p.M - 1) * (FUSED ? p.x_stride : p.K) +
@@ -418,8 +423,29 @@ __device__ __forceinline__ void tile_accum(f32x4 (&acc)[MT], const TileW<BITS, G
 // The end of a workgroup item: K parts 1.. hand their sums to part 0 through
 // LDS (added in part order), then y (one K split) or the split's f32 partial
 // tile.
+// The residual values this lane adds in tile_finish<RES> (rows past M read
+// row M - 1, columns past N column N - 1: no branch around the loads),
+// loaded when the workgroup starts so that their latency hides under the
+// math instead of following it.
+template <int BITS, int GS, int MT, int WV, int NCH, int KH>
+__device__ __forceinline__ void tile_load_res(const TileParams& p, int tile, float (&rv)[MT][4]) {
+  using Tg = TileGeom<BITS, GS, MT, WV, NCH, KH>;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int rg = wave % Tg::RG;
+  const int nn = min(tile * 16 * Tg::RG + rg * 16 + (lane & 15), p.N - 1);
+#pragma unroll
+  for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      const int m = min(m_block0<MT>() + 16 * mt + 4 * (lane >> 4) + v, p.M - 1);
+      rv[mt][v] = bf16_bits_to_f32((p.res ? p.res : p.y)[static_cast<int64_t>(m) * p.N + nn]);
+    }
+}
+
 template <int BITS, int GS, int MT, int WV, int NCH, int KH, bool RES = false>
-__device__ __forceinline__ void tile_finish(const TileParams& p, int tile, int split, f32x4 (&acc)[MT], f32x4* red) {
+__device__ __forceinline__ void tile_finish(const TileParams& p, int tile, int split, f32x4 (&acc)[MT], f32x4* red,
+                                            const float (*rv)[4] = nullptr) {
   using Tg = TileGeom<BITS, GS, MT, WV, NCH, KH>;
   const int M = p.M, N = p.N;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -460,7 +486,8 @@ __device__ __forceinline__ void tile_finish(const TileParams& p, int tile, int s
         if (m >= M) continue;
         const int64_t o = static_cast<int64_t>(m) * N + nn;
         uint32_t r = f32_to_bf16_bits(acc[mt][v] + bb);
-        if (RES && p.res) r = f32_to_bf16_bits(bf16_bits_to_f32(p.res[o]) + bf16_bits_to_f32(r));  // residual: bf16(r + bf16(v))
+        if (RES && p.res)  // residual: bf16(r + bf16(v))
+          r = f32_to_bf16_bits((rv ? rv[mt][v] : bf16_bits_to_f32(p.res[o])) + bf16_bits_to_f32(r));
         p.y[o] = static_cast<uint16_t>(r);
       }
     return;
@@ -552,7 +579,7 @@ __global__ __launch_bounds__(64 * WV) void qmv_tile_kernel(const TileParams p) {
 
 // Fused forms on the whole-K single-slice kernel: blockIdx.x picks the
 // segment (weight matrix) and its tile, blockIdx.z the M block; no K split.
-template <int BITS, int GS, int MT, int WV, int NCH, int KH>
+template <int BITS, int GS, int MT, int WV, int NCH, int KH, bool RES>
 __global__ __launch_bounds__(64 * WV) void qmv_tile_fused_kernel(const TileFused f) {
   using Tg = TileGeom<BITS, GS, MT, WV, NCH, KH>;
   __shared__ u32x4 xs[Tg::MR * Tg::ROW16];
@@ -575,13 +602,19 @@ __global__ __launch_bounds__(64 * WV) void qmv_tile_fused_kernel(const TileFused
   TileW<BITS, GS, MT, WV, NCH, KH> W;
   tile_load_x<BITS, GS, MT, WV, NCH, KH, true>(p, 0, X);
   tile_load_w(p, tile, 0, W);
+  // RES (some segment has a residual): loaded on every path (from y in a
+  // segment without one, values unused) -- a load issued on one side of a
+  // branch would make the compiler wait for every earlier load where the
+  // paths join
+  float rv[MT][4] = {};
+  if constexpr (RES) tile_load_res<BITS, GS, MT, WV, NCH, KH>(p, tile, rv);
   __builtin_amdgcn_sched_barrier(0);  // every load is issued before the first wait
   tile_stage(X, xs, sx);
   f32x4 acc[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; mt++) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
   tile_accum(acc, W, xs, sx);
-  tile_finish<BITS, GS, MT, WV, NCH, KH, true>(p, tile, 0, acc, red);
+  tile_finish<BITS, GS, MT, WV, NCH, KH, RES>(p, tile, 0, acc, red, rv);
 }
 
 // Streaming form: a workgroup owns its 16 RG weight rows over `steps`
@@ -1134,18 +1167,24 @@ int launch_qmv_tile(const uint16_t* x, int64_t M, const uint32_t* wq, const uint
 
 namespace tile {
 
-template <int BITS>
-int run_fused(const Cfg& c, const TileFused& f, int tiles, int mb, hipStream_t st) {
+template <int BITS, bool RES>
+int run_fused_r(const Cfg& c, const TileFused& f, int tiles, int mb, hipStream_t st) {
   if (c.kh == 4) {  // two row groups x four K parts (32 rows per workgroup)
-    hipLaunchKernelGGL((qmv_tile_fused_kernel<BITS, 64, 1, 8, BITS == 4 ? 8 : 16, 4>), dim3(tiles, 1, mb), dim3(512), 0,
-                       st, f);
+    hipLaunchKernelGGL((qmv_tile_fused_kernel<BITS, 64, 1, 8, BITS == 4 ? 8 : 16, 4, RES>), dim3(tiles, 1, mb),
+                       dim3(512), 0, st, f);
   } else if (c.nch == 4) {
-    hipLaunchKernelGGL((qmv_tile_fused_kernel<BITS, 64, 1, 8, 4, 8>), dim3(tiles, 1, mb), dim3(512), 0, st, f);
+    hipLaunchKernelGGL((qmv_tile_fused_kernel<BITS, 64, 1, 8, 4, 8, RES>), dim3(tiles, 1, mb), dim3(512), 0, st, f);
   } else {
     if constexpr (BITS == 8)
-      hipLaunchKernelGGL((qmv_tile_fused_kernel<BITS, 64, 1, 8, 8, 8>), dim3(tiles, 1, mb), dim3(512), 0, st, f);
+      hipLaunchKernelGGL((qmv_tile_fused_kernel<BITS, 64, 1, 8, 8, 8, RES>), dim3(tiles, 1, mb), dim3(512), 0, st, f);
   }
   return check_launch("qmv_tile_fused");
+}
+template <int BITS>
+int run_fused(const Cfg& c, const TileFused& f, int tiles, int mb, hipStream_t st) {
+  bool res = false;
+  for (int i = 0; i < f.nseg; i++) res = res || f.seg[i].res;
+  return res ? run_fused_r<BITS, true>(c, f, tiles, mb, st) : run_fused_r<BITS, false>(c, f, tiles, mb, st);
 }
 
 }  // namespace tile
@@ -1247,6 +1286,12 @@ int launch_qmv_tile_fused(const QmvFused& f, hipStream_t st) {
   if (f.rep > 1 && f.rep_hd % 8) return fail(MLXQ_ERR_UNSUPPORTED, "qmv_tile_fused: head size not a multiple of 8");
   a.p.rcp_hd8 = 1.0f / static_cast<float>(a.p.rep_hd8);
   a.p.rcp_grp = 1.0f / static_cast<float>(a.p.rep_hd8 * a.p.rep);
+  {
+    auto lg = [](int v) { return v > 0 && (v & (v - 1)) == 0 ? __builtin_ctz(static_cast<unsigned>(v)) : -1; };
+    const int sh = lg(a.p.rep_hd8), sg = lg(a.p.rep_hd8 * a.p.rep);
+    a.p.rep_sh_hd8 = sh;
+    a.p.rep_sh_grp = sh >= 0 && sg >= 0 ? sg : -1;
+  }
   a.nseg = f.nproj;
   const int64_t ch = chunks_of(f.K, f.bits);
   const int mb = static_cast<int>(ceil_div(f.M, 16));
