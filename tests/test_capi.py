@@ -143,3 +143,32 @@ def test_decode_plan_size_and_unsupported_widths():
     assert L.mlxq_decode_plan_size(ctypes.byref(_decode_cfg(layers=0)), ctypes.byref(size)) == mlxq.ERR_INVALID
     assert L.mlxq_decode_plan_size(None, ctypes.byref(size)) == mlxq.ERR_INVALID
     assert L.mlxq_decode_step(None, None, None, None) == mlxq.ERR_INVALID
+
+
+def test_header_compiles_as_c99(tmp_path):
+    """include/mlxq.h is a plain C header (the boundary binds from C / cgo /
+    bindgen): it compiles alone under -std=c99 -pedantic with warnings as errors."""
+    import shutil
+    import subprocess
+
+    if not shutil.which("gcc"):
+        pytest.skip("no gcc")
+    src = tmp_path / "h.c"
+    src.write_text('#include "mlxq.h"\nint main(void) { return 0; }\n')
+    r = subprocess.run(["gcc", "-std=c99", "-pedantic", "-Wall", "-Wextra", "-Werror", f"-I{ROOT / 'include'}",
+                        "-c", str(src), "-o", str(tmp_path / "h.o")], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+
+
+def test_qmatmul_add_rms_norm_argument_errors():
+    """Checked before any launch: shape, null and alignment, N % 8, eps."""
+    L = mlxq.lib()
+    p = ctypes.c_void_p(0x1000)
+    f = L.mlxq_qmatmul_add_rms_norm
+    ok = (p, 16, p, p, p, None, 4096, 4096, 64, 4)
+    assert f(p, 16, p, p, p, None, 4096, 100, 64, 4, p, p, 1e-5, p, p, None, 0, None) == mlxq.ERR_SHAPE
+    assert f(*ok, None, p, 1e-5, p, p, None, 0, None) == mlxq.ERR_INVALID
+    assert f(*ok, p, p, 1e-5, ctypes.c_void_p(0x1002), p, None, 0, None) == mlxq.ERR_INVALID
+    assert f(p, 16, p, p, p, None, 4100, 4096, 64, 4, p, p, 1e-5, p, p, None, 0, None) == mlxq.ERR_SHAPE
+    assert f(*ok, p, p, -1.0, p, p, None, 0, None) == mlxq.ERR_INVALID
+    assert f(p, 0, p, p, p, None, 4096, 4096, 64, 4, p, p, 1e-5, p, p, None, 0, None) == mlxq.OK
