@@ -259,7 +259,7 @@ def main(argv=None) -> int:
     achieved = dbytes / (avg_us * 1e-6) / 1e9
     # which kernels serve the call (the dispatch rule of qmatmul.cpp /
     # qmv_tile.hip, restated here for the label only)
-    if dm == 1:
+    if row_route(dm, dn, dk, dbits):
         kname = "qmv_row_kernel (vector ALU, whole rows per wave)"
     elif dot_preferred(dm, dn, dk, dbits):
         kname = "qmv_dot_kernel (vector ALU)"
@@ -267,6 +267,8 @@ def main(argv=None) -> int:
         kname = "qmv_stream_kernel (MFMA, a workgroup streams its rows over the whole K; one launch)"
     elif tile_preferred(dm, dn, dk, dbits) and stream_splits(dm, dn, dk, dbits):
         kname = "qmv_stream_kernel + split_reduce4_kernel (MFMA, K in 4 splits; one call = both launches)"
+    elif _short_fullk(dm, dn, dk, dbits):
+        kname = "qmv_tile_kernel (MFMA, whole K per workgroup; one launch)"
     elif tile_preferred(dm, dn, dk, dbits):
         kname = "qmv_tile_kernel + split_reduce4_kernel (MFMA, split K; one call = both launches)"
     else:
@@ -427,26 +429,48 @@ def bench_gguf(torch, mlxq, iters=10):
     return res
 
 
+def _short_fullk(m, n, k, bits):
+    """short_fullk of qmv_tile.hip: the whole-K form on short matrices."""
+    if n * k >= 1 << 25 or m < (6 if n <= 2048 else 8 if bits == 4 else 12):
+        return False
+    ch = k * bits // 8 // 64
+    if ch % 8 or not (ch // 8 == 4 or (bits == 8 and ch // 8 == 8)):
+        return False
+    cdiv = lambda a, b: -(-a // b)  # noqa: E731
+    return cdiv(n, 16) * cdiv(m, 16) <= 256 or (bits == 4 and ch // 4 == 8 and cdiv(n, 32) * cdiv(m, 16) <= 256)
+
+
 def tile_preferred(m, n, k, bits):
     """The decode kernel choice of qmv_tile.hip (qmv_tile_preferred), for labels."""
     large = n * k >= 1 << 25
     if m <= 4:
-        return large and k < n and bits == 4 and m >= 3
+        return large and k < n and m >= (3 if bits == 4 else 4)
+    if _short_fullk(m, n, k, bits):
+        return True
     if large:
-        return m >= (8 if bits == 4 else 16)
-    return m >= (24 if bits == 4 else 32)
+        return k < n or m >= (8 if bits == 4 else 16)
+    if n <= 2048:
+        return m >= 16
+    return m > 16
 
 
 def stream_splits(m, n, k, bits):
     """K splits of the streaming form where qmv_tile.hip's stream_preferred
     takes it (0: not taken), for labels."""
-    if n * k < 1 << 25 or m < 8:
+    if n * k < 1 << 25 or m < (3 if k < n else 8):
         return 0
     if k < n:
         return 1
-    if m > 16 or (bits == 8 and m == 16):
-        return 4
-    return 0
+    return 4 if m >= 16 else 0
+
+
+def row_route(m, n, k, bits):
+    """The whole-row kernel's share of qmatmul.cpp's dispatch (M = 1, 2, Q8
+    gate/up-like at 3, short matrices at 2..4), for labels."""
+    if m > 4 or (m > 1 and k > 4096) or (k * bits // 8) % 1024:
+        return False
+    gate_like = k < n and n * k >= 1 << 25
+    return m == 1 or (m == 2 and not (bits == 4 and gate_like)) or (m == 3 and bits == 8 and gate_like) or n <= 2048
 
 
 def dot_preferred(m, n, k, bits):
