@@ -288,3 +288,30 @@ def test_swiglu_without_norm_needs_more_rows(torch_gpu):
     dw["y"] = out_like(4, 256)
     with pytest.raises(mlxq.Unsupported):
         mlxq.qmatmul_fused(dev(bf16_acts(91, 4, 512), True), [dw, dict(dw)], 64, 4, swiglu=True)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("m", [16, 24])
+def test_tile_fused_32_row_workgroups_ragged(torch_gpu, bits, m):
+    """Three projections whose 16-row tiles exceed one round of CUs take 32
+    rows per workgroup (ragged N = 4008 / 1032 / 1032); one projection has a
+    residual, so the launch loads residual values early and the other
+    segments read their dummy values from y.  Against the oracle chain."""
+    k = 4096
+    x = bf16_acts(70 + m, m, k)
+    r = bf16_acts(71 + m, m, 1032)
+    shapes = [4008, 1032, 1032]
+    host_w, projs = [], []
+    for i, n in enumerate(shapes):
+        hw, dw = qlayer(72 + i + bits, n, k, 64, bits)
+        host_w.append(hw)
+        dw["y"] = out_like(m, n)
+        if i == 2:
+            dw["residual"] = dev(r, True)
+        projs.append(dw)
+    mlxq.qmatmul_fused(dev(x, True), projs, 64, bits)
+    for i, (hw, p) in enumerate(zip(host_w, projs)):
+        want = orc.qlinear_bf16(x, hw, 64, bits)
+        if i == 2:
+            want = orc.add(r, want)
+        check(p["y"], want)

@@ -147,3 +147,30 @@ def test_tile_graph_replay(torch_gpu, tile_all):
         assert torch.equal(c.out, e), f"replay {i}"
         mlxq.qmatmul(x[:8], *d, 64, 4)
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("m", [17, 32])
+def test_tile_whole_k_32_row_workgroups_ragged(torch_gpu, monkeypatch, m):
+    """Q4 q/o-like matrices past one round of 16-row tiles take 32 rows per
+    workgroup (two row groups x four K parts) under the default dispatch;
+    N = 4008 leaves the last workgroup 8 real rows.  Sampled rows (the last
+    ones included) against the oracle, with a bias, and the 16-row form
+    (MLXQ_QMV_TILE_FUSED_RG=1) agrees to the same bar."""
+    for v in ("MLXQ_QMV_TILE", "MLXQ_QMV_TILE_ALL", "MLXQ_QMV_TILE_MB", "MLXQ_QMV_TILE_STREAM",
+              "MLXQ_QMV_TILE_FUSED_RG"):
+        monkeypatch.delenv(v, raising=False)
+    mlxq.reload_overrides()
+    n, k = 4008, 4096
+    wq, s, b = make_layer(90 + m, n, k, 64, 4)
+    x = bf16_acts(91 + m, m, k)
+    bias = orc.f32_to_bf16(np.linspace(-1, 1, n, dtype=np.float32))
+    rows = np.concatenate([np.random.default_rng(92).choice(n - 8, 120, replace=False), np.arange(n - 8, n)])
+    ref = orc.qmatmul_f64(x, wq[rows], s[rows], b[rows], 64, 4) + orc.bf16_to_f32(bias[rows]).astype(np.float64)
+    y = run(x, wq, s, b, 64, 4, bias=bias)
+    assert rel_err(y[:, rows], ref) <= TIGHT
+    monkeypatch.setenv("MLXQ_QMV_TILE_FUSED_RG", "1")
+    mlxq.reload_overrides()
+    y16 = run(x, wq, s, b, 64, 4, bias=bias)
+    monkeypatch.delenv("MLXQ_QMV_TILE_FUSED_RG")
+    mlxq.reload_overrides()
+    assert rel_err(y16[:, rows], ref) <= TIGHT
