@@ -1264,9 +1264,16 @@ bool qmv_tile_fused_eligible(const QmvFused& f) {
   // 13.5 for the norm kernel and the fused projections; a 128256-row
   // lm_head 379 us)
   if (f.norm_w) return false;
-  int64_t tiles = 0;
-  for (int i = 0; i < f.nproj; i++) tiles += ceil_div(f.proj[i].N, 16);
-  if (tiles * ceil_div(f.M, 16) > 2 * cu_count()) return false;  // one workgroup per CU: at most two rounds
+  int64_t tiles = 0, tiles32 = 0;
+  for (int i = 0; i < f.nproj; i++) {
+    tiles += ceil_div(f.proj[i].N, 16);
+    tiles32 += ceil_div(f.proj[i].N, 32);
+  }
+  // one workgroup per CU: at most two rounds (of 32-row workgroups where
+  // launch_qmv_tile_fused takes them)
+  const bool rg2 = ch / 4 == (f.bits == 4 ? 8 : 16) && overrides().tile_fused_rg != 1;
+  if ((rg2 && tiles * ceil_div(f.M, 16) > cu_count() ? tiles32 : tiles) * ceil_div(f.M, 16) > 2 * cu_count())
+    return false;
   for (int i = 0; i < f.nproj; i++)
     if (f.proj[i].N < 1 || f.proj[i].N > (int64_t(1) << 24)) return false;
   return f.x_stride * f.M < (int64_t(1) << 31) && f.K * f.M < (int64_t(1) << 31);
