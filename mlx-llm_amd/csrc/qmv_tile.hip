@@ -919,6 +919,15 @@ bool stream_preferred(int64_t M, int64_t N, int64_t K, int bits, SCfg& c, int& s
   // (re-measured with every load issued on every path: Q4 M = 32 gate 17.33
   // -> 16.58 on {8, 2, 2}, Q8 M = 16 19.34 -> 18.41 on {4, 4, 1}, Q4 M = 16
   // down 15.94 -> 15.56 on {4, 4, 1} with 4 splits)
+  if (K < N && N >= 65536) {
+    // very tall (an lm_head: 128256 rows, thousands of 64-row tiles): 4-wave
+    // workgroups, several per CU (Q4 M = 4 / 8 / 16 / 32: 85.6 / 91.5 /
+    // 95.6 / 119.8 -> 74.1 / 77.0 / 81.1 / 102.4 us; Q8 M = 4 132.0 -> 115.7,
+    // M = 32 161.3 -> 146.0 on {4, 2, 1})
+    c = bits == 8 && M > 16 ? SCfg{4, 2, 1} : SCfg{4, 4, 1};
+    splits = 1;
+    return true;
+  }
   if (K < N) {
     if (bits == 4) c = M > 16 || M <= 4 ? SCfg{8, 2, 2} : SCfg{8, 4, 2};
     else c = M > 16 ? SCfg{8, 2, 2} : M > 4 ? SCfg{4, 4, 1} : SCfg{8, 4, 2};

@@ -113,3 +113,27 @@ def test_stream_graph_replay_bit_exact(torch_gpu, stream):
         assert torch.equal(y, eager), i
         mlxq.qmatmul(xd, wd, sd, bd, 64, 4)  # eager work on the same workspace in between
         torch.cuda.synchronize()
+
+
+@pytest.fixture(scope="module")
+def tall_layers():
+    """A ragged very tall gate/up-like matrix (65544 rows, an lm_head's
+    shape class) per bit width, quantized once by the oracle."""
+    return {bits: make_layer(0x7A11 + bits, 65544, 4096, 64, bits) for bits in (4, 8)}
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("m", [4, 16, 32])
+def test_stream_default_very_tall(torch_gpu, monkeypatch, tall_layers, bits, m):
+    """Very tall matrices (N >= 65536) stream in 4-wave workgroups under the
+    default dispatch; sampled rows (the ragged last ones included) against
+    the oracle."""
+    for v in ("MLXQ_QMV_TILE_STREAM", "MLXQ_QMV_TILE", "MLXQ_QMV_TILE_ALL"):
+        monkeypatch.delenv(v, raising=False)
+    n, k = 65544, 4096
+    wq, s, b = tall_layers[bits]
+    x = bf16_acts(0x7A12 + m, m, k)
+    y = run(x, wq, s, b, 64, bits)
+    rows = np.concatenate([np.random.default_rng(0x7A13).choice(n - 8, 248, replace=False), np.arange(n - 8, n)])
+    ref = orc.qmatmul_f64(x, wq[rows], s[rows], b[rows], 64, bits)
+    assert rel_err(y[:, rows], ref) <= TIGHT
