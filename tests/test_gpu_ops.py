@@ -113,3 +113,35 @@ def test_qmatmul_add_rms_norm(torch_gpu, bits, m, k, n, with_bias):
         ref += orc.bf16_to_f32(bias)[None, :].astype(np.float64)
     # two bf16 roundings (the projection's output, then the sum): twice the bar
     assert rel_err(orc.bf16_to_f32(host(s_got)), ref) <= 2 * TIGHT
+
+
+def test_qmatmul_add_rms_norm_graph_replay(torch_gpu):
+    """Captured in a HIP graph (split-K sum, add and norm in the second
+    launch), replayed three times with other eager work on the same
+    workspace in between: every replay bit-identical to the eager call."""
+    torch = torch_gpu
+    from test_gpu_qmatmul import make_layer
+    m, k, n = 16, 14336, 4096
+    wq, s, b = make_layer(700, n, k, 64, 4)
+    x = dev(orc.f32_to_bf16(orc.normal(701, m * k, 0.0, 1.0)).reshape(m, k), True)
+    r = dev(orc.f32_to_bf16(orc.normal(702, m * n, 0.0, 1.0)).reshape(m, n), True)
+    w = dev(orc.f32_to_bf16(orc.normal(703, n, 1.0, 0.2)), True)
+    wd, sd, bd = dev(wq), dev(s, True), dev(b, True)
+    s_out = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    y_out = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    mlxq.qmatmul_add_rms_norm(x, wd, sd, bd, r, w, 1e-5, 64, 4, sum_out=s_out, out=y_out)
+    torch.cuda.synchronize()
+    s_eager, y_eager = s_out.clone(), y_out.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        mlxq.qmatmul_add_rms_norm(x, wd, sd, bd, r, w, 1e-5, 64, 4, sum_out=s_out, out=y_out)
+    other = make_layer(704, 4096, 14336, 64, 8)
+    od = (dev(other[0]), dev(other[1], True), dev(other[2], True))
+    for i in range(3):
+        s_out.zero_()
+        y_out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(s_out, s_eager) and torch.equal(y_out, y_eager), i
+        mlxq.qmatmul(x, *od, 64, 8)  # eager work through the same workspace
+        torch.cuda.synchronize()
