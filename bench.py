@@ -1,6 +1,6 @@
 """Benchmark of the quantized-weight hot path on one MI355X.
 
-Step (the timed unit): one pass of BASELINE config 2 -- every Llama-3-8B
+Step (the timed unit): one pass of the benchmark's config 2 -- every Llama-3-8B
 projection of a decoder layer (q, k, v, o, gate, up, down) as a quantized
 matmul at M in {1, 4, 16, 32} activation rows, for Q4 and Q8 (group 64).
 Four distinct layer copies are cycled (Q4 + Q8 weights ~1.4 GB, far above
