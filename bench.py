@@ -448,7 +448,7 @@ def tile_preferred(m, n, k, bits):
     if _short_fullk(m, n, k, bits):
         return True
     if large:
-        return k < n or m >= (8 if bits == 4 else 16)
+        return k < n or m >= (8 if bits == 4 else 9)
     if n <= 2048:
         return m >= 16
     return m > 16
@@ -461,7 +461,7 @@ def stream_splits(m, n, k, bits):
         return 0
     if k < n:
         return 1
-    return 4 if m >= 16 else 0
+    return 4 if m >= 16 or (bits == 8 and m > 8) else 0
 
 
 def row_route(m, n, k, bits):

@@ -939,7 +939,7 @@ bool stream_preferred(int64_t M, int64_t N, int64_t K, int bits, SCfg& c, int& s
     splits = 4;
     return true;
   }
-  if (M == 16) {
+  if (M == 16 || (bits == 8 && M > 8)) {  // Q8 M = 9 / 12 / 15: 20.59 / 23.51 / 24.71 -> 19.56 / 19.79 / 19.76 us
     c = SCfg{4, 4, 1};
     splits = 4;
     return true;
@@ -1053,7 +1053,7 @@ bool qmv_tile_preferred(int64_t M, int64_t N, int64_t K, int bits) {
   const bool large = N * K >= (int64_t(1) << 25);
   if (M <= 4) return large && K < N && M >= (bits == 4 ? 3 : 4);
   if (short_fullk(M, N, K, bits, nullptr)) return true;
-  if (large) return K < N || M >= (bits == 4 ? 8 : 16);  // gate/up-like: the streaming form (Q8 M = 8 20.4 -> 19.0)
+  if (large) return K < N || M >= (bits == 4 ? 8 : 9);  // gate/up-like: the streaming form (Q8 M = 8 20.4 -> 19.0)
   if (N <= 2048) return M >= 16;  // k/v: M = 16 Q4 8.28 -> 7.93 us, Q8 9.27 -> 8.06; Q8 M = 24 11.07 -> 8.93
   return M > 16;  // q/o-like: Q4 M = 20 10.16 -> 9.21 us, Q8 M = 24 11.36 -> 10.42 against the block kernel
 }

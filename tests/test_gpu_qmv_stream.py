@@ -70,7 +70,7 @@ def test_stream_bias_and_outliers(torch_gpu, stream, bits, cfg):
 
 
 @pytest.mark.parametrize("bits", [4, 8])
-@pytest.mark.parametrize("proj,m", [("gate_up", 8), ("gate_up", 16), ("gate_up", 32), ("down", 16), ("down", 32)])
+@pytest.mark.parametrize("proj,m", [("gate_up", 8), ("gate_up", 16), ("gate_up", 32), ("down", 12), ("down", 16), ("down", 32)])
 def test_stream_default_llama(torch_gpu, monkeypatch, bits, proj, m):
     """The shapes the default dispatch streams (no overrides), sampled rows
     against the oracle."""
