@@ -51,6 +51,8 @@ const Overrides* read_overrides() {
   o->qmv_no_tile_fused = flag("MLXQ_QMV_NO_TILE_FUSED");
   if (const char* e = getenv("MLXQ_QMV_TILE")) sscanf(e, "%d,%d,%d", &o->tile_wv, &o->tile_nch, &o->tile_kh);
   if (const char* e = getenv("MLXQ_QMV_TILE_FUSED_RG")) o->tile_fused_rg = atoi(e);
+  o->stream64 = -1;
+  if (const char* e = getenv("MLXQ_QMV_STREAM64")) o->stream64 = atoi(e);
   if (const char* e = getenv("MLXQ_QMV_TILE_STREAM")) {
     o->stream_set = true;
     sscanf(e, "%d,%d,%d,%d", &o->stream_wv, &o->stream_nch, &o->stream_kh, &o->stream_splits);

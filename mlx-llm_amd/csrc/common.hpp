@@ -24,6 +24,7 @@ struct Overrides {
   bool qmv_row_all, qmv_no_row, qmv_mfma, qmv_dot_all, qmv_tile_all, qmv_legacy, qmv_stream, qmv_narrow;
   int tile_wv, tile_nch, tile_kh;  // MLXQ_QMV_TILE=waves,chunks[,K parts]
   int tile_fused_rg;               // MLXQ_QMV_TILE_FUSED_RG=1: 16-row whole-K tiles only
+  int stream64;                    // MLXQ_QMV_STREAM64=1 / 0: force / forbid the 64-row streaming form
   bool tile_mb;                     // MLXQ_QMV_TILE_MB: M blocks of 16 rows
   bool qmv_no_tile_fused;           // MLXQ_QMV_NO_TILE_FUSED
   bool stream_set;                                      // MLXQ_QMV_TILE_STREAM given

@@ -45,6 +45,17 @@ QmvPlan qmv_plan_for(int64_t M, int64_t N, int64_t K, int group_size, int bits) 
 //    56.7 vs 75.2 library; q/o M = 256: 30.8 vs 34.7).
 enum class Route { Fused, Lib, Chunks };
 
+// Short prefills of gate/up-like matrices on the 64-row streaming form: 65..128
+// rows (two row blocks, one round of CUs), measured against the other routes
+// (µs, one box): Q4 M = 96 46.7 -> 34.5, M = 128 48.0 -> 35.2, Q8 M = 128
+// 47.1 -> 41.5; slower at 64 rows and below (two 32-row decode calls) and from
+// 192 (two rounds).  MLXQ_QMV_STREAM64=1 / 0 forces / forbids it.
+bool stream64_route(int64_t M, int64_t N, int64_t K, int group_size, int bits) {
+  const int ov = overrides().stream64;
+  if (ov == 0 || !qmv_stream64_eligible(M, N, K, group_size, bits)) return false;
+  return ov == 1 || (M > 2 * kQmvMaxM && M <= 4 * kQmvMaxM);
+}
+
 Route prefill_route(int64_t M, int64_t N, int64_t K, int bits) {
   const Overrides& ov = overrides();
   if (ov.qmm_fused) return Route::Fused;
@@ -86,6 +97,7 @@ extern "C" int mlxq_qmatmul_workspace_size(int64_t M, int64_t N, int64_t K, int 
   *bytes = fused_workspace_bytes(M, N, K, group_size, bits);
   if (M > kQmvMaxM && prefill_route(M, N, K, bits) == Route::Lib)
     *bytes = std::max(*bytes, qmm_lib_workspace_bytes(N, K));
+  if (M > kQmvMaxM && stream64_route(M, N, K, group_size, bits)) *bytes = 0;  // one launch, no partial sums
   return MLXQ_OK;
 }
 
@@ -117,6 +129,10 @@ int qmatmul_dispatch(const void* x, int64_t M, const uint32_t* wq, const void* s
                           group_size, bits, static_cast<uint16_t*>(y), workspace, workspace_bytes,
                           as_stream(stream));
   if (algo == MLXQ_ALGO_AUTO && M > kQmvMaxM) {
+    if (stream64_route(M, N, K, group_size, bits) && x && wq && scales && biases && y)
+      return launch_qmv_stream64(static_cast<const uint16_t*>(x), M, wq, static_cast<const uint16_t*>(scales),
+                                 static_cast<const uint16_t*>(biases), static_cast<const uint16_t*>(bias_vec), N, K,
+                                 group_size, bits, static_cast<uint16_t*>(y), as_stream(stream));
     const Route r = prefill_route(M, N, K, bits);
     if (r == Route::Lib && allow_lib && workspace && workspace_bytes >= qmm_lib_workspace_bytes(N, K)) {
       rc = launch_qmm_lib(static_cast<const uint16_t*>(x), M, wq, static_cast<const uint16_t*>(scales),

@@ -1044,6 +1044,39 @@ bool qmv_tile_eligible(int64_t M, int64_t N, int64_t K, int group_size, int bits
 
 size_t qmv_tile_workspace_bytes(int64_t M, int64_t N) { return static_cast<size_t>(kMaxSplits) * M * N * 4; }
 
+// Short prefills of gate/up-like matrices (33..256 rows): the streaming form
+// with 64 activation rows per workgroup (4 MFMA row tiles x 8 row groups of
+// one K part, slices of 256 k), grid z = blocks of 64 rows; one launch, no
+// K split.
+bool qmv_stream64_eligible(int64_t M, int64_t N, int64_t K, int group_size, int bits) {
+  if (M <= kQmvMaxM || M > 256 || group_size != 64 || (bits != 4 && bits != 8)) return false;
+  if (K >= N || N * K < (int64_t(1) << 25) || K % 256 || N > (int64_t(1) << 24) || M * K >= (int64_t(1) << 31))
+    return false;
+  return true;
+}
+
+int launch_qmv_stream64(const uint16_t* x, int64_t M, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
+                        const uint16_t* bias, int64_t N, int64_t K, int group_size, int bits, uint16_t* y,
+                        hipStream_t st) {
+  if (!qmv_stream64_eligible(M, N, K, group_size, bits))
+    return fail(MLXQ_ERR_UNSUPPORTED, "qmv_stream64: shape not supported");
+  TileParams a{};
+  a.x = x;
+  a.wq = wq;
+  a.s = s;
+  a.b = b;
+  a.bias = bias;
+  a.y = y;
+  a.M = static_cast<int>(M);
+  a.N = static_cast<int>(N);
+  a.K = static_cast<int>(K);
+  a.splits = 1;
+  a.steps = static_cast<int>(K / 256);
+  const int tiles = static_cast<int>(ceil_div(N, 16 * 8));
+  const int mb = static_cast<int>(ceil_div(M, 64));
+  return bits == 4 ? run_stream<4, 4, 8, 2, 1>(a, tiles, mb, st) : run_stream<8, 4, 8, 4, 1>(a, tiles, mb, st);
+}
+
 bool qmv_tile_preferred(int64_t M, int64_t N, int64_t K, int bits) {
   // Measured against the block kernel (qmv.hip) and the vector-ALU kernel
   // (qmv_dot) at the Llama-3-8B projection shapes: the tile kernel wins on

@@ -137,3 +137,30 @@ def test_stream_default_very_tall(torch_gpu, monkeypatch, tall_layers, bits, m):
     rows = np.concatenate([np.random.default_rng(0x7A13).choice(n - 8, 248, replace=False), np.arange(n - 8, n)])
     ref = orc.qmatmul_f64(x, wq[rows], s[rows], b[rows], 64, bits)
     assert rel_err(y[:, rows], ref) <= TIGHT
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("m,force", [(65, False), (96, False), (128, False), (33, True), (200, True)])
+def test_stream64_short_prefill(torch_gpu, monkeypatch, bits, m, force):
+    """Short prefills of gate/up-like matrices on the 64-row streaming form
+    (grid z = blocks of 64 activation rows, ragged last block): taken by
+    default at 65..128 rows (no workspace), forced outside that range with
+    MLXQ_QMV_STREAM64=1; sampled rows with a bias against the oracle."""
+    import mlxq
+    for v in ("MLXQ_QMV_TILE_STREAM", "MLXQ_QMV_TILE", "MLXQ_QMV_TILE_ALL", "MLXQ_QMV_STREAM64"):
+        monkeypatch.delenv(v, raising=False)
+    if force:
+        monkeypatch.setenv("MLXQ_QMV_STREAM64", "1")
+    mlxq.reload_overrides()
+    k, n = 4096, 14336
+    if not force:
+        assert mlxq.workspace_size(m, n, k, 64, bits) == 0
+    wq, s, b = make_layer(0x6400 + bits, n, k, 64, bits)
+    x = bf16_acts(0x6401 + m, m, k)
+    bias = orc.f32_to_bf16(np.linspace(-1, 1, n, dtype=np.float32))
+    y = run(x, wq, s, b, 64, bits, bias=bias)
+    rows = np.concatenate([np.random.default_rng(0x6402).choice(n - 8, 120, replace=False), np.arange(n - 8, n)])
+    ref = orc.qmatmul_f64(x, wq[rows], s[rows], b[rows], 64, bits) + orc.bf16_to_f32(bias[rows]).astype(np.float64)
+    assert rel_err(y[:, rows], ref) <= TIGHT
+    monkeypatch.delenv("MLXQ_QMV_STREAM64", raising=False)
+    mlxq.reload_overrides()
