@@ -53,7 +53,9 @@ enum class Route { Fused, Lib, Chunks };
 bool stream64_route(int64_t M, int64_t N, int64_t K, int group_size, int bits) {
   const int ov = overrides().stream64;
   if (ov == 0 || !qmv_stream64_eligible(M, N, K, group_size, bits)) return false;
-  return ov == 1 || (M > 2 * kQmvMaxM && M <= 4 * kQmvMaxM);
+  // default: gate/up-like only (down-like ones at 65..128 rows, with four K
+  // splits, measured slower than the library route: Q4 M = 128 41.4 vs 37.1)
+  return ov == 1 || (K < N && M > 2 * kQmvMaxM && M <= 4 * kQmvMaxM);
 }
 
 Route prefill_route(int64_t M, int64_t N, int64_t K, int bits) {
@@ -97,7 +99,7 @@ extern "C" int mlxq_qmatmul_workspace_size(int64_t M, int64_t N, int64_t K, int 
   *bytes = fused_workspace_bytes(M, N, K, group_size, bits);
   if (M > kQmvMaxM && prefill_route(M, N, K, bits) == Route::Lib)
     *bytes = std::max(*bytes, qmm_lib_workspace_bytes(N, K));
-  if (M > kQmvMaxM && stream64_route(M, N, K, group_size, bits)) *bytes = 0;  // one launch, no partial sums
+  if (M > kQmvMaxM && stream64_route(M, N, K, group_size, bits)) *bytes = qmv_stream64_workspace_bytes(M, N, K);
   return MLXQ_OK;
 }
 
@@ -129,10 +131,14 @@ int qmatmul_dispatch(const void* x, int64_t M, const uint32_t* wq, const void* s
                           group_size, bits, static_cast<uint16_t*>(y), workspace, workspace_bytes,
                           as_stream(stream));
   if (algo == MLXQ_ALGO_AUTO && M > kQmvMaxM) {
-    if (stream64_route(M, N, K, group_size, bits) && x && wq && scales && biases && y)
-      return launch_qmv_stream64(static_cast<const uint16_t*>(x), M, wq, static_cast<const uint16_t*>(scales),
-                                 static_cast<const uint16_t*>(biases), static_cast<const uint16_t*>(bias_vec), N, K,
-                                 group_size, bits, static_cast<uint16_t*>(y), as_stream(stream));
+    if (stream64_route(M, N, K, group_size, bits) && x && wq && scales && biases && y) {
+      rc = launch_qmv_stream64(static_cast<const uint16_t*>(x), M, wq, static_cast<const uint16_t*>(scales),
+                               static_cast<const uint16_t*>(biases), static_cast<const uint16_t*>(bias_vec), N, K,
+                               group_size, bits, static_cast<uint16_t*>(y), workspace, workspace_bytes,
+                               as_stream(stream));
+      if (rc != MLXQ_ERR_UNSUPPORTED) return rc;  // else (workspace too small for the K split): the other routes
+      clear_error();
+    }
     const Route r = prefill_route(M, N, K, bits);
     if (r == Route::Lib && allow_lib && workspace && workspace_bytes >= qmm_lib_workspace_bytes(N, K)) {
       rc = launch_qmm_lib(static_cast<const uint16_t*>(x), M, wq, static_cast<const uint16_t*>(scales),

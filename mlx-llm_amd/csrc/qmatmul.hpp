@@ -91,12 +91,13 @@ int launch_qmv_tile_swiglu(const QmvFused& f, hipStream_t st);
 size_t qmv_tile_workspace_bytes(int64_t M, int64_t N);
 bool qmv_tile_preferred(int64_t M, int64_t N, int64_t K, int bits);
 bool qmv_dot_preferred(int64_t M, int64_t N, int64_t K, int bits);  // M <= 4: vector-ALU kernel
-// Short prefills (33..256 rows) of gate/up-like matrices on the streaming
-// form with 64 activation rows per workgroup.
+// Short prefills (33..256 rows) of large matrices on the streaming form with
+// 64 activation rows per workgroup (down-like ones with four K splits).
 bool qmv_stream64_eligible(int64_t M, int64_t N, int64_t K, int group_size, int bits);
+size_t qmv_stream64_workspace_bytes(int64_t M, int64_t N, int64_t K);
 int launch_qmv_stream64(const uint16_t* x, int64_t M, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
                         const uint16_t* bias, int64_t N, int64_t K, int group_size, int bits, uint16_t* y,
-                        hipStream_t st);
+                        void* workspace, size_t workspace_bytes, hipStream_t st);
 
 // The decode chain's down projection with the residual add and the next
 // RMSNorm in the second kernel of a split-K launch: instead of y, sum_out =

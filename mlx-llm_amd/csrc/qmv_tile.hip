@@ -1048,18 +1048,34 @@ size_t qmv_tile_workspace_bytes(int64_t M, int64_t N) { return static_cast<size_
 // with 64 activation rows per workgroup (4 MFMA row tiles x 8 row groups of
 // one K part, slices of 256 k), grid z = blocks of 64 rows; one launch, no
 // K split.
+// Down-like matrices (K > N) split K in four (f32 partial sums in the
+// workspace, added by the second launch) so that their fewer row tiles fill
+// the CUs.
+int qmv_stream64_splits(int64_t N, int64_t K) { return K > N ? 4 : 1; }
+
 bool qmv_stream64_eligible(int64_t M, int64_t N, int64_t K, int group_size, int bits) {
   if (M <= kQmvMaxM || M > 256 || group_size != 64 || (bits != 4 && bits != 8)) return false;
-  if (K >= N || N * K < (int64_t(1) << 25) || K % 256 || N > (int64_t(1) << 24) || M * K >= (int64_t(1) << 31))
+  const int splits = qmv_stream64_splits(N, K);
+  if (N * K < (int64_t(1) << 25) || K % (256 * splits) || N > (int64_t(1) << 24) || M * K >= (int64_t(1) << 31) ||
+      (splits > 1 && N % 4))
     return false;
   return true;
 }
 
+size_t qmv_stream64_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  const int splits = qmv_stream64_splits(N, K);
+  return splits > 1 ? static_cast<size_t>(splits) * M * N * 4 : 0;
+}
+
 int launch_qmv_stream64(const uint16_t* x, int64_t M, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
                         const uint16_t* bias, int64_t N, int64_t K, int group_size, int bits, uint16_t* y,
-                        hipStream_t st) {
+                        void* workspace, size_t workspace_bytes, hipStream_t st) {
   if (!qmv_stream64_eligible(M, N, K, group_size, bits))
     return fail(MLXQ_ERR_UNSUPPORTED, "qmv_stream64: shape not supported");
+  const int splits = qmv_stream64_splits(N, K);
+  const size_t need = qmv_stream64_workspace_bytes(M, N, K);
+  if (need && (!workspace || workspace_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 255u)))
+    return fail(MLXQ_ERR_UNSUPPORTED, "qmv_stream64: workspace too small for the K split");
   TileParams a{};
   a.x = x;
   a.wq = wq;
@@ -1070,11 +1086,14 @@ int launch_qmv_stream64(const uint16_t* x, int64_t M, const uint32_t* wq, const 
   a.M = static_cast<int>(M);
   a.N = static_cast<int>(N);
   a.K = static_cast<int>(K);
-  a.splits = 1;
-  a.steps = static_cast<int>(K / 256);
+  a.splits = splits;
+  a.steps = static_cast<int>(K / 256 / splits);
+  a.part = splits > 1 ? static_cast<float*>(workspace) : nullptr;
   const int tiles = static_cast<int>(ceil_div(N, 16 * 8));
   const int mb = static_cast<int>(ceil_div(M, 64));
-  return bits == 4 ? run_stream<4, 4, 8, 2, 1>(a, tiles, mb, st) : run_stream<8, 4, 8, 4, 1>(a, tiles, mb, st);
+  const int rc = bits == 4 ? run_stream<4, 4, 8, 2, 1>(a, tiles, mb, st) : run_stream<8, 4, 8, 4, 1>(a, tiles, mb, st);
+  if (rc || splits == 1) return rc;
+  return launch_split_reduce(a.part, bias, y, M, N, splits, st);
 }
 
 bool qmv_tile_preferred(int64_t M, int64_t N, int64_t K, int bits) {

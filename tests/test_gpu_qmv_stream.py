@@ -164,3 +164,24 @@ def test_stream64_short_prefill(torch_gpu, monkeypatch, bits, m, force):
     assert rel_err(y[:, rows], ref) <= TIGHT
     monkeypatch.delenv("MLXQ_QMV_STREAM64", raising=False)
     mlxq.reload_overrides()
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("m", [40, 100])
+def test_stream64_down_like_forced(torch_gpu, monkeypatch, bits, m):
+    """The 64-row streaming form on a down-like matrix (four K splits through
+    the workspace, then the reduction launch), forced with
+    MLXQ_QMV_STREAM64=1 (not the default there); against the oracle."""
+    import mlxq
+    monkeypatch.setenv("MLXQ_QMV_STREAM64", "1")
+    mlxq.reload_overrides()
+    k, n = 14336, 4096
+    assert mlxq.workspace_size(m, n, k, 64, bits) == 4 * m * n * 4
+    wq, s, b = make_layer(0x6410 + bits, n, k, 64, bits)
+    x = bf16_acts(0x6411 + m, m, k)
+    y = run(x, wq, s, b, 64, bits)
+    rows = np.random.default_rng(0x6412).choice(n, 128, replace=False)
+    assert rel_err(y[:, rows], orc.qmatmul_f64(x, wq[rows], s[rows], b[rows], 64, bits)) <= TIGHT
+    monkeypatch.delenv("MLXQ_QMV_STREAM64")
+    mlxq.reload_overrides()
+
