@@ -700,17 +700,32 @@ __global__ __launch_bounds__(256) void qmv_tile_reduce_kernel(const float* __res
 }
 
 // The same sum, four consecutive outputs per thread (N % 4 == 0, y 8-byte
-// aligned): 16-byte partial loads, one 8-byte store.
+// aligned): 16-byte partial loads, one 8-byte store.  S > 0: the split count
+// at compile time, every partial load issued before the first add (one
+// memory round trip instead of one per split); S = 0: any count.
+template <int S>
 __global__ __launch_bounds__(256) void split_reduce4_kernel(const float4* __restrict__ part,
                                                             const uint16_t* __restrict__ bias,
                                                             uint2* __restrict__ y, int64_t MN4, int N,
                                                             int splits) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (i >= MN4) return;
-  float4 sum = part[i];
-  for (int sp = 1; sp < splits; sp++) {
-    const float4 v = part[sp * MN4 + i];
-    sum.x += v.x; sum.y += v.y; sum.z += v.z; sum.w += v.w;
+  float4 sum;
+  if constexpr (S > 0) {
+    float4 v[S];
+#pragma unroll
+    for (int sp = 0; sp < S; sp++) v[sp] = part[sp * MN4 + i];
+    sum = v[0];
+#pragma unroll
+    for (int sp = 1; sp < S; sp++) {
+      sum.x += v[sp].x; sum.y += v[sp].y; sum.z += v[sp].z; sum.w += v[sp].w;
+    }
+  } else {
+    sum = part[i];
+    for (int sp = 1; sp < splits; sp++) {
+      const float4 v = part[sp * MN4 + i];
+      sum.x += v.x; sum.y += v.y; sum.z += v.z; sum.w += v.w;
+    }
   }
   if (bias) {
     const int n = static_cast<int>((4 * i) % N);
@@ -830,8 +845,12 @@ int launch_split_reduce(const float* part, const uint16_t* bias, uint16_t* y, in
   const int64_t mn = M * N;
   if (N % 4 == 0 && (reinterpret_cast<uintptr_t>(y) & 7u) == 0) {
     const int64_t mn4 = mn / 4;
-    hipLaunchKernelGGL(tile::split_reduce4_kernel, dim3(static_cast<unsigned>(ceil_div(mn4, 256))), dim3(256), 0,
-                       st, reinterpret_cast<const float4*>(part), bias, reinterpret_cast<uint2*>(y), mn4,
+    auto kern = splits == 2 ? tile::split_reduce4_kernel<2>
+                : splits == 4 ? tile::split_reduce4_kernel<4>
+                : splits == 8 ? tile::split_reduce4_kernel<8>
+                              : tile::split_reduce4_kernel<0>;
+    hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(ceil_div(mn4, 256))), dim3(256), 0, st,
+                       reinterpret_cast<const float4*>(part), bias, reinterpret_cast<uint2*>(y), mn4,
                        static_cast<int>(N), splits);
   } else {
     hipLaunchKernelGGL(tile::qmv_tile_reduce_kernel, dim3(static_cast<unsigned>(ceil_div(mn, 256))), dim3(256), 0,
