@@ -34,7 +34,7 @@ HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, published
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, published
 METRIC = "Q4/Q8 qmatmul GB/s & TFLOP/s (% roofline), Llama-3-8B proj shapes, 1 GPU"
 # measured HBM traffic per launch (bytes) of a dominant-kernel candidate, keyed (bits, M, K, N)
-TRAFFIC_BYTES = {(8, 32, 4096, 14336): 65_787_730}
+TRAFFIC_BYTES = {(8, 32, 4096, 14336): 65_808_266}
 # measured HBM traffic per call of the Q4 g64 M=1 GEMV, by projection shape
 # (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated; profiles/qmv_q4_m1_traffic.md)
 HEADLINE_TRAFFIC = {"q": 9_584_354, "k": 2_482_332, "v": 2_482_332, "o": 9_584_354, "gate": 33_209_997,
