@@ -84,7 +84,9 @@ def build(jobs: int = 8, verbose: bool = False) -> Path:
     # a kernel whose host-side stub the compiler dropped (it can, silently,
     # for some builtins in template kernels) would only fail at load time
     nm = subprocess.run(["nm", "-u", str(tmp)], capture_output=True, text=True)
-    missing = [ln.split()[-1] for ln in nm.stdout.splitlines() if "__device_stub__" in ln]
+    # (or the kernel symbol itself, when the host pass found the kernel body
+    # invalid: any undefined symbol of the library's own namespace)
+    missing = [ln.split()[-1] for ln in nm.stdout.splitlines() if "__device_stub__" in ln or "_ZN4mlxq" in ln]
     if missing:
         raise RuntimeError("kernel stubs missing from the library:\n" + "\n".join(missing[:10]))
     os.replace(tmp, LIB)

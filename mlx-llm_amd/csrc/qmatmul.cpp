@@ -31,18 +31,16 @@ QmvPlan qmv_plan_for(int64_t M, int64_t N, int64_t K, int group_size, int bits) 
 }
 
 // The kernel route of a call with more than 32 activation rows
-// (MLXQ_ALGO_AUTO), from graph-timed A/B runs at the Llama-3-8B shapes
-// (warm clocks; µs, Q4, fused kernel / library GEMM / 32-row decode chunks):
-//  * up to 64 rows: the batched-decode kernels over 32-row chunks (M = 64:
-//    gate 51.7 / 52.4 / 2 x 17.5, q/o 26.6 / 29.6 / 2 x 9.3, k/v 25.5 / 27.1
-//    / 2 x 6.5; down 37.8 / 62.8 / 2 x 19.6);
-//  * the library GEMM on the dequantized weight (qmm_lib.hip): gate/up-like
-//    (K < N) from M = 512 (90.8 -> 81.1; M = 2048 253 -> 190, 942 -> 1267
-//    TFLOP/s), square (q/o) from 1024 (62.3 -> 49.7), down-like from 1024 (Q4:
-//    141.8 -> 137.2) / 2048 (Q8; Q4 M = 2048 253 -> 210) and short matrices
-//    with K > N (k/v) from 2048 (42.3 -> 36.6);
-//  * the fused LDS-dequant kernel (qmm.hip) otherwise (e.g. down M = 256:
-//    56.7 vs 75.2 library; q/o M = 256: 30.8 vs 34.7).
+// (MLXQ_ALGO_AUTO), from graph-timed A/B runs of every route at the
+// Llama-3-8B shapes, M = 64 .. 4096, Q4 and Q8 (µs, Q4: qmm / library GEMM):
+//  * up to 64 rows: the batched-decode kernels over 32-row chunks;
+//  * the hand-written qmm kernel (qmm.hip) up to 2048 rows on down-like
+//    matrices (K > N: down M = 2048 206 / 217, M = 1024 123 / 142), up to
+//    512 rows on gate/up-like ones (K < N: M = 512 62 / 80) and up to 512
+//    rows on square ones;
+//  * the library GEMM on the dequantized weight (qmm_lib.hip) above that
+//    (gate/up M = 1024 128 / 114, M = 2048 219 / 197; q/o M = 1024 50 / 46;
+//    every shape at M = 4096, e.g. down 360 / 325).
 enum class Route { Fused, Lib, Chunks };
 
 // Short prefills of gate/up-like matrices on the 64-row streaming form: 65..128
@@ -58,14 +56,13 @@ bool stream64_route(int64_t M, int64_t N, int64_t K, int group_size, int bits) {
   return ov == 1 || (K < N && M > 2 * kQmvMaxM && M <= 4 * kQmvMaxM);
 }
 
-Route prefill_route(int64_t M, int64_t N, int64_t K, int bits) {
+Route prefill_route(int64_t M, int64_t N, int64_t K, int group_size) {
   const Overrides& ov = overrides();
   if (ov.qmm_fused) return Route::Fused;
   if (ov.qmm_lib) return Route::Lib;
   if (N <= 16384 && M <= 2 * kQmvMaxM) return Route::Chunks;
-  const bool large = N * K >= (int64_t(1) << 25);
-  if (K < N) return M >= 512 ? Route::Lib : Route::Fused;
-  if (K > N) return M >= (large && bits == 4 ? 1024 : 2048) ? Route::Lib : Route::Fused;
+  if (!qmm_eligible(K, group_size)) return Route::Lib;
+  if (K > N) return M >= 4096 ? Route::Lib : Route::Fused;
   return M >= 1024 ? Route::Lib : Route::Fused;
 }
 
@@ -78,8 +75,8 @@ size_t fused_workspace_bytes(int64_t M, int64_t N, int64_t K, int group_size, in
   if (mq >= 2 && qmv_tile_eligible(mq, N, K, group_size, bits))
     bytes = qmv_tile_workspace_bytes(mq, N);  // split-K partials (the M = 1 decode kernel needs none)
   if (M > kQmvMaxM) {
-    const size_t qmm = K % 64 == 0 ? qmm_workspace_bytes(M, N, K) : 0;
-    bytes = prefill_route(M, N, K, bits) == Route::Chunks ? std::max(bytes, qmm) : qmm;
+    const size_t qmm = qmm_eligible(K, group_size) ? qmm_workspace_bytes(M, N, K, group_size) : 0;
+    bytes = prefill_route(M, N, K, group_size) == Route::Chunks ? std::max(bytes, qmm) : qmm;
   }
   return bytes;
 }
@@ -97,7 +94,7 @@ extern "C" int mlxq_qmatmul_workspace_size(int64_t M, int64_t N, int64_t K, int 
   if (rc) return rc;
   if (!bytes) return fail(MLXQ_ERR_INVALID, "qmatmul: null output pointer");
   *bytes = fused_workspace_bytes(M, N, K, group_size, bits);
-  if (M > kQmvMaxM && prefill_route(M, N, K, bits) == Route::Lib)
+  if (M > kQmvMaxM && prefill_route(M, N, K, group_size) == Route::Lib)
     *bytes = std::max(*bytes, qmm_lib_workspace_bytes(N, K));
   if (M > kQmvMaxM && stream64_route(M, N, K, group_size, bits)) *bytes = qmv_stream64_workspace_bytes(M, N, K);
   return MLXQ_OK;
@@ -139,7 +136,7 @@ int qmatmul_dispatch(const void* x, int64_t M, const uint32_t* wq, const void* s
       if (rc != MLXQ_ERR_UNSUPPORTED) return rc;  // else (workspace too small for the K split): the other routes
       clear_error();
     }
-    const Route r = prefill_route(M, N, K, bits);
+    const Route r = prefill_route(M, N, K, group_size);
     if (r == Route::Lib && allow_lib && workspace && workspace_bytes >= qmm_lib_workspace_bytes(N, K)) {
       rc = launch_qmm_lib(static_cast<const uint16_t*>(x), M, wq, static_cast<const uint16_t*>(scales),
                           static_cast<const uint16_t*>(biases), static_cast<const uint16_t*>(bias_vec), N, K,
@@ -160,7 +157,7 @@ int qmatmul_dispatch(const void* x, int64_t M, const uint32_t* wq, const void* s
     }
   }
   if (algo == MLXQ_ALGO_AUTO) algo = M <= kQmvMaxM ? MLXQ_ALGO_QMV : MLXQ_ALGO_QMM;
-  if (algo == MLXQ_ALGO_QMM && K % 64) algo = MLXQ_ALGO_QMV;  // qmm steps K by 64
+  if (algo == MLXQ_ALGO_QMM && !qmm_eligible(K, group_size)) algo = MLXQ_ALGO_QMV;  // 32-row chunks
 
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   const uint16_t* sp = static_cast<const uint16_t*>(scales);

@@ -122,13 +122,14 @@ int launch_split_add_norm(const float* part, const uint16_t* bias, int64_t M, in
 int launch_split_reduce(const float* part, const uint16_t* bias, uint16_t* y, int64_t M, int64_t N, int splits,
                         hipStream_t st);
 
-// qmm: LDS-dequant bf16 MFMA GEMM, any M, K % 64 == 0.  Shapes whose
-// 256 x 256 tiles leave most CUs idle split K (qmm_split_k slices, f32
-// partials in the workspace); without a large enough workspace the call
-// runs unsplit.
+// qmm: the prefill GEMM (bf16 MFMA on weights dequantized in registers),
+// any M; K % 512 == 0 and K % (8 * group_size) == 0 (qmm_eligible).  Shapes
+// whose tiles leave most CUs idle split K (qmm_split_k slices, f32 partials
+// in the workspace); without a workspace large enough the call runs unsplit.
 constexpr int kQmmMaxSplits = 8;
-int qmm_split_k(int64_t M, int64_t N, int64_t K);
-size_t qmm_workspace_bytes(int64_t M, int64_t N, int64_t K);
+bool qmm_eligible(int64_t K, int group_size);
+int qmm_split_k(int64_t M, int64_t N, int64_t K, int group_size);
+size_t qmm_workspace_bytes(int64_t M, int64_t N, int64_t K, int group_size);
 // prefill as dequantize into the workspace + hipBLASLt bf16 GEMM (qmm_lib.hip)
 size_t qmm_lib_workspace_bytes(int64_t N, int64_t K);
 int launch_qmm_lib(const uint16_t* x, int64_t M, const uint32_t* wq, const uint16_t* s, const uint16_t* b,

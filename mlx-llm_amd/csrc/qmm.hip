@@ -1,31 +1,46 @@
 // Prefill-shaped quantized matmul (qmm) for gfx950: y[M,N] = x[M,K] . W^T,
-// W group-wise affine quantized (Q4 / Q8), any M.
+// W group-wise affine quantized (Q4 / Q8), any M; K a multiple of 512 and
+// of 8 groups.
 //
 // Reference: QuantizedLinear::forward (src/primitives/quant.rs:56-70) ->
 // mlx_rs::ops::quantized_matmul, which MLX serves with its qmm kernels when M
 // is large (prefill, batched decode).
 //
-// Design (MFMA-bound):
-//  * Workgroup tile BM x BN, K step 64, WM x WN wavefronts each owning
-//    (BM/WM) x (BN/WN) of the output as tiles of v_mfma_f32_32x32x16_bf16
-//    with f32 accumulators.  256 x 256 tiles of 8 wavefronts (2 per SIMD) or
-//    128 x 128 tiles of 4 (two workgroups per CU), chosen from the grid size.
-//  * One or two threads own each weight row of the tile per K step: they load
-//    the row's 64 codes and scale/bias, dequantize them once for the whole
-//    workgroup (codes -> f32 -> scale*q + bias -> bf16, round to nearest
-//    even: the values MLX's qmm places in threadgroup memory) and write them
-//    to LDS.  Activations are copied to LDS as they are.
-//  * Latency: two LDS stages and two register stages.  The global loads of
-//    K step k+2 are issued before the MFMAs of step k; step k+1, already in
-//    registers, is written to the other LDS stage after them; one barrier per
-//    step.  Rows are padded to 72 bf16 so the 16-byte fragment reads of 16
-//    consecutive rows hit distinct banks.
+// Design (MFMA-bound at prefill sizes):
+//  * Workgroup tile BM x 256 (BM = 256 or 128), four waves side by side
+//    along N; each wave owns BM x 64 of the output as (BM/32) x 2 tiles of
+//    v_mfma_f32_32x32x16_bf16 with f32 accumulators (up to 256 per lane, in
+//    the accumulator registers).  K advances 64 per step.
+//  * Everything arrives by LDS DMA (global_load_lds_dwordx4: no VGPRs, no
+//    VALU), in whole 128-byte lines: the memory path pays per line touched,
+//    so a 32-byte slice of a code row costs as much as a full line.
+//      - activations: the BM x 64 bf16 tile of one step (one line per row),
+//        two stages, requested one step ahead;
+//      - codes: 128 bytes of each of the 256 weight rows (4 steps at Q4, 2
+//        at Q8), two buffers;
+//      - scales and biases: 16 bytes per row and array (8 steps of groups),
+//        two buffers.
+//    Rows are stored with their 16-byte chunks permuted (chunk c of row r at
+//    c ^ swz(r)), which makes the 16-byte fragment reads bank-conflict free.
+//  * Weights are dequantized straight into the MFMA B-operand layout in
+//    registers, by the wave that multiplies them: lane (n, h) of a 32-column
+//    tile takes the 32 codes k0 + 32h .. +32 of weight row n (one 16-byte LDS
+//    read at Q4), and for sub-step j the 8 codes 32h + 8j .. +8 become its
+//    bf16x8 operand (bf16(s * q + b): f32 FMA, round to nearest even).  The
+//    activation fragment of sub-step j is the 16-byte chunk 4h + j of the
+//    row: both operands follow the same k order, which the MFMA sums over.
+//    No weight tile is written to LDS.
+//  * Step k's MFMAs use the operands decoded during step k-1: the wave
+//    alternates one MFMA (32 cycles on the matrix core) with a few decode
+//    instructions and LDS reads, in a fixed per-step schedule.
+//  * Tiles are ordered so that each XCD (workgroups round-robin over the 8
+//    XCDs) takes a contiguous, M-major run of tiles: the workgroups of one
+//    XCD share activation rows in that XCD's L2.
 #include <hip/hip_runtime.h>
 
-#include <stdlib.h>
-
+#include <algorithm>
 #include <string>
-#include <type_traits>
+#include <utility>
 
 #include "common.hpp"
 #include "qmatmul.hpp"
@@ -34,370 +49,443 @@ namespace mlxq {
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int BK = 64;
-constexpr int LDR = BK + 8;  // padded LDS row, bf16 elements
+constexpr int BK = 64;      // K per step
+constexpr int PERIOD = 8;   // steps per unrolled period (one scale batch)
 
-// Tile BM x BN, WM x WN wavefronts (each (BM/WM) x (BN/WN) of the output)
-// in MF x MF MFMA tiles (32: v_mfma_f32_32x32x16_bf16, 16:
-// v_mfma_f32_16x16x32_bf16).
-template <int BM, int BN, int WM, int WN, int BITS, int MF>
+template <int BITS, int GS, int TM, int TN>
 struct QmmGeom {
-  static constexpr int THREADS = 64 * WM * WN;
-  static constexpr int PARTS = THREADS >= 2 * BN ? 2 : 1;  // threads per weight row
-  // rows the weight loader covers: BN, or more when BN does not divide the
-  // threads (the extra rows repeat clamped weights into spare LDS rows, so
-  // no thread branches around its loads)
-  static constexpr int LROWS = THREADS / PARTS;
-  static constexpr int STAGE = (BM + LROWS) * LDR;         // bf16 per LDS stage
-  static constexpr int LDS_BYTES = 2 * STAGE * 2;          // two stages
-  static constexpr int TM = BM / WM / MF;                  // MFMA row tiles per wave
-  static constexpr int TN = BN / WN / MF;                  // MFMA column tiles per wave
-  static constexpr int NV = MF * MF / 64;                  // accumulator floats per lane per tile
-  static constexpr int KS = 512 / MF;                      // k per MFMA
-  static constexpr int AU4 = BM * 8 / THREADS;             // activation uint4 per thread per step
-  static constexpr int CPT = BK / PARTS;                   // codes per thread per step
-  static constexpr int BU4 = CPT * BITS / 128;             // code uint4 per thread per step
-  static_assert(MF == 16 || MF == 32, "MFMA shape");
-  static_assert(LROWS >= BN && THREADS % PARTS == 0, "weight rows map onto threads");
-  static_assert((BM / WM) % MF == 0 && (BN / WN) % MF == 0, "wave tiles are whole MFMA tiles");
-  static_assert(BM * 8 % THREADS == 0, "activation chunks map onto threads");
-  static_assert(LDS_BYTES <= 160 * 1024, "two stages fit in LDS");
+  static constexpr int WAVES = 4, THREADS = 64 * WAVES;
+  static constexpr int BN = 256;               // weight rows per workgroup
+  static constexpr int WN = BN / (32 * TN);    // waves along N (each TN 32-column tiles)
+  static constexpr int WM = WAVES / WN;        // waves along M (each TM 32-row tiles)
+  static constexpr int BM = WM * TM * 32;
+  static constexpr int A_BYTES = BM * BK * 2;  // activation tile of one step
+  static constexpr int CROW = BK * BITS / 8;   // code bytes per weight row per step
+  static constexpr int CB = 128 / CROW;        // steps per code batch (one 128-byte line per row)
+  static constexpr int C_BYTES = BN * 128;
+  static constexpr int SROW = GS == 32 ? 32 : 16;  // scale bytes per row per batch (and bias bytes)
+  static constexpr int S_BYTES = BN * 2 * SROW;
+  static constexpr int A_OFF = 0, C_OFF = 2 * A_BYTES, S_OFF = C_OFF + 2 * C_BYTES;
+  static constexpr int LDS_BYTES = S_OFF + 2 * S_BYTES;
+  // DMA instructions per wave: activations per step, codes / scales per batch
+  static constexpr int A_DMA = A_BYTES / 1024 / WAVES;
+  static constexpr int C_DMA = C_BYTES / 1024 / WAVES;
+  static constexpr int S_DMA = S_BYTES / 1024 / WAVES;
+  static constexpr int CW = BITS == 4 ? 1 : 2;  // 16-byte code reads per lane per tile per step
+  static_assert(A_BYTES % (1024 * WAVES) == 0 && C_BYTES % (1024 * WAVES) == 0 && S_BYTES % (1024 * WAVES) == 0,
+                "whole DMA chunks");
+  static_assert(PERIOD % CB == 0, "code batches tile the period");
+  static_assert(WM * WN == WAVES && TM % 2 == 0 && TN % 2 == 0, "wave grid");
+  static_assert(4 * TM * TN >= 3 * TM * TN + 2 + A_DMA && 4 * TM * TN >= C_DMA + S_DMA, "DMA slots");
+  static_assert(LDS_BYTES <= 160 * 1024, "fits in LDS");
+  static_assert(CB >= 2, "a code batch is needed two boundaries after its request");
+  // DMA instructions a boundary issues after its activations: codes when a
+  // batch starts two steps later, scales at boundary 6 of the period
+  static constexpr int after(int b) { return ((b + 2) % CB == 0 ? C_DMA : 0) + (b == PERIOD - 2 ? S_DMA : 0); }
 };
 
+// LDS DMA of 16 bytes per lane (global_load_lds_dwordx4): lane l's bytes
+// land at lds + 16 l.  Written out rather than through the compiler's
+// builtin: the builtin only emits the 64-bit per-lane address form, while
+// the SGPR-base form (wave-uniform base + 32-bit per-lane offset) carries
+// half the per-lane address data, which the issuing wave pays for.  Every
+// LDS DMA of this kernel goes through these two functions, so M0 (the LDS
+// destination) is only ever written here, right before its use; the caller
+// accounts for them in its own s_waitcnt vmcnt (the compiler does not count
+// inline assembly).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16_to_lds_sbase(const void* base, uint32_t off, unsigned char* lds) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)));
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(m0)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void dma16_to_lds(const void* g, unsigned char* lds) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)));
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m0) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// s_waitcnt with only the vector-memory counter limited to n (gfx9 encoding)
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
+// 16-byte chunk position of logical chunk c in 128-byte LDS row r is
+// c ^ swz(r): a bijection within the row under which rows 0..15 at one c
+// hit distinct banks
+__device__ __forceinline__ int swz(int r) { return (r ^ (r >> 3)) & 7; }
+
+// f(integral_constant<int, I>) for I = 0 .. N-1, unrolled at compile time
+template <typename F, int... Is>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
+  (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
 __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
   bf16x2 v;
   v[0] = static_cast<__bf16>(a);  // v_cvt_pk_bf16_f32: round to nearest even
   v[1] = static_cast<__bf16>(b);
   return __builtin_bit_cast(uint32_t, v);
 }
 
-// One K step of global data held in registers by one thread.
-template <typename Gm, int NSG>
-struct Stage {
-  u32x4 a[Gm::AU4];  // native vectors (not uint4 structs) so the stage stays in registers
-  u32x4 b[Gm::BU4];
-  // scale/bias bits of the thread's codes (two groups only for g32 with 64
-  // codes).  Kept as loaded: converting at load time would make the
-  // compiler wait for these loads -- and, since loads retire in order, for
-  // the whole step's loads -- right after issuing them.
-  uint16_t s[NSG], z[NSG];
-};
+template <int BITS, int GS, int TM, int TN>
+__global__ __launch_bounds__(256, 1) void qmm_kernel(const uint16_t* __restrict__ x, int M,
+                                                     const uint32_t* __restrict__ wq,
+                                                     const uint16_t* __restrict__ scales,
+                                                     const uint16_t* __restrict__ biases,
+                                                     const uint16_t* __restrict__ bias_vec, int N, int K,
+                                                     uint16_t* __restrict__ y, float* __restrict__ part, int k_len) {
+  using Gm = QmmGeom<BITS, GS, TM, TN>;
+  constexpr int BM = Gm::BM, BN = Gm::BN, CB = Gm::CB;
+  extern __shared__ __align__(16) unsigned char lds[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wn = wave % Gm::WN, wm = wave / Gm::WN;  // this wave's column / row block
 
-template <int BITS, int GS, int BM, int BN, int WM, int WN, int MF, int PP>
-__global__ __launch_bounds__(64 * WM * WN, 1) void qmm_kernel(const uint16_t* __restrict__ x, int M,
-                                                               const uint32_t* __restrict__ wq,
-                                                               const uint16_t* __restrict__ scales,
-                                                               const uint16_t* __restrict__ biases,
-                                                               const uint16_t* __restrict__ bias_vec, int N, int K,
-                                                               uint16_t* __restrict__ y, float* __restrict__ part,
-                                                               int k_len) {
-  using Gm = QmmGeom<BM, BN, WM, WN, BITS, MF>;
-  using AccT = std::conditional_t<MF == 32, f32x16, f32x4>;
-  static_assert(!PP || (WM == 4 && WN == 2 && BM == 256), "ping-pong: two groups of four waves");
-  // scale/bias groups per thread per step: two only for g32 with 64 codes
-  constexpr int NSG = (GS == 32 && Gm::CPT == 64) ? 2 : 1;
-  using St = Stage<Gm, NSG>;
-  constexpr int T = Gm::THREADS;
-  extern __shared__ __align__(16) uint16_t lds[];
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / WN, wn = wave % WN;
-  const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
-  // split K: slice blockIdx.z covers k_len codes from k_base (k_len = K unsplit)
-  const int k_base = blockIdx.z * k_len;
-  const int KT = k_len / BK;
+  // tile of this workgroup: XCD blockIdx.x % 8 takes tiles [xcd * per, (xcd + 1) * per)
+  const int nbn = (N + BN - 1) / BN, nbm = (M + BM - 1) / BM;
+  const int tiles = nbn * nbm, per = (tiles + 7) / 8;
+  const int t = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+  if (t >= tiles) return;
+  const int m0 = (t / nbn) * BM, n0 = (t % nbn) * BN;
+  const int kb = blockIdx.y * k_len;  // first K of this slice (split K)
+  const int KT = k_len / BK;          // a multiple of PERIOD
   const int G = K / GS;
-  const int64_t row_words = static_cast<int64_t>(K) * BITS / 32;
+  const uint32_t row_bytes = static_cast<uint32_t>(K) * BITS / 8;
 
-  // activation loader: 8 threads per row (16 B each), rows tid/8 + (T/8) i;
-  // ping-pong: each half of the threads loads the rows its own waves
-  // multiply (half h: rows 128 h + (tid % 256)/8 + 32 i)
-  const int a_chunk = tid & 7;
-  const int a_row0 = PP != 0 ? (tid >> 8) * (BM / 2) + ((tid & (T / 2 - 1)) >> 3) : (tid >> 3);
-  constexpr int A_STRIDE = PP != 0 ? T / 16 : T / 8;
-  const u32x4* a_src = reinterpret_cast<const u32x4*>(x) + a_chunk;
-  int a_off[Gm::AU4];  // uint4 offset of each row (rows past M repeat row M-1; results dropped)
+  // ---- DMA sources: per-lane byte offsets (32-bit: the host checks sizes)
+  // activations: 1 KB chunk q = 8 rows; lane -> row 8q + lane/8, chunk position lane % 8
+  uint32_t a_off[Gm::A_DMA];
 #pragma unroll
-  for (int i = 0; i < Gm::AU4; i++) a_off[i] = min(m0 + a_row0 + A_STRIDE * i, M - 1) * (K / 8);
-  // weight loader: PARTS threads per row, each CPT consecutive codes
-  const int b_row = tid / Gm::PARTS, b_part = tid % Gm::PARTS;
-  const int b_n = min(n0 + b_row, N - 1);
-  const u32x4* b_src = reinterpret_cast<const u32x4*>(wq + b_n * row_words) + b_part * Gm::BU4;
-  const uint16_t* s_src = scales + static_cast<int64_t>(b_n) * G;
-  const uint16_t* z_src = biases + static_cast<int64_t>(b_n) * G;
+  for (int i = 0; i < Gm::A_DMA; i++) {
+    const int r = 8 * (wave * Gm::A_DMA + i) + (lane >> 3), c = (lane & 7) ^ swz(r);
+    a_off[i] = (static_cast<uint32_t>(min(m0 + r, M - 1)) * K + kb + 8 * c) * 2;
+  }
+  // codes: the same row / chunk mapping over 128-byte code lines
+  uint32_t c_off[Gm::C_DMA];
+#pragma unroll
+  for (int i = 0; i < Gm::C_DMA; i++) {
+    const int r = 8 * (wave * Gm::C_DMA + i) + (lane >> 3), c = (lane & 7) ^ swz(r);
+    c_off[i] = static_cast<uint32_t>(min(n0 + r, N - 1)) * row_bytes + kb * BITS / 8 + 16 * c;
+  }
+  // scales / biases: per row [scales SROW bytes][biases SROW bytes]; lanes
+  // (row, array, 16-byte part)
+  constexpr int SPR = 2 * Gm::SROW / 16;  // lanes per row
+  uint32_t s_off[Gm::S_DMA];
+#pragma unroll
+  for (int i = 0; i < Gm::S_DMA; i++) {
+    const int r = (wave * Gm::S_DMA + i) * (64 / SPR) + lane / SPR;
+    const int part = lane % (Gm::SROW / 16);
+    s_off[i] = (static_cast<uint32_t>(min(n0 + r, N - 1)) * G + kb / GS) * 2 + 16 * part;
+  }
+  const char* sb_base = reinterpret_cast<const char*>((lane % SPR) >= SPR / 2 ? biases : scales);
 
-  auto load_a = [&](St& r, int kt) __attribute__((always_inline)) {
-    const int k0 = k_base + kt * BK;
-#pragma unroll
-    for (int i = 0; i < Gm::AU4; i++) r.a[i] = a_src[a_off[i] + k0 / 8];
+  // DMA of the activations of step kt / code batch c / scale batch sb into
+  // stage / buffer `buf` (the index is clamped past the end, the buffer not)
+  // instruction i of this wave's share of a DMA
+  auto dma_a1 = [&](int kt, int buf, int i) __attribute__((always_inline)) {
+    dma16_to_lds_sbase(reinterpret_cast<const char*>(x) + kt * (BK * 2), a_off[i],
+                 lds + Gm::A_OFF + buf * Gm::A_BYTES + (wave * Gm::A_DMA + i) * 1024);
   };
-  auto load_b = [&](St& r, int kt) __attribute__((always_inline)) {
-    const int k0 = k_base + kt * BK;
+  auto dma_c1 = [&](int c, int buf, int i) __attribute__((always_inline)) {  // steps CB c .. CB c + CB - 1
+    dma16_to_lds_sbase(reinterpret_cast<const char*>(wq) + c * 128, c_off[i],
+                 lds + Gm::C_OFF + buf * Gm::C_BYTES + (wave * Gm::C_DMA + i) * 1024);
+  };
+  auto dma_s1 = [&](int sb, int buf, int i) __attribute__((always_inline)) {  // steps 8 sb .. 8 sb + 7
+    // groups from 8 * floor(first group / 8): 16 bytes of 8 groups (GS = 128:
+    // the batch's 4 groups are one half of them)
+    dma16_to_lds(sb_base + ((sb * PERIOD * BK / GS) & ~7) * 2 + s_off[i],
+                 lds + Gm::S_OFF + buf * Gm::S_BYTES + (wave * Gm::S_DMA + i) * 1024);
+  };
+  auto dma_a = [&](int kt, int buf) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < Gm::BU4; i++) r.b[i] = b_src[k0 * BITS / 128 + i];
-    const int kc = k0 + b_part * Gm::CPT;  // first code of this thread
+    for (int i = 0; i < Gm::A_DMA; i++) dma_a1(kt, buf, i);
+  };
+  auto dma_c = [&](int c, int buf) __attribute__((always_inline)) {
 #pragma unroll
-    for (int g = 0; g < NSG; g++) {
-      r.s[g] = s_src[kc / GS + g];
-      r.z[g] = z_src[kc / GS + g];
+    for (int i = 0; i < Gm::C_DMA; i++) dma_c1(c, buf, i);
+  };
+  auto dma_s = [&](int sb, int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < Gm::S_DMA; i++) dma_s1(sb, buf, i);
+  };
+
+  // ---- fragment addressing (bytes within a stage / buffer)
+  const int fr = lane & 31, h = lane >> 5;
+  const int sw0 = (fr & 7) ^ (fr >> 3);  // swz(32 i + fr) = sw0 ^ 4 (i & 1)
+  int a_rd[4][2];
+#pragma unroll
+  for (int j = 0; j < 4; j++)
+#pragma unroll
+    for (int p = 0; p < 2; p++) a_rd[j][p] = (wm * TM * 32 + fr) * 128 + 16 * ((4 * h + j) ^ sw0 ^ (4 * p));
+  // codes of step s (s % CB = u) for tile tt: logical chunks CW (u * 2 + h) + v
+  int c_rd[CB][TN][Gm::CW];
+#pragma unroll
+  for (int u = 0; u < CB; u++)
+#pragma unroll
+    for (int tt = 0; tt < TN; tt++)
+#pragma unroll
+      for (int v = 0; v < Gm::CW; v++)
+        c_rd[u][tt][v] = (wn * TN * 32 + tt * 32 + fr) * 128 +
+                         16 * ((Gm::CW * (2 * u + h) + v) ^ swz(wn * TN * 32 + tt * 32 + fr));
+  const int s_rd = (wn * TN * 32 + fr) * 2 * Gm::SROW;  // + tt * 32 rows
+
+  bf16x8 bop[2][TN][4];  // decoded weight operands, double-buffered over steps
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int tt = 0; tt < TN; tt++)
+#pragma unroll
+      for (int v = 0; v < 16; v++) acc[i][tt][v] = 0.f;
+
+  // codes and scale/bias bits of one step for this lane, read from LDS
+  struct Raw {
+    uint32_t w[TN][4 * Gm::CW];
+    uint32_t s[TN], z[TN];
+  };
+  // step s = k0 + u (k0 % PERIOD == 0, u compile-time, may reach PERIOD + 1)
+  auto read_raw = [&](int k0, auto uc, Raw& r) __attribute__((always_inline)) {
+    constexpr int u = decltype(uc)::value;
+    const unsigned char* cs = lds + Gm::C_OFF + ((u / CB) & 1) * Gm::C_BYTES;  // k0 / CB is even
+    const int sbuf = ((k0 / PERIOD + u / PERIOD) & 1);
+    const unsigned char* ss = lds + Gm::S_OFF + sbuf * Gm::S_BYTES + s_rd;
+    // element of this step's group within the row's 16 / 32 bytes
+    int e;
+    if constexpr (GS == 32) e = 2 * (u % PERIOD) + h;
+    else if constexpr (GS == 64) e = u % PERIOD;
+    else e = 4 * ((k0 / PERIOD + u / PERIOD) & 1) + (u % PERIOD) / 2;
+#pragma unroll
+    for (int tt = 0; tt < TN; tt++) {
+      r.s[tt] = *reinterpret_cast<const uint16_t*>(ss + tt * 32 * 2 * Gm::SROW + 2 * e);
+      r.z[tt] = *reinterpret_cast<const uint16_t*>(ss + tt * 32 * 2 * Gm::SROW + Gm::SROW + 2 * e);
+#pragma unroll
+      for (int v = 0; v < Gm::CW; v++) {
+        const u32x4 q = *reinterpret_cast<const u32x4*>(cs + c_rd[u % CB][tt][v]);
+        r.w[tt][4 * v] = q[0];
+        r.w[tt][4 * v + 1] = q[1];
+        r.w[tt][4 * v + 2] = q[2];
+        r.w[tt][4 * v + 3] = q[3];
+      }
     }
   };
-  auto load = [&](St& r, int kt) __attribute__((always_inline)) {
-    load_a(r, kt);
-    load_b(r, kt);
+  auto read_a = [&](const unsigned char* as, int j, int i) __attribute__((always_inline)) {
+    return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(as + i * 32 * 128 + a_rd[j][i & 1]));
   };
-
-  // activations from ra, weights from r (the same stage)
-  auto store2 = [&](const St& ra, const St& r, int stage) __attribute__((always_inline)) {
-    uint16_t* sa = lds + stage * Gm::STAGE;
-    uint16_t* sb = sa + BM * LDR;
-#pragma unroll
-    for (int i = 0; i < Gm::AU4; i++)
-      *reinterpret_cast<u32x4*>(sa + (a_row0 + A_STRIDE * i) * LDR + a_chunk * 8) = ra.a[i];
-    constexpr int NW = Gm::BU4 * 4;  // code words
-    uint32_t w[NW];
-#pragma unroll
-    for (int i = 0; i < Gm::BU4; i++) {
-      w[4 * i] = r.b[i][0]; w[4 * i + 1] = r.b[i][1]; w[4 * i + 2] = r.b[i][2]; w[4 * i + 3] = r.b[i][3];
+  // Decode piece p (0..31) of raw codes into `dst`: word w = p / 4 (tile
+  // w / 4, sub-step w % 4), bf16 pair p % 4 of its operand.
+  float sc[TN], zz[TN], sc16[TN];
+  uint32_t lo = 0, hi = 0, d[4];
+  auto piece = [&](const Raw& r, auto pc, bf16x8 (&dst)[TN][4]) __attribute__((always_inline)) {
+    constexpr int p = decltype(pc)::value;
+    constexpr int w = p >> 2, tt = w >> 2, jj = w & 3, pp = p & 3;
+    if constexpr (jj == 0 && pp == 0) {
+      sc[tt] = __uint_as_float(r.s[tt] << 16);
+      zz[tt] = __uint_as_float(r.z[tt] << 16);
+      sc16[tt] = sc[tt] * 0.0625f;
     }
-    uint32_t packed[Gm::CPT / 2];
     if constexpr (BITS == 4) {
-#pragma unroll
-      for (int wi = 0; wi < NW; wi++) {  // word wi: codes 8 wi .. 8 wi + 7
-        const int g = NSG == 2 ? wi / 4 : 0;
-        const float sc = bf16_bits_to_f32(r.s[g]), zz = bf16_bits_to_f32(r.z[g]);
-        // even codes to the bytes of lo, odd codes to the bytes of hi: each
-        // code is then one v_cvt_f32_ubyte
-        uint32_t lo = w[wi] & 0x0F0F0F0Fu, hi = (w[wi] >> 4) & 0x0F0F0F0Fu;
-        // opaque to the optimizer (an empty asm, no instruction): otherwise
-        // it folds the masks back into one bit-field extract per code
-        asm volatile("" : "+v"(lo), "+v"(hi));
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-          packed[4 * wi + j] = pack_bf16(sc * static_cast<float>((lo >> (8 * j)) & 0xFFu) + zz,
-                                         sc * static_cast<float>((hi >> (8 * j)) & 0xFFu) + zz);
+      if constexpr (pp == 0) {
+        // even codes in the bytes of lo, odd codes (x16) in the bytes of hi
+        lo = r.w[tt][jj] & 0x0F0F0F0Fu;
+        hi = r.w[tt][jj] & 0xF0F0F0F0u;
+        asm("" : "+v"(lo), "+v"(hi));  // keep the byte form (one v_cvt_f32_ubyte per code)
       }
+      d[pp] = pack_bf16(__builtin_fmaf(sc[tt], static_cast<float>((lo >> (8 * pp)) & 0xFFu), zz[tt]),
+                        __builtin_fmaf(sc16[tt], static_cast<float>((hi >> (8 * pp)) & 0xFFu), zz[tt]));
     } else {
-#pragma unroll
-      for (int wi = 0; wi < NW; wi++) {  // word wi: codes 4 wi .. 4 wi + 3
-        const int g = NSG == 2 ? wi / 8 : 0;
-        const float sc = bf16_bits_to_f32(r.s[g]), zz = bf16_bits_to_f32(r.z[g]);
-        const uint32_t q = w[wi];
-        packed[2 * wi] = pack_bf16(sc * static_cast<float>(q & 0xFFu) + zz, sc * static_cast<float>((q >> 8) & 0xFFu) + zz);
-        packed[2 * wi + 1] = pack_bf16(sc * static_cast<float>((q >> 16) & 0xFFu) + zz, sc * static_cast<float>(q >> 24) + zz);
+      const uint32_t q = r.w[tt][2 * jj + (pp >> 1)];
+      const int b0 = 16 * (pp & 1);
+      d[pp] = pack_bf16(__builtin_fmaf(sc[tt], static_cast<float>((q >> b0) & 0xFFu), zz[tt]),
+                        __builtin_fmaf(sc[tt], static_cast<float>((q >> (b0 + 8)) & 0xFFu), zz[tt]));
+    }
+    if constexpr (pp == 3) dst[tt][jj] = __builtin_bit_cast(bf16x8, u32x4{d[0], d[1], d[2], d[3]});
+  };
+
+  // One K step (kt = k0 + u) as a fixed instruction schedule: slot s issues
+  // MFMA s (sub-step j = s / (TM TN), row tile i, column tile tt); after the
+  // last MFMA of row tile i the LDS read of its fragment for sub-step j + 1
+  // (for j = 3: the next step's first sub-step) into the same registers;
+  // then decode pieces of the next step's operands.  Each slot is fenced, so
+  // the wave alternates between the matrix core and the vector ALU.  In the
+  // last sub-step, once every activation read of the step has been issued,
+  // sits the step boundary: wait for this wave's DMA of the next step's
+  // activations, barrier, issue the DMA that the schedule places here, read
+  // the codes of the step after next.  With 256-row tiles the decode pieces
+  // all come before the boundary, so one set of raw-code registers serves
+  // (the boundary refills it); with 128-row tiles they spread over the whole
+  // step and the raw codes are double-buffered.
+  constexpr int S = 4 * TM * TN, NP = 4 * 4 * TN, BOUNDARY = 3 * TM * TN + 1;
+  constexpr bool ONE_RAW = NP <= BOUNDARY;
+  constexpr int PIECE_SLOTS = ONE_RAW ? BOUNDARY : S;
+  constexpr int NRAW = ONE_RAW ? 1 : 2;
+  const int KTL = KT - 1;
+  auto step = [&](int k0, auto uc, const bf16x8 (&cur)[TN][4], bf16x8 (&nxt)[TN][4], const Raw& rcur, Raw& rnext,
+                  bf16x8 (&a)[TM]) __attribute__((always_inline)) {
+    constexpr int u = decltype(uc)::value;
+    const int kt = k0 + u;
+    const unsigned char* as = lds + Gm::A_OFF + (u & 1) * Gm::A_BYTES;
+    const unsigned char* an = lds + Gm::A_OFF + ((u + 1) & 1) * Gm::A_BYTES;
+    static_for<S>([&](auto sc_) __attribute__((always_inline)) {
+      constexpr int s = decltype(sc_)::value;
+      constexpr int j = s / (TM * TN), r = s % (TM * TN), i = r / TN, tt = r % TN;
+      if constexpr (s == BOUNDARY) {
+        wait_lgkm0();  // this wave's reads of stage kt & 1 are done
+        // activations of step kt + 1 (issued at the previous boundary, before
+        // the codes / scales that boundary issued)
+        wait_vm<Gm::after((u + PERIOD - 1) % PERIOD)>();
+        __builtin_amdgcn_s_barrier();
+        read_raw(k0, std::integral_constant<int, u + 2>{}, rnext);
+        __builtin_amdgcn_sched_barrier(0);
       }
-    }
-    u32x4* dst = reinterpret_cast<u32x4*>(sb + b_row * LDR + b_part * Gm::CPT);
-#pragma unroll
-    for (int i = 0; i < Gm::CPT / 8; i++)
-      dst[i] = u32x4{packed[4 * i], packed[4 * i + 1], packed[4 * i + 2], packed[4 * i + 3]};
+      // weights as the first operand: the output tile comes out transposed,
+      // lane = activation row, 4 consecutive output columns per register quad
+      acc[i][tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cur[tt][j], a[i], acc[i][tt], 0, 0, 0);
+      if constexpr (tt == TN - 1) a[i] = read_a(j < 3 ? as : an, (j + 1) & 3, i);
+      // DMA, one instruction per slot so the requests do not queue up
+      // behind each other: after the boundary the activations of step kt + 2
+      // into stage kt & 1 (read by every wave before the barrier); in the
+      // first slots, when the previous boundary scheduled them (after its
+      // activations), code batch (kt + 1) / CB + 1 (when step kt + 1 starts a
+      // batch) and scale batch (kt + 9) / 8 (at u = 7).  Past the end: the
+      // last step / batch again, into buffers nobody reads.
+      if constexpr (s > BOUNDARY && s <= BOUNDARY + Gm::A_DMA) dma_a1(min(kt + 2, KTL), u & 1, s - BOUNDARY - 1);
+      if constexpr (u > 0 && (u + 1) % CB == 0 && s < Gm::C_DMA)
+        dma_c1(min((kt + 1) / CB + 1, KTL / CB), ((u + 1) / CB + 1) & 1, s);
+      if constexpr (u == PERIOD - 1 && s >= Gm::C_DMA && s < Gm::C_DMA + Gm::S_DMA)
+        dma_s1(min((kt + 9) / PERIOD, KTL / PERIOD), (k0 / PERIOD) & 1, s - Gm::C_DMA);
+      // pieces p with p * PIECE_SLOTS / NP == s
+      constexpr int P_LO = (s * NP + PIECE_SLOTS - 1) / PIECE_SLOTS;
+      constexpr int P_HI = ((s + 1) * NP + PIECE_SLOTS - 1) / PIECE_SLOTS;
+      static_for<(NP + PIECE_SLOTS - 1) / PIECE_SLOTS>([&](auto qc) __attribute__((always_inline)) {
+        constexpr int p = P_LO + decltype(qc)::value;
+        if constexpr (p < P_HI && p < NP) piece(rcur, std::integral_constant<int, p>{}, nxt);
+      });
+      __builtin_amdgcn_sched_barrier(0);
+    });
   };
-  auto store = [&](const St& r, int stage) __attribute__((always_inline)) { store2(r, r, stage); };
 
-  AccT acc[Gm::TM][Gm::TN];
+  // ---- prologue: code batches 0 and 1, scale batches 0 and 1, activations
+  // of steps 0 and 1; the operands of step 0 decoded here
+  bf16x8 a[TM];
+  Raw raw[NRAW];
+  dma_c(0, 0);
+  dma_s(0, 0);
+  dma_a(0, 0);
+  dma_c(min(1, KTL / CB), 1);
+  dma_s(min(1, KTL / PERIOD), 1);
+  dma_a(min(1, KTL), 1);
+  wait_vm<Gm::A_DMA + Gm::C_DMA + Gm::S_DMA>();
+  __builtin_amdgcn_s_barrier();
+  read_raw(0, std::integral_constant<int, 0>{}, raw[0]);
 #pragma unroll
-  for (int i = 0; i < Gm::TM; i++)
-#pragma unroll
-    for (int j = 0; j < Gm::TN; j++)
-#pragma unroll
-      for (int v = 0; v < Gm::NV; v++) acc[i][j][v] = 0.f;
+  for (int i = 0; i < TM; i++) a[i] = read_a(lds + Gm::A_OFF, 0, i);
+  static_for<NP>([&](auto pc) __attribute__((always_inline)) { piece(raw[0], pc, bop[0]); });
+  read_raw(0, std::integral_constant<int, 1>{}, raw[NRAW - 1]);
 
-  // A/B fragment of an MF x MF tile: lane holds row lane % MF and 8
-  // consecutive k from (lane / MF) * 8
-  const int frag_row = lane & (MF - 1);
-  const int frag_k = (lane / MF) * 8;
-  constexpr int WROWS = BM / WM, WCOLS = BN / WN;
+  for (int k0 = 0; k0 < KT; k0 += PERIOD) {
+    static_for<PERIOD / 2>([&](auto vc) __attribute__((always_inline)) {
+      constexpr int u = 2 * decltype(vc)::value;
+      step(k0, std::integral_constant<int, u>{}, bop[0], bop[1], raw[NRAW - 1], raw[0], a);
+      step(k0, std::integral_constant<int, u + 1>{}, bop[1], bop[0], raw[0], raw[NRAW - 1], a);
+    });
+  }
+  wait_vm<0>();  // no DMA may land after the workgroup's LDS is released
 
-  St r0, r1;
-  load(r0, 0);
-  load(r1, min(1, KT - 1));
-  __builtin_amdgcn_sched_barrier(0);
-  store(r0, 0);
-  if constexpr ((PP & 8) != 0) load_b(r0, min(2, KT - 1));  // the weights run one step further ahead
-  __syncthreads();
-  // One K step: LDS stage kt&1 holds step kt, `ready` holds step kt+1 and
-  // `target` receives step kt+2.  Called with (r0, r1) and (r1, r0) in turn
-  // so that the register roles are static.
-  auto step = [&](int kt, St& target, St& ready) __attribute__((always_inline)) {
-    const int cur = kt & 1;
-    // unconditional (past the end: the last step again, its lines are on
-    // chip): a conditional load would make the compiler's memory-counter wait
-    // before `store(ready)` drain every load in flight, this step's included
-    load(target, min(kt + 2, KT - 1));
-    __builtin_amdgcn_sched_barrier(0);
-    const uint16_t* sa = lds + cur * Gm::STAGE + (wm * WROWS + frag_row) * LDR + frag_k;
-    const uint16_t* sb = lds + cur * Gm::STAGE + BM * LDR + (wn * WCOLS + frag_row) * LDR + frag_k;  // weights
+  // Output layout of a 32x32 tile (weights x activations^T): lane holds
+  // activation row m = lane % 32 and output columns n = 8 (v / 4) + 4 (lane /
+  // 32) + v % 4 for accumulator v.  Pairs of column groups are exchanged
+  // between the wave halves (permlane32 swap) so that every lane ends with 8
+  // consecutive columns: one 16-byte store (bf16) or two (f32 partials).
+  const int mrow0 = m0 + wm * TM * 32 + fr;
+  const int ncol0 = n0 + wn * TN * 32;
+  if (part) {  // split K: this slice's f32 partial sums, added by the reduce kernel
+    float* dst = part + static_cast<int64_t>(blockIdx.y) * M * N;
 #pragma unroll
-    for (int ks = 0; ks < BK / Gm::KS; ks++) {
-      bf16x8 a[Gm::TM], b[Gm::TN];
+    for (int i = 0; i < TM; i++) {
+      const int m = mrow0 + i * 32;
+      if (m >= M) continue;
 #pragma unroll
-      for (int i = 0; i < Gm::TM; i++)
-        a[i] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(sa + MF * i * LDR + ks * Gm::KS));
+      for (int tt = 0; tt < TN; tt++)
 #pragma unroll
-      for (int j = 0; j < Gm::TN; j++)
-        b[j] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(sb + MF * j * LDR + ks * Gm::KS));
+        for (int g = 0; g < 4; g++) {
+          const int n = ncol0 + tt * 32 + 8 * g + 4 * h;
+          float* q = dst + static_cast<int64_t>(m) * N + n;
+          if (n + 3 < N && (N & 3) == 0) {
+            *reinterpret_cast<f32x4*>(q) = f32x4{acc[i][tt][4 * g], acc[i][tt][4 * g + 1], acc[i][tt][4 * g + 2],
+                                                 acc[i][tt][4 * g + 3]};
+          } else {
 #pragma unroll
-      for (int i = 0; i < Gm::TM; i++)
-#pragma unroll
-        for (int j = 0; j < Gm::TN; j++) {
-          if constexpr (MF == 32)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
-          else
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
-        }
-    }
-    if (kt + 1 < KT) store(ready, cur ^ 1);
-    __syncthreads();
-  };
-  if constexpr (PP != 0) {
-    // Ping-pong: waves 0-3 (group 0, output rows 0-127) and 4-7 (group 1,
-    // rows 128-255) take turns between barriers.  While one group runs its
-    // MFMAs on stage kt, the other writes its half of stage kt+1 (loaded two
-    // phases earlier) and requests its half of stage kt+2; each SIMD (one
-    // wave of each group) so has one wave on the matrix core and one on
-    // the vector ALU and LDS.  Stage (kt+1)&1 was last read in the previous
-    // step, which both groups have left.
-    const int grp = __builtin_amdgcn_readfirstlane((PP & 3) == 1 ? wave >> 2 : wave & 1);
-    auto mma = [&](int kt) __attribute__((always_inline)) {
-      if constexpr ((PP & 4) != 0) __builtin_amdgcn_s_setprio(1);
-      const int cur = kt & 1;
-      const uint16_t* sa = lds + cur * Gm::STAGE + (wm * WROWS + frag_row) * LDR + frag_k;
-      const uint16_t* sb = lds + cur * Gm::STAGE + BM * LDR + (wn * WCOLS + frag_row) * LDR + frag_k;
-#pragma unroll
-      for (int ks = 0; ks < BK / Gm::KS; ks++) {
-        bf16x8 a[Gm::TM], b[Gm::TN];
-#pragma unroll
-        for (int i = 0; i < Gm::TM; i++)
-          a[i] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(sa + MF * i * LDR + ks * Gm::KS));
-#pragma unroll
-        for (int j = 0; j < Gm::TN; j++)
-          b[j] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(sb + MF * j * LDR + ks * Gm::KS));
-#pragma unroll
-        for (int i = 0; i < Gm::TM; i++)
-#pragma unroll
-          for (int j = 0; j < Gm::TN; j++) {
-            if constexpr (MF == 32)
-              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
-            else
-              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+            for (int e = 0; e < 4; e++)
+              if (n + e < N) q[e] = acc[i][tt][4 * g + e];
           }
-      }
-      if constexpr ((PP & 4) != 0) __builtin_amdgcn_s_setprio(0);
-    };
-    // r1 holds this thread's part of stage 1; past the end a stage nobody
-    // reads is written (unconditional: no branch around the loads)
-    auto fill = [&](int kt) __attribute__((always_inline)) {
-      store(r1, (kt + 1) & 1);
-      load(r1, min(kt + 2, KT - 1));
-    };
-    // deep form (PP & 8, KT even): the weights of stage kt+1 alternate
-    // between r1 and r0 and are requested three steps ahead, the
-    // activations (mostly L2 hits) two
-    auto fill_e = [&](int kt) __attribute__((always_inline)) {
-      store2(r1, r1, (kt + 1) & 1);
-      load_a(r1, min(kt + 2, KT - 1));
-      load_b(r1, min(kt + 3, KT - 1));
-    };
-    auto fill_o = [&](int kt) __attribute__((always_inline)) {
-      store2(r1, r0, (kt + 1) & 1);
-      load_a(r1, min(kt + 2, KT - 1));
-      load_b(r0, min(kt + 3, KT - 1));
-    };
-    // one loop per group (a wave-uniform branch): both run two barriers per
-    // step, so the barriers pair up with the groups half a step apart
-    if constexpr ((PP & 8) != 0) {
-      if (grp == 0) {
-        for (int kt = 0; kt < KT; kt += 2) {
-          mma(kt);
-          __syncthreads();
-          fill_e(kt);
-          __syncthreads();
-          mma(kt + 1);
-          __syncthreads();
-          fill_o(kt + 1);
-          __syncthreads();
         }
-      } else {
-        for (int kt = 0; kt < KT; kt += 2) {
-          fill_e(kt);
-          __syncthreads();
-          mma(kt);
-          __syncthreads();
-          fill_o(kt + 1);
-          __syncthreads();
-          mma(kt + 1);
-          __syncthreads();
-        }
-      }
-    } else if (grp == 0) {
-      for (int kt = 0; kt < KT; kt++) {
-        mma(kt);
-        __syncthreads();
-        fill(kt);
-        __syncthreads();
-      }
-    } else {
-      for (int kt = 0; kt < KT; kt++) {
-        fill(kt);
-        __syncthreads();
-        mma(kt);
-        __syncthreads();
-      }
     }
   } else {
-    for (int kt = 0; kt < KT; kt += 2) {
-      step(kt, r0, r1);
-      if (kt + 1 < KT) step(kt + 1, r1, r0);
-    }
-  }
-
-  // C layout of an MFMA tile: lane holds column lane % MF and, for 32x32,
-  // rows 8*(v/4) + 4*(lane/32) + v%4; for 16x16, rows 4*(lane/16) + v.
-  auto row_of = [&](int i, int v) {
-    return m0 + wm * WROWS + MF * i +
-           (MF == 32 ? 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3) : 4 * (lane >> 4) + v);
-  };
-  if (part) {  // split K: this slice's f32 partial sums, added by the reduce kernel
-    float* dst = part + static_cast<int64_t>(blockIdx.z) * M * N;
 #pragma unroll
-    for (int j = 0; j < Gm::TN; j++) {
-      const int n = n0 + wn * WCOLS + MF * j + (lane & (MF - 1));
-      if (n >= N) continue;
+    for (int tt = 0; tt < TN; tt++) {
 #pragma unroll
-      for (int i = 0; i < Gm::TM; i++)
+      for (int gp = 0; gp < 2; gp++) {
+        // columns ncol0 + tt 32 + 16 gp + 8 h + [0, 8) after the exchange;
+        // before it this lane holds groups 2 gp + q (q = 0, 1) at columns
+        // ncol0 + tt 32 + 16 gp + 8 q + 4 h + [0, 4)
+        const int n = ncol0 + tt * 32 + 16 * gp + 8 * h;
+        float bb[2][4];
 #pragma unroll
-        for (int v = 0; v < Gm::NV; v++) {
-          const int m = row_of(i, v);
-          if (m < M) dst[static_cast<int64_t>(m) * N + n] = acc[i][j][v];
+        for (int q = 0; q < 2; q++)
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const int nb = ncol0 + tt * 32 + 16 * gp + 8 * q + 4 * h + e;
+            bb[q][e] = bias_vec && nb < N ? bf16_bits_to_f32(bias_vec[nb]) : 0.f;
+          }
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+          const f32x16& c = acc[i][tt];
+          const uint32_t lo0 = pack_bf16(c[8 * gp + 0] + bb[0][0], c[8 * gp + 1] + bb[0][1]);
+          const uint32_t lo1 = pack_bf16(c[8 * gp + 2] + bb[0][2], c[8 * gp + 3] + bb[0][3]);
+          const uint32_t hi0 = pack_bf16(c[8 * gp + 4] + bb[1][0], c[8 * gp + 5] + bb[1][1]);
+          const uint32_t hi1 = pack_bf16(c[8 * gp + 6] + bb[1][2], c[8 * gp + 7] + bb[1][3]);
+          // lanes 0-31 keep group 2 gp and receive the other half's group
+          // 2 gp; lanes 32-63 keep group 2 gp + 1 and receive the first
+          // half's group 2 gp + 1
+          const auto s0 = __builtin_amdgcn_permlane32_swap(lo0, hi0, false, false);
+          const auto s1 = __builtin_amdgcn_permlane32_swap(lo1, hi1, false, false);
+          const uint32_t w0 = s0[0], w1 = s1[0], w2 = s0[1], w3 = s1[1];
+          const int m = mrow0 + i * 32;
+          if (m >= M) continue;
+          uint16_t* q = y + static_cast<int64_t>(m) * N + n;
+          if (n + 7 < N && (N & 7) == 0) {
+            *reinterpret_cast<u32x4*>(q) = u32x4{w0, w1, w2, w3};
+          } else {
+            const uint32_t ww[4] = {w0, w1, w2, w3};
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+              if (n + e < N) q[e] = static_cast<uint16_t>(ww[e >> 1] >> (16 * (e & 1)));
+          }
         }
-    }
-    return;
-  }
-#pragma unroll
-  for (int j = 0; j < Gm::TN; j++) {
-    const int n = n0 + wn * WCOLS + MF * j + (lane & (MF - 1));
-    if (n >= N) continue;
-    const float bb = bias_vec ? bf16_bits_to_f32(bias_vec[n]) : 0.f;
-#pragma unroll
-    for (int i = 0; i < Gm::TM; i++)
-#pragma unroll
-      for (int v = 0; v < Gm::NV; v++) {
-        const int m = row_of(i, v);
-        if (m < M) y[static_cast<int64_t>(m) * N + n] = static_cast<uint16_t>(f32_to_bf16_bits(acc[i][j][v] + bb));
       }
+    }
   }
 }
 
-template <int BITS, int GS, int BM, int BN, int WM, int WN, int MF = 32, int PP = 0>
+template <int BITS, int GS, int TM, int TN>
 int launch(const uint16_t* x, int M, const uint32_t* wq, const uint16_t* s, const uint16_t* b, const uint16_t* bias,
            int N, int K, uint16_t* y, float* part, int splits, hipStream_t st) {
-  using Gm = QmmGeom<BM, BN, WM, WN, BITS, MF>;
-  auto kern = qmm_kernel<BITS, GS, BM, BN, WM, WN, MF, PP>;
+  using Gm = QmmGeom<BITS, GS, TM, TN>;
+  auto kern = qmm_kernel<BITS, GS, TM, TN>;
   static bool attr_set = false;  // once per process; the attribute is per function
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -405,7 +493,8 @@ int launch(const uint16_t* x, int M, const uint32_t* wq, const uint16_t* s, cons
     if (e != hipSuccess) return fail(MLXQ_ERR_DEVICE, std::string("qmm: set LDS size: ") + hipGetErrorString(e));
     attr_set = true;
   }
-  dim3 grid(ceil_div(N, BN), ceil_div(M, BM), splits);
+  const int64_t tiles = ceil_div(N, Gm::BN) * ceil_div(M, Gm::BM);
+  dim3 grid(static_cast<unsigned>(8 * ceil_div(tiles, 8)), splits);
   hipLaunchKernelGGL(kern, grid, dim3(Gm::THREADS), Gm::LDS_BYTES, st, x, M, wq, s, b, bias, N, K, y,
                      splits > 1 ? part : nullptr, K / splits);
   if (int rc = check_launch("qmm")) return rc;
@@ -424,81 +513,60 @@ int cu_count() {
   return cus;
 }
 
+// Workgroup tile of a launch: 256 rows (four waves of 256 x 64) when those
+// tiles give at least one full round of workgroups, else 128 rows (four
+// waves of 128 x 64: half the MFMAs per decoded code, twice the workgroups).
+// MLXQ_QMM_CFG = 82 / 42 forces one (tests, tuning).  Measured and not kept
+// (Llama-3-8B prefill, M = 2048): 2 x 2 waves of 128 x 128 (each column
+// decoded twice), and two 128-row workgroups per CU.
+int qmm_cfg(int64_t M, int64_t N, int splits) {
+  if (const int c = overrides().qmm_cfg) return c == 42 ? 42 : 82;
+  return ceil_div(N, 256) * ceil_div(M, 256) * splits >= cu_count() ? 82 : 42;
+}
+
 template <int BITS, int GS>
 int launch_cfg(const uint16_t* x, int M, const uint32_t* wq, const uint16_t* s, const uint16_t* b, const uint16_t* bias,
                int N, int K, uint16_t* y, float* part, int splits, hipStream_t st) {
-  // Configurations measured at the Llama-3-8B projection shapes for M from
-  // 256 to 4096; MLXQ_QMM_CFG overrides (tuning).
-  const int64_t tiles256 = ceil_div(N, 256) * ceil_div(M, 256);
-  const int64_t cus = cu_count();
-  // Ping-pong 256-row tiles (two groups of four waves take turns on the
-  // matrix cores) when the grid fills the CUs or K is split; the deep form
-  // (weights three K steps ahead) needs an even number of K steps.  For N a
-  // multiple of 224 (gate/up: 14336 = 64 x 224) Q4 takes 256 x 224 tiles,
-  // which make whole rounds of CUs where 256-wide ones leave a partial one.
-  // Grids too small for either: 128 x 128 tiles, two workgroups per CU.
-  const bool even_steps = (K / splits / BK) % 2 == 0;
-  int cfg = 6;
-  if (tiles256 * splits * 8 >= cus * 7) cfg = even_steps ? 14 : 9;
-  if (BITS == 4 && splits == 1 && N % 224 == 0 && (N / 224) * ceil_div(M, 256) * 8 >= cus * 7)
-    cfg = even_steps ? 15 : 10;
-  if (overrides().qmm_cfg) cfg = overrides().qmm_cfg;
-  switch (cfg) {
-    case 1: return launch<BITS, GS, 256, 256, 2, 4>(x, M, wq, s, b, bias, N, K, y, part, splits, st);
-    case 2: return launch<BITS, GS, 256, 128, 2, 2>(x, M, wq, s, b, bias, N, K, y, part, splits, st);
-    case 3: return launch<BITS, GS, 128, 256, 2, 4>(x, M, wq, s, b, bias, N, K, y, part, splits, st);
-    case 4: return launch<BITS, GS, 256, 256, 4, 2>(x, M, wq, s, b, bias, N, K, y, part, splits, st);
-    case 6: return launch<BITS, GS, 128, 128, 2, 2>(x, M, wq, s, b, bias, N, K, y, part, splits, st);
-    case 7: return launch<BITS, GS, 256, 224, 4, 2, 16>(x, M, wq, s, b, bias, N, K, y, part, splits, st);
-    case 9: return launch<BITS, GS, 256, 256, 4, 2, 32, 1>(x, M, wq, s, b, bias, N, K, y, part, splits, st);
-    case 10: return launch<BITS, GS, 256, 224, 4, 2, 16, 1>(x, M, wq, s, b, bias, N, K, y, part, splits, st);
-    case 14: return launch<BITS, GS, 256, 256, 4, 2, 32, 9>(x, M, wq, s, b, bias, N, K, y, part, splits, st);
-    case 15: return launch<BITS, GS, 256, 224, 4, 2, 16, 9>(x, M, wq, s, b, bias, N, K, y, part, splits, st);
-    default: return launch<BITS, GS, 128, 256, 2, 2>(x, M, wq, s, b, bias, N, K, y, part, splits, st);
-  }
+  if (qmm_cfg(M, N, splits) == 42) return launch<BITS, GS, 4, 2>(x, M, wq, s, b, bias, N, K, y, part, splits, st);
+  return launch<BITS, GS, 8, 2>(x, M, wq, s, b, bias, N, K, y, part, splits, st);
 }
 
 }  // namespace
 
-int qmm_split_k(int64_t M, int64_t N, int64_t K) {
-  // 256 x 256 tiles times splits should fill about one round of workgroups
-  // (one per CU) when the unsplit grid leaves most CUs idle; each slice
-  // keeps at least 16 K steps and whole groups (K / splits % 128 == 0).
-  // MLXQ_QMM_SPLIT overrides (tuning).
+bool qmm_eligible(int64_t K, int group_size) { return K % (PERIOD * BK) == 0 && K % (8 * group_size) == 0; }
+
+int qmm_split_k(int64_t M, int64_t N, int64_t K, int group_size) {
+  // split K when even 128-row tiles leave most CUs idle; every slice is a
+  // whole number of unrolled periods and of 8-group scale batches.
+  // MLXQ_QMM_SPLIT overrides (tests, tuning).
+  const int64_t grain = std::max<int64_t>(PERIOD * BK, 8 * group_size);
   if (const int sp = overrides().qmm_split) {
-    return sp >= 1 && sp <= kQmmMaxSplits && K % (128 * sp) == 0 ? sp : 1;
+    return sp >= 1 && sp <= kQmmMaxSplits && K % (grain * sp) == 0 ? sp : 1;
   }
   const int64_t cus = cu_count();
-  const int64_t tiles = ceil_div(N, 256) * ceil_div(M, 256);
-  if (tiles * 8 >= cus * 7) return 1;
-  for (int sp = 2; sp <= kQmmMaxSplits; sp++) {
-    if (tiles * sp > cus) break;
-    if (tiles * sp * 8 >= cus * 7 && K % (128 * sp) == 0 && K / sp >= 16 * 64) return sp;
-  }
-  // grids that no split of 256 x 256 tiles fills (short matrices or few
-  // rows): 128 x 128 tiles (two workgroups per CU), K split as far as the
-  // CUs and the 16-step minimum allow (launch_cfg takes the 128 x 128 form
-  // whenever the split 256-wide grid would still leave CUs idle).  Measured
-  // (Q4, µs): q/o M = 128 63.6 -> 28.8, M = 512 65.7 -> 40.5; k/v M = 512
-  // 64.3 -> 27.3; down M = 128 195 -> 39.9, M = 256 197 -> 56.7
-  const int64_t t128 = ceil_div(N, 128) * ceil_div(M, 128);
+  const int64_t t128 = ceil_div(N, 256) * ceil_div(M, 128);
+  if (t128 * 4 >= cus * 3) return 1;
   int best = 1;
   for (int sp = 2; sp <= kQmmMaxSplits; sp++)
-    if (t128 * sp <= 2 * cus && K % (128 * sp) == 0 && K / sp >= 16 * 64) best = sp;
+    if (t128 * sp <= cus && K % (grain * sp) == 0) best = sp;
   return best;
 }
 
-size_t qmm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
-  const int sp = qmm_split_k(M, N, K);
+size_t qmm_workspace_bytes(int64_t M, int64_t N, int64_t K, int group_size) {
+  const int sp = qmm_split_k(M, N, K, group_size);
   return sp > 1 ? static_cast<size_t>(sp) * M * N * sizeof(float) : 0;
 }
 
 int launch_qmm(const uint16_t* x, int64_t M, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
                const uint16_t* bias, int64_t N, int64_t K, int group_size, int bits, uint16_t* y, void* workspace,
                size_t workspace_bytes, hipStream_t st) {
+  // the DMA offsets are 32-bit byte offsets from the array bases
+  if (M * K * 2 >= (int64_t(1) << 32) || N * K * bits / 8 >= (int64_t(1) << 32) || !qmm_eligible(K, group_size))
+    return fail(MLXQ_ERR_UNSUPPORTED, "qmm: activations and codes must each be below 4 GiB, K a multiple of " +
+                                          std::to_string(PERIOD * BK) + " and of 8 groups");
   const int m = static_cast<int>(M), n = static_cast<int>(N), k = static_cast<int>(K);
   // split K only when the caller's workspace holds the partials
-  int splits = qmm_split_k(M, N, K);
+  int splits = qmm_split_k(M, N, K, group_size);
   if (splits > 1 && (!workspace || workspace_bytes < static_cast<size_t>(splits) * M * N * sizeof(float) ||
                      (reinterpret_cast<uintptr_t>(workspace) & 255u)))
     splits = 1;

@@ -77,21 +77,23 @@ def test_quantize_and_qmatmul_argument_errors():
     assert L.mlxq_qmatmul(p, 1, p, p, p, None, 64, 100, 64, 4, p, None, 0, None) == mlxq.ERR_SHAPE
     assert L.mlxq_qmatmul(p, 1, p, p, p, None, 64, 128, 64, 2, p, None, 0, None) == mlxq.ERR_UNSUPPORTED
     # workspace: split-K partials of the batched-decode kernel (group 64,
-    # 2 <= M <= 32: at most 16 slices of M x N f32) and of prefill shapes
-    # whose 256 x 256 tiles fill under 7/8 of the 256 CUs (slices chosen to
-    # fill about one round)
+    # 2 <= M <= 32: at most 16 slices of M x N f32) and of qmm shapes whose
+    # 128-row tiles fill under 3/4 of the 256 CUs (slices chosen to fill
+    # about one round)
     assert mlxq.workspace_size(1, 4096, 4096, 64, 4) == 0
     assert mlxq.workspace_size(32, 4096, 4096, 64, 4) == 16 * 32 * 4096 * 4
     assert mlxq.workspace_size(32, 4096, 4096, 32, 4) == 0
     # prefill routes: the library GEMM needs the whole weight as bf16 plus
     # 32 MiB for hipBLASLt; 33..64 rows run as 32-row decode calls
     lib = lambda n, k: n * k * 2 + (32 << 20)  # noqa: E731
-    assert mlxq.workspace_size(2048, 4096, 4096, 64, 4) == max(lib(4096, 4096), 2 * 2048 * 4096 * 4)
-    assert mlxq.workspace_size(512, 4096, 4096, 64, 4) == 4 * 512 * 4096 * 4        # fused, 128-wide tiles, 4 slices
-    assert mlxq.workspace_size(2048, 4096, 14336, 64, 4) == lib(4096, 14336)
-    assert mlxq.workspace_size(1024, 4096, 14336, 64, 8) == 4 * 1024 * 4096 * 4   # fused: 64 tiles -> 4 slices
-    assert mlxq.workspace_size(2048, 14336, 4096, 64, 4) == lib(14336, 4096)
-    assert mlxq.workspace_size(2048, 1024, 4096, 64, 4) == lib(1024, 4096)
+    assert mlxq.workspace_size(2048, 4096, 4096, 64, 4) == lib(4096, 4096)          # square, M >= 1024: library
+    assert mlxq.workspace_size(512, 4096, 4096, 64, 4) == 4 * 512 * 4096 * 4        # qmm, 128-row tiles, 4 slices
+    # (arguments: M, N, K)
+    assert mlxq.workspace_size(2048, 14336, 4096, 64, 4) == lib(14336, 4096)        # gate/up-like, M >= 1024
+    assert mlxq.workspace_size(512, 14336, 4096, 64, 8) == 0                        # gate/up-like qmm: unsplit
+    assert mlxq.workspace_size(2048, 4096, 14336, 64, 4) == 0                       # down-like qmm: unsplit
+    assert mlxq.workspace_size(4096, 4096, 14336, 64, 4) == lib(4096, 14336)        # down-like, M = 4096
+    assert mlxq.workspace_size(2048, 1024, 4096, 64, 4) == 4 * 2048 * 1024 * 4      # k/v-like qmm: 4 slices
     assert mlxq.workspace_size(64, 4096, 4096, 64, 4) == 16 * 32 * 4096 * 4      # decode chunks of 32
     assert L.mlxq_qmatmul_algo(p, 1, p, p, p, None, 64, 128, 64, 4, p, None, 0, 7, None) == mlxq.ERR_INVALID
     # M = 0 is a no-op
@@ -99,13 +101,13 @@ def test_quantize_and_qmatmul_argument_errors():
 
 
 def test_workspace_sizes_fused_prefill(monkeypatch):
-    """MLXQ_QMM_FUSED=1: prefill always on the fused kernel, whose split-K
-    partials fill about one round of the 256 CUs when its 256 x 256 tiles
-    fill under 7/8 of them."""
+    """MLXQ_QMM_FUSED=1: prefill always on the qmm kernel, which splits K
+    (f32 partials in the workspace) only when even its 128-row tiles fill
+    under 3/4 of the 256 CUs, into slices of whole 512-K periods."""
     monkeypatch.setenv("MLXQ_QMM_FUSED", "1")
-    assert mlxq.workspace_size(2048, 4096, 4096, 64, 4) == 2 * 2048 * 4096 * 4    # 128 tiles -> 2 slices
-    assert mlxq.workspace_size(2048, 4096, 14336, 64, 4) == 2 * 2048 * 4096 * 4
-    assert mlxq.workspace_size(2048, 14336, 4096, 64, 4) == 0                     # 448 tiles: unsplit
+    assert mlxq.workspace_size(2048, 4096, 4096, 64, 4) == 0                      # 256 128-row tiles: unsplit
+    assert mlxq.workspace_size(2048, 4096, 14336, 64, 4) == 0
+    assert mlxq.workspace_size(2048, 14336, 4096, 64, 4) == 0
     assert mlxq.workspace_size(2048, 1024, 4096, 64, 4) == 4 * 2048 * 1024 * 4    # 128-wide tiles, 4 slices
 
 

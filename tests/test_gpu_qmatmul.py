@@ -93,7 +93,7 @@ def test_qmv_repeat_reuses_workspace(torch_gpu):
 @pytest.mark.parametrize("gs", [32, 64, 128])
 @pytest.mark.parametrize("m", [16, 300])
 def test_qmm_small(torch_gpu, bits, gs, m):
-    n, k = 200, 512
+    n, k = 200, 1024
     wq, s, b = make_layer(50 + bits + gs, n, k, gs, bits)
     x = bf16_acts(60 + m, m, k)
     ref = orc.qmatmul_f64(x, wq, s, b, gs, bits)
@@ -111,31 +111,33 @@ def test_qmm_split_k(torch_gpu, monkeypatch, bits, gs, splits, n):
     0) and the scalar one, a bias vector, M not a multiple of the tile."""
     monkeypatch.setenv("MLXQ_QMM_SPLIT", str(splits))
     monkeypatch.setenv("MLXQ_QMM_FUSED", "1")
-    m, k = 300, 1024
+    # slices of whole 512-K periods and 8-group scale batches
+    m, k = 300, 4096 if splits * max(512, 8 * gs) <= 4096 else 8192
     assert mlxq.workspace_size(m, n, k, gs, bits) == splits * m * n * 4
     wq, s, b = make_layer(90 + bits + gs + n, n, k, gs, bits)
     x = bf16_acts(91 + splits, m, k)
     bias = orc.f32_to_bf16(orc.normal(92, n, 0, 1))
     ref = orc.qmatmul_f64(x, wq, s, b, gs, bits) + orc.bf16_to_f32(bias)[None, :]
-    assert rel_err(run(x, wq, s, b, gs, bits, mlxq.ALGO_QMM, bias=bias), ref) <= TIGHT
+    # the bf16 rounding of each dequantized weight adds noise growing as sqrt(K)
+    assert rel_err(run(x, wq, s, b, gs, bits, mlxq.ALGO_QMM, bias=bias), ref) <= TIGHT * (k / 4096) ** 0.5
 
 
 @pytest.mark.parametrize("bits", [4, 8])
-@pytest.mark.parametrize("cfg", [4, 6, 7, 9, 10, 14, 15])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+@pytest.mark.parametrize("cfg", [82, 42])
 @pytest.mark.parametrize("n", [448, 300])
-def test_qmm_tile_configs(torch_gpu, monkeypatch, bits, cfg, n):
-    """Every qmm workgroup tile the dispatcher picks (256x256 / 128x128 in
-    32x32 MFMA tiles, 256x224 in 16x16 ones; plain, ping-pong and ping-pong
-    with the weights three steps ahead) with a bias, M and N not multiples
-    of the tile (K = 512: 8 K steps, the deep form's even count)."""
+def test_qmm_tile_configs(torch_gpu, monkeypatch, bits, gs, cfg, n):
+    """Both qmm workgroup tiles (256 and 128 activation rows, four waves
+    along N) with a bias, M and N not multiples of the tile (N = 300: the
+    element-wise store tail), K = 2048 (four unrolled periods)."""
     monkeypatch.setenv("MLXQ_QMM_CFG", str(cfg))
     monkeypatch.setenv("MLXQ_QMM_SPLIT", "1")
-    m, k = 300, 512
-    wq, s, b = make_layer(95 + bits + n, n, k, 64, bits)
+    m, k = 300, 2048
+    wq, s, b = make_layer(95 + bits + n + gs, n, k, gs, bits)
     x = bf16_acts(96 + cfg, m, k)
     bias = orc.f32_to_bf16(orc.normal(97, n, 0, 1))
-    ref = orc.qmatmul_f64(x, wq, s, b, 64, bits) + orc.bf16_to_f32(bias)[None, :]
-    assert rel_err(run(x, wq, s, b, 64, bits, mlxq.ALGO_QMM, bias=bias), ref) <= TIGHT
+    ref = orc.qmatmul_f64(x, wq, s, b, gs, bits) + orc.bf16_to_f32(bias)[None, :]
+    assert rel_err(run(x, wq, s, b, gs, bits, mlxq.ALGO_QMM, bias=bias), ref) <= TIGHT
 
 
 def test_bias_vector(torch_gpu):
@@ -148,14 +150,17 @@ def test_bias_vector(torch_gpu):
         assert rel_err(run(x, wq, s, b, 64, 4, algo, bias=bias), ref) <= TIGHT
 
 
+@pytest.mark.parametrize("algo", ["auto", "qmm"])
 @pytest.mark.parametrize("name", ["gate_up", "down"])
-def test_qmm_config3_prefill(torch_gpu, name):
-    """Config 3: M=2048, Q4 g64, 0.1% outlier input channels x20; the oracle
+def test_qmm_config3_prefill(torch_gpu, name, algo):
+    """Config 3: M=2048, Q4 g64, 0.1% outlier input channels x20, on the
+    default route and forced onto the hand-written qmm kernel (256-row tiles
+    for gate/up, 128-row tiles for down; 64 and 224 K steps); the oracle
     checks a seeded sample of 64 rows (rows are independent)."""
     k, n = LLAMA[name]
     wq, s, b = make_layer(0x5EED0300 + k, n, k, 64, 4, outlier_cols=(k + 999) // 1000)
     x = bf16_acts(0x5EED0301, 2048, k)
-    y = run(x, wq, s, b, 64, 4)
+    y = run(x, wq, s, b, 64, 4, mlxq.ALGO_QMM if algo == "qmm" else mlxq.ALGO_AUTO)
     rows = np.sort(np.random.default_rng(3).choice(2048, 64, replace=False))
     ref = orc.qmatmul_f64(x[rows], wq, s, b, 64, 4)
     err = rel_err(y[rows], ref)
@@ -164,7 +169,7 @@ def test_qmm_config3_prefill(torch_gpu, name):
     # weight to bf16 (the values MLX's qmm stages), and with the x20 outlier
     # channels the largest outputs are far above the typical one, so the
     # outputs near 1% of the largest carry relative errors of several %
-    print(f"prefill {name}: rel_err {err:.2e}, elementwise {elem:.2e}")
+    print(f"prefill {name} ({algo}): rel_err {err:.2e}, elementwise {elem:.2e}")
     assert err <= TIGHT, err
 
 
