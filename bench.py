@@ -33,15 +33,41 @@ import seeded  # noqa: E402  (SplitMix64 / Box-Muller inputs; torch is imported 
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, published
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, published
 METRIC = "Q4/Q8 qmatmul GB/s & TFLOP/s (% roofline), Llama-3-8B proj shapes, 1 GPU"
-# measured HBM traffic per launch (bytes) of a dominant-kernel candidate, keyed (bits, M, K, N)
-TRAFFIC_BYTES = {(8, 32, 4096, 14336): 65_808_266}
-# measured HBM traffic per call of the Q4 g64 M=1 GEMV, by projection shape
-# (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated; profiles/qmv_q4_m1_traffic.md)
-HEADLINE_TRAFFIC = {"q": 9_584_354, "k": 2_482_332, "v": 2_482_332, "o": 9_584_354, "gate": 33_209_997,
-                    "up": 33_209_997, "down": 33_357_387}
-# MFMA busy fraction of the prefill qmm calls from SQ counters
-# (SQ_VALU_MFMA_BUSY_CYCLES / (SIMDs x GRBM_GUI_ACTIVE); profiles/qmm_prefill_m2048_mfma_counters.md)
-PREFILL_MFMA_BUSY = {"gate_up": 0.408, "down": 0.468}
+PROFILES = ROOT / "profiles"
+
+
+def profile_facts():
+    """Measured figures committed under profiles/: every ```json block of a
+    profiles/*.md holds facts {"kind", "bits", "m", "k", "n", "algo", "route",
+    "value"}, "route" being what mlxq_qmatmul_route named for the measured
+    call when the counters were read."""
+    import re
+
+    facts = []
+    for f in sorted(PROFILES.glob("*.md")):
+        for blk in re.findall(r"```json\n(.*?)```", f.read_text(), re.S):
+            d = json.loads(blk)
+            for fact in d if isinstance(d, list) else [d]:
+                fact["file"] = f"profiles/{f.name}"
+                facts.append(fact)
+    return facts
+
+
+def algos(mlxq):
+    return {"auto": mlxq.ALGO_AUTO, "qmm": mlxq.ALGO_QMM, "lib": mlxq.ALGO_QMM_LIB}
+
+
+def measured(facts, mlxq, kind, bits, m, k, n, algo="auto"):
+    """The committed figure of `kind` for this call if it was measured on the
+    kernels the call runs now; None (with the reason) otherwise."""
+    route = mlxq.qmatmul_route(m, n, k, GS, bits, algos(mlxq)[algo])
+    for f in facts:
+        if (f["kind"], f["bits"], f["m"], f["k"], f["n"], f.get("algo", "auto")) == (kind, bits, m, k, n, algo):
+            if f["route"] == route:
+                return f["value"], f["file"]
+            return None, f"{f['file']} measured {f['route']!r}; the call now runs {route!r}"
+    return None, "not measured"
+
 
 # (name, K, N): y[M, N] = x[M, K] . W[N, K]^T
 PROJ = [("q", 4096, 4096), ("k", 4096, 1024), ("v", 4096, 1024), ("o", 4096, 4096),
@@ -139,7 +165,7 @@ def main(argv=None) -> int:
     if a.profile_shape:
         bits, m, name, *alg = a.profile_shape.split(",")
         bits, m = int(bits), int(m)
-        algo = {"auto": mlxq.ALGO_AUTO, "qmm": mlxq.ALGO_QMM, "lib": mlxq.ALGO_QMM_LIB}[alg[0] if alg else "auto"]
+        algo = algos(mlxq)[alg[0] if alg else "auto"]
         k, n = {p[0]: (p[1], p[2]) for p in PROJ}[name]
         layers = make_layers(torch, mlxq, bits, 8, 0x5EED0000 + 100 * bits)
         x = seeded.normal(0x5EED1000 + m, m * k, device="cuda").view(m, k).to(torch.bfloat16)
@@ -152,13 +178,15 @@ def main(argv=None) -> int:
         return 0
 
     if a.leg:
-        legs = {"prefill": lambda: bench_prefill(torch, mlxq), "gguf": lambda: bench_gguf(torch, mlxq),
+        legs = {"prefill": lambda: bench_prefill(torch, mlxq, profile_facts()), "gguf": lambda: bench_gguf(torch, mlxq),
                 "decode_stack": lambda: bench_stack(torch)}
         print(json.dumps({a.leg: legs[a.leg]()}), flush=True)
         return 0
 
     torch.manual_seed(0)
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    mlxq.check_build()  # refuses a library built from other sources than this tree's
+    facts = profile_facts()
     dev = torch.device("cuda:0")
     weights = {bits: make_layers(torch, mlxq, bits, LAYERS, 0x5EED0000 + 100 * bits) for bits in BITS}
     xs = {(m, k): seeded.normal(0x5EED1000 + 100000 * m + k, m * k, device=dev).view(m, k).to(torch.bfloat16)
@@ -257,38 +285,25 @@ def main(argv=None) -> int:
     (dbits, dm, (dk, dn)), (dt, dc, dbytes) = max(shapes.items(), key=lambda kv: kv[1][0])
     avg_us = dt / dc
     achieved = dbytes / (avg_us * 1e-6) / 1e9
-    # which kernels serve the call (the dispatch rule of qmatmul.cpp /
-    # qmv_tile.hip, restated here for the label only)
-    if row_route(dm, dn, dk, dbits):
-        kname = "qmv_row_kernel (vector ALU, whole rows per wave)"
-    elif dot_preferred(dm, dn, dk, dbits):
-        kname = "qmv_dot_kernel (vector ALU)"
-    elif tile_preferred(dm, dn, dk, dbits) and stream_splits(dm, dn, dk, dbits) == 1:
-        kname = "qmv_stream_kernel (MFMA, a workgroup streams its rows over the whole K; one launch)"
-    elif tile_preferred(dm, dn, dk, dbits) and stream_splits(dm, dn, dk, dbits):
-        kname = "qmv_stream_kernel + split_reduce4_kernel (MFMA, K in 4 splits; one call = both launches)"
-    elif _short_fullk(dm, dn, dk, dbits):
-        kname = "qmv_tile_kernel (MFMA, whole K per workgroup; one launch)"
-    elif tile_preferred(dm, dn, dk, dbits):
-        kname = "qmv_tile_kernel + split_reduce4_kernel (MFMA, split K; one call = both launches)"
-    else:
-        kname = "qmv_kernel (MFMA)"
-    # HBM bytes per call from rocprofv3 FETCH_SIZE / WRITE_SIZE
-    # runs (scaled by a 64 MiB copy's readings), profiles/qmv_stream_q8_m32_gate_traffic.md;
-    # known for that call only
-    traffic = TRAFFIC_BYTES.get((dbits, dm, dk, dn))
+    # the kernels that serve the call, from the library's own dispatch, and
+    # the HBM bytes per call that rocprofv3 FETCH_SIZE + WRITE_SIZE read for
+    # them (copy-calibrated), when they were measured on these kernels
+    kname = mlxq.qmatmul_route(dm, dn, dk, GS, dbits)
+    traffic, traffic_src = measured(facts, mlxq, "traffic_bytes", dbits, dm, dk, dn)
     roofline = {"kernel": f"{kname}, Q{dbits} g64, M={dm}, K={dk} -> N={dn}", "bound": "hbm",
                 "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_source": traffic_src,
                 "avg_launch_us": round(avg_us, 3), "algorithmic_bytes_per_launch": int(dbytes),
                 "share_of_step": round(dt * LAYERS / (ms_per_step * 1e3), 3)}
     # the north-star headline: Q4 g64 decode GEMV (M=1) at each projection shape
-    headline = {nm: {"us": round(per[(4, 1, nm)][0], 2),
-                     "GB/s": round(per[(4, 1, nm)][1] / per[(4, 1, nm)][0] / 1e3, 1),
-                     "frac_hbm": round(per[(4, 1, nm)][1] / per[(4, 1, nm)][0] / 1e3 / HBM_PEAK_GBS, 3),
-                     "algorithmic_bytes": per[(4, 1, nm)][1], "traffic": HEADLINE_TRAFFIC[nm],
-                     "traffic_ratio": round(HEADLINE_TRAFFIC[nm] / per[(4, 1, nm)][1], 3)}
-                for nm, _, _ in PROJ}
+    headline = {}
+    for nm, k, n in PROJ:
+        us, nbytes = per[(4, 1, nm)]
+        tr, tr_src = measured(facts, mlxq, "traffic_bytes", 4, 1, k, n)
+        headline[nm] = {"us": round(us, 2), "GB/s": round(nbytes / us / 1e3, 1),
+                        "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 3), "algorithmic_bytes": nbytes,
+                        "route": mlxq.qmatmul_route(1, n, k, GS, 4), "traffic": tr, "traffic_source": tr_src,
+                        "traffic_ratio": round(tr / nbytes, 3) if tr else None}
     q4m1 = kernels["q4_m1"]
     del copies
     torch.cuda.empty_cache()
@@ -310,7 +325,7 @@ def main(argv=None) -> int:
     }
 
     if not a.quick:
-        out["prefill"] = bench_prefill(torch, mlxq)
+        out["prefill"] = bench_prefill(torch, mlxq, facts)
         out["gguf"] = bench_gguf(torch, mlxq)
         out["decode_stack"] = bench_stack(torch)
     if not a.quick and not a.no_cpu_baseline:
@@ -319,19 +334,25 @@ def main(argv=None) -> int:
     return 0
 
 
-def bench_prefill(torch, mlxq, iters=10):
-    """Config 3: M=2048 bf16 x Q4 g64 weights, gate/up (4096->14336) and down (14336->4096)."""
+def bench_prefill(torch, mlxq, facts, iters=10):
+    """Config 3: M=2048 bf16 x Q4 g64 weights, gate/up (4096->14336) and
+    down (14336->4096), ceil(0.001 K) outlier input channels x20.  Times the
+    default route of mlxq_qmatmul and, beside it, the hand-written MFMA
+    kernel forced (ALGO_QMM, what the no-alloc entry point runs) and the
+    library's plain bf16 GEMM on already dequantized weights (a reference
+    point outside the path)."""
     res = {}
+    m = 2048
     for name, k, n in (("gate_up", 4096, 14336), ("down", 14336, 4096)):
         w = seeded.normal(0x5EED0300 + k, n * k, 0.0, 0.02, device="cuda").view(n, k)
-        # ceil(0.001 K) outlier input channels, chosen by the seeded stream, x20
         cols = seeded.choice(0x5EED0700 + k, k, (k + 999) // 1000)
         w[:, cols] *= 20
         wq, s, b = mlxq.quantize(w.to(torch.bfloat16), 64, 4)
-        x = seeded.normal(0x5EED0400 + k, 2048 * k, device="cuda").view(2048, k).to(torch.bfloat16)
-        y = torch.empty((2048, n), device="cuda", dtype=torch.bfloat16)
-        def timed(algo):
-            fn = mlxq.bind_qmatmul(x, wq, s, b, 64, 4, out=y, algo=algo)
+        x = seeded.normal(0x5EED0400 + k, m * k, device="cuda").view(m, k).to(torch.bfloat16)
+        y = torch.empty((m, n), device="cuda", dtype=torch.bfloat16)
+        flops = 2 * m * n * k
+
+        def timed(fn):
             for _ in range(100):  # the first launches of a ~300 us kernel run below full clocks (~30 ms to settle)
                 fn()
             torch.cuda.synchronize()
@@ -346,136 +367,166 @@ def bench_prefill(torch, mlxq, iters=10):
                 reps.append(e0.elapsed_time(e1) * 1e3 / iters)
             return sorted(reps)[len(reps) // 2]
 
-        # the default route (mlxq_qmatmul): at M = 2048 the weight dequantized
-        # into the workspace + hipBLASLt's bf16 GEMM; beside it the fused
-        # LDS-dequant MFMA kernel (what the no-alloc entry point runs)
-        lib_route = mlxq.workspace_size(2048, n, k, 64, 4) >= n * k * 2
-        us = timed(mlxq.ALGO_AUTO)
-        us_fused = timed(mlxq.ALGO_QMM)
-        tf = 2.0 * 2048 * n * k / (us * 1e-6) / 1e12
-        tf_fused = 2.0 * 2048 * n * k / (us_fused * 1e-6) / 1e12
-        res[name] = {"us": round(us, 1), "TFLOP/s": round(tf, 1), "frac_mfma_bf16": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
-                     "route": "dequantize + hipBLASLt bf16 GEMM" if lib_route else "fused qmm_kernel",
-                     "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
-                                  "unit": "TFLOP/s", "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
-                                  "flops_per_launch": 2 * 2048 * n * k},
-                     "fused_qmm": {"us": round(us_fused, 1), "TFLOP/s": round(tf_fused, 1),
-                                   "frac_mfma_bf16": round(tf_fused / MFMA_BF16_PEAK_TFLOPS, 4),
-                                   "mfma_busy_counter": PREFILL_MFMA_BUSY[name]}}
-        # reference point, not part of the path: the library's plain bf16 GEMM
-        # (torch -> hipBLASLt) of the same shape on already dequantized weights
+        def entry(us, route):
+            tf = flops / (us * 1e-6) / 1e12
+            return {"route": route, "us": round(us, 1), "TFLOP/s": round(tf, 1),
+                    "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
+                                 "unit": "TFLOP/s", "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                                 "flops_per_launch": flops}}
+
+        r = entry(timed(mlxq.bind_qmatmul(x, wq, s, b, 64, 4, out=y)), mlxq.qmatmul_route(m, n, k, 64, 4))
+        hw = entry(timed(mlxq.bind_qmatmul(x, wq, s, b, 64, 4, out=y, algo=mlxq.ALGO_QMM)),
+                   mlxq.qmatmul_route(m, n, k, 64, 4, mlxq.ALGO_QMM))
+        busy, src = measured(facts, mlxq, "mfma_busy", 4, m, k, n, "qmm")
+        hw["mfma_busy_counter"], hw["mfma_busy_source"] = busy, src
+        r["hand_written_qmm"] = hw
         wd = w.to(torch.bfloat16)
-        for _ in range(5):
-            torch.matmul(x, wd.t(), out=y)
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(iters):
-            torch.matmul(x, wd.t(), out=y)
-        e1.record()
-        torch.cuda.synchronize()
-        lib_tf = 2.0 * 2048 * n * k / (e0.elapsed_time(e1) * 1e3 / iters * 1e-6) / 1e12
-        res[name]["library_bf16_gemm_TFLOP/s"] = round(lib_tf, 1)
+        lib_us = timed(lambda: torch.matmul(x, wd.t(), out=y))
+        r["library_bf16_gemm_TFLOP/s"] = round(flops / (lib_us * 1e-6) / 1e12, 1)
+        res[name] = r
         del w, wd, wq, s, b, x, y
     return res
 
 
-def bench_gguf(torch, mlxq, iters=10):
-    """Config 4: 14336x4096 tensor per type; synthetic blocks (random codes, finite f16 scales)."""
+# ---- config 4 inputs: GGUF blocks quantized from seeded N(0, 0.02) on the
+# device (torch), llama.cpp block layouts as the reference decodes them
+# (src/gguf/dequant.rs): only the input generator of the gguf leg ----
+IQ4NL_VALUES = (-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113)
+
+
+def _f16_bytes(torch, d):
+    """f16 little-endian bytes of a [nb] float tensor -> [nb, 2] uint8."""
+    return d.to(torch.float16).contiguous().view(torch.uint8).view(-1, 2)
+
+
+def _signed_absmax(torch, x):
+    """The element of largest magnitude (with its sign) along the last axis."""
+    return x.gather(-1, x.abs().argmax(-1, keepdim=True)).squeeze(-1)
+
+
+def _nibbles(torch, lo, hi):
+    return (lo | (hi << 4)).to(torch.uint8)
+
+
+def _nearest_iq4(torch, v):
+    t = torch.tensor(IQ4NL_VALUES, dtype=torch.float32, device=v.device)
+    return (v.unsqueeze(-1) - t).abs().argmin(-1)
+
+
+def gguf_blocks(torch, tname, x):
+    """Blocks of GGUF type `tname` for the f32 values x (on any device)."""
+    f = torch.float32
+    if tname == "Q8_0":
+        xb = x.view(-1, 32)
+        d = xb.abs().amax(-1) / 127
+        q = torch.round(xb * torch.where(d != 0, 1 / d, 0).unsqueeze(-1)).clamp(-128, 127).to(torch.int8)
+        return torch.cat([_f16_bytes(torch, d), q.view(torch.uint8)], 1).view(-1)
+    if tname == "Q4_0":
+        xb = x.view(-1, 32)
+        d = _signed_absmax(torch, xb) / -8
+        q = torch.floor(xb * torch.where(d != 0, 1 / d, 0).unsqueeze(-1) + 8.5).clamp(0, 15).to(torch.int32)
+        return torch.cat([_f16_bytes(torch, d), _nibbles(torch, q[:, :16], q[:, 16:])], 1).view(-1)
+    if tname == "IQ4_NL":
+        xb = x.view(-1, 32)
+        d = _signed_absmax(torch, xb) / -127
+        dq = d.to(torch.float16).to(f)
+        i = _nearest_iq4(torch, xb * torch.where(dq != 0, 1 / dq, 0).unsqueeze(-1))
+        return torch.cat([_f16_bytes(torch, d), _nibbles(torch, i[:, :16], i[:, 16:])], 1).view(-1)
+    if tname == "IQ4_XS":
+        xb = x.view(-1, 8, 32)
+        dsub = _signed_absmax(torch, xb) / -127
+        d = _signed_absmax(torch, dsub) / -32
+        dq = d.to(torch.float16).to(f)
+        lv = torch.round(dsub * torch.where(dq != 0, 1 / dq, 0).unsqueeze(-1)).clamp(-32, 31).to(torch.int32) + 32
+        sl = _nibbles(torch, lv[:, 0::2] & 15, lv[:, 1::2] & 15)                    # [nb, 4]
+        sh = ((lv >> 4) & 3) << (2 * torch.arange(8, device=x.device, dtype=torch.int32))
+        sh = sh.sum(-1).to(torch.int32)
+        shb = torch.stack([sh & 255, sh >> 8], 1).to(torch.uint8)
+        dl = dq.unsqueeze(-1) * (lv - 32).to(f)
+        i = _nearest_iq4(torch, xb * torch.where(dl != 0, 1 / dl, 0).unsqueeze(-1))  # [nb, 8, 32]
+        qs = _nibbles(torch, i[..., :16], i[..., 16:]).view(-1, 128)
+        return torch.cat([_f16_bytes(torch, d), shb, sl, qs], 1).view(-1)
+    if tname == "Q4_K":
+        xb = x.view(-1, 8, 32)
+        lo = xb.amin(-1).clamp(max=0)
+        sc, mn = (xb.amax(-1) - lo) / 15, -lo
+        d, dmin = sc.amax(-1) / 63, mn.amax(-1) / 63
+        dq, dmq = d.to(torch.float16).to(f), dmin.to(torch.float16).to(f)
+        ls = torch.where(dq.unsqueeze(-1) > 0, torch.round(sc / dq.unsqueeze(-1)), 0).clamp(0, 63).to(torch.int32)
+        lm = torch.where(dmq.unsqueeze(-1) > 0, torch.round(mn / dmq.unsqueeze(-1)), 0).clamp(0, 63).to(torch.int32)
+        s = torch.cat([ls[:, :4] | ((ls[:, 4:] >> 4) << 6), lm[:, :4] | ((lm[:, 4:] >> 4) << 6),
+                       (ls[:, 4:] & 15) | ((lm[:, 4:] & 15) << 4)], 1).to(torch.uint8)        # [nb, 12]
+        dl, ml = dq.unsqueeze(-1) * ls.to(f), dmq.unsqueeze(-1) * lm.to(f)
+        q = torch.where(dl.unsqueeze(-1) > 0, torch.round((xb + ml.unsqueeze(-1)) / dl.unsqueeze(-1)), 0)
+        q = q.clamp(0, 15).to(torch.int32).view(-1, 4, 2, 32)
+        qs = _nibbles(torch, q[:, :, 0], q[:, :, 1]).view(-1, 128)
+        return torch.cat([_f16_bytes(torch, d), _f16_bytes(torch, dmin), s, qs], 1).view(-1)
+    if tname == "Q6_K":
+        xb = x.view(-1, 16, 16)
+        sb = _signed_absmax(torch, xb) / -32
+        d = sb.abs().amax(-1) / 127
+        dq = d.to(torch.float16).to(f)
+        sc = torch.where(dq.unsqueeze(-1) > 0, torch.round(sb / dq.unsqueeze(-1)), 0).clamp(-128, 127)
+        dl = (dq.unsqueeze(-1) * sc).unsqueeze(-1)
+        q = torch.where(dl != 0, torch.round(xb / dl), 0).clamp(-32, 31).to(torch.int32) + 32
+        q = q.view(-1, 2, 4, 32)                                                      # [nb, half, quarter, l]
+        ql = torch.stack([(q[:, :, 0] & 15) | ((q[:, :, 2] & 15) << 4),
+                          (q[:, :, 1] & 15) | ((q[:, :, 3] & 15) << 4)], 2).to(torch.uint8).view(-1, 128)
+        qh = ((q[:, :, 0] >> 4) | ((q[:, :, 1] >> 4) << 2) | ((q[:, :, 2] >> 4) << 4) | ((q[:, :, 3] >> 4) << 6))
+        qh = qh.to(torch.uint8).view(-1, 64)
+        return torch.cat([ql, qh, sc.to(torch.int8).view(torch.uint8), _f16_bytes(torch, d)], 1).view(-1)
+    raise ValueError(tname)
+
+
+GGUF_LEG_TYPES = ("Q4_0", "Q8_0", "Q4_K", "Q6_K", "IQ4_NL", "IQ4_XS")
+
+
+def bench_gguf(torch, mlxq, iters=3):
+    """Config 4: a 14336 x 4096 tensor per type, blocks quantized from seeded
+    N(0, 0.02).  Enough copies of the blocks are cycled (>= 512 MB, twice the
+    256 MB MALL) that every launch reads its input from HBM; outputs go to
+    two alternating buffers."""
     res = {}
-    n = 14336 * 4096
-    g = torch.Generator(device="cuda")
-    g.manual_seed(0x5EED0400)
-    d_off = {"Q4_0": [0], "Q8_0": [0], "Q4_K": [0, 2], "Q6_K": [208], "IQ4_NL": [0], "IQ4_XS": [0]}
-    out32 = torch.empty(n, device="cuda", dtype=torch.float32)
-    out16 = torch.empty(n, device="cuda", dtype=torch.bfloat16)
-    for tname, offs in d_off.items():
+    rows, cols = 14336, 4096
+    n = rows * cols
+    out32 = [torch.empty(n, device="cuda", dtype=torch.float32) for _ in range(2)]
+    out16 = [torch.empty(n, device="cuda", dtype=torch.bfloat16) for _ in range(2)]
+    rq = [mlxq.gguf_requantize(mlxq.GGUF_TAGS["Q8_0"], torch.zeros(n // 32 * 34, dtype=torch.uint8, device="cuda"),
+                               rows, cols, 0, 64, 4) for _ in range(2)]
+
+    def timed(fns):
+        for f in fns:
+            f(0)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for r in range(iters):
+            for i, f in enumerate(fns):
+                f((i + r) & 1)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / (iters * len(fns))
+
+    for tname in GGUF_LEG_TYPES:
         tag = mlxq.GGUF_TAGS[tname]
-        be, bb = mlxq.gguf_block(tag)
-        nblk = n // be
-        raw = torch.randint(0, 256, (nblk, bb), generator=g, device="cuda", dtype=torch.uint8)
-        for o in offs:  # f16 scale ~ 2^-7 .. 2^-5, positive
-            raw[:, o] = torch.randint(0, 256, (nblk,), generator=g, device="cuda", dtype=torch.uint8)
-            raw[:, o + 1] = 0x20 + torch.randint(0, 8, (nblk,), generator=g, device="cuda", dtype=torch.uint8)
-        raw = raw.reshape(-1).contiguous()
-        entry = {}
-        for oname, o, ob in (("f32", out32, 4), ("bf16", out16, 2)):
-            mlxq.gguf_dequantize(tag, raw, n, out=o)
-            torch.cuda.synchronize()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
-            for _ in range(iters):
-                mlxq.gguf_dequantize(tag, raw, n, out=o)
-            e1.record()
-            torch.cuda.synchronize()
-            us = e0.elapsed_time(e1) * 1e3 / iters
+        x = seeded.normal(0x5EED0400 + tag, n, 0.0, 0.02, device="cuda")
+        raw = gguf_blocks(torch, tname, x)
+        del x
+        assert raw.numel() == mlxq.gguf_tensor_byte_len(tag, n)
+        copies = [raw] + [raw.clone() for _ in range(max(0, -(-(512 << 20) // raw.numel()) - 1))]
+        entry = {"input_copies": len(copies)}
+        for oname, outs, ob in (("f32", out32, 4), ("bf16", out16, 2)):
+            us = timed([lambda j, c=c: mlxq.gguf_dequantize(tag, c, n, out=outs[j]) for c in copies])
             gbs = (raw.numel() + n * ob) / (us * 1e-6) / 1e9
             entry[oname] = {"us": round(us, 1), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 3)}
         # config 4's tail: the fused convert straight to MLX Q4 g64 (dequant ->
         # bf16 -> requant in one pass; bytes = GGUF in + codes/scales/biases out)
-        rq = mlxq.gguf_requantize(tag, raw, 14336, 4096, 0, 64, 4)
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(iters):
-            mlxq.gguf_requantize(tag, raw, 14336, 4096, 0, 64, 4, out=rq)
-        e1.record()
-        torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) * 1e3 / iters
+        us = timed([lambda j, c=c: mlxq.gguf_requantize(tag, c, rows, cols, 0, 64, 4, out=rq[j]) for c in copies])
         gbs = (raw.numel() + n // 2 + 2 * 2 * (n // 64)) / (us * 1e-6) / 1e9
         entry["requant_q4g64"] = {"us": round(us, 1), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 3)}
         res[tname] = entry
-        del raw
+        del raw, copies
     return res
-
-
-def _short_fullk(m, n, k, bits):
-    """short_fullk of qmv_tile.hip: the whole-K form on short matrices."""
-    if n * k >= 1 << 25 or m < (6 if n <= 2048 else 8 if bits == 4 else 12):
-        return False
-    ch = k * bits // 8 // 64
-    if ch % 8 or not (ch // 8 == 4 or (bits == 8 and ch // 8 == 8)):
-        return False
-    cdiv = lambda a, b: -(-a // b)  # noqa: E731
-    return cdiv(n, 16) * cdiv(m, 16) <= 256 or (bits == 4 and ch // 4 == 8 and cdiv(n, 32) * cdiv(m, 16) <= 256)
-
-
-def tile_preferred(m, n, k, bits):
-    """The decode kernel choice of qmv_tile.hip (qmv_tile_preferred), for labels."""
-    large = n * k >= 1 << 25
-    if m <= 4:
-        return large and k < n and m >= (3 if bits == 4 else 4)
-    if _short_fullk(m, n, k, bits):
-        return True
-    if large:
-        return k < n or m >= (8 if bits == 4 else 9)
-    if n <= 2048:
-        return m >= 16
-    return m > 16
-
-
-def stream_splits(m, n, k, bits):
-    """K splits of the streaming form where qmv_tile.hip's stream_preferred
-    takes it (0: not taken), for labels."""
-    if n * k < 1 << 25 or m < (3 if k < n else 8):
-        return 0
-    if k < n:
-        return 1
-    return 4 if m >= 16 or (bits == 8 and m > 8) else 0
-
-
-def row_route(m, n, k, bits):
-    """The whole-row kernel's share of qmatmul.cpp's dispatch (M = 1, 2, Q8
-    gate/up-like at 3, short matrices at 2..4), for labels."""
-    if m > 4 or (m > 1 and k > 4096) or (k * bits // 8) % 1024:
-        return False
-    gate_like = k < n and n * k >= 1 << 25
-    return m == 1 or (m == 2 and not (bits == 4 and gate_like)) or (m == 3 and bits == 8 and gate_like) or n <= 2048
-
-
-def dot_preferred(m, n, k, bits):
-    """qmv_dot_preferred of qmv_tile.hip, for labels."""
-    return m == 1 or (m == 2 and n * k >= 1 << 25 and k < n)
 
 
 def bench_stack(torch, steps=20, batches=(1, 16)):
@@ -506,96 +557,106 @@ def bench_stack(torch, steps=20, batches=(1, 16)):
         return {"ms_per_step": round(ms, 3), "tokens_per_s": round(b / (ms * 1e-3), 1),
                 "weight_GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 3)}
 
-    fused_b1 = None
     for b in batches:
         graph = st.capture(b)
         res[f"batch{b}"] = timed(graph, b)
-        if b == 1:
-            fused_b1 = st.logits[:1].float().clone()
         del graph
-    # the single-launch persistent step (mlxq_decode_step), batch 1.  Its
-    # barrier error flag is sticky: a plan that timed out leaves every later
-    # replay at its first barrier, so the leg fails instead of reporting a
-    # time for unverified logits; the logits are checked against the fused
-    # launches' on the same input.
-    graph = st.capture(1, persistent=True)
-    r = timed(graph, 1)
-    torch.cuda.synchronize()
-    if st.persistent_plan().timed_out():
-        raise RuntimeError("persistent decode step timed out at a grid barrier (workgroups not co-resident)")
-    if fused_b1 is not None:
-        pers = st.logits[:1].float()
-        r["rel_err_vs_fused"] = float((pers - fused_b1).abs().max() / fused_b1.abs().max().clamp_min(1e-30))
-        # two chains that differ only in summation order end ~3e-2 apart
-        # after 32 layers (the chain amplifies bf16 rounding differences)
-        if not r["rel_err_vs_fused"] <= 6e-2:
-            raise RuntimeError(f"persistent decode logits differ from the fused chain: {r['rel_err_vs_fused']}")
-    res["batch1_persistent"] = r
-    res["batch1_persistent"]["kernel"] = "decode_step_kernel (one launch, grid barrier between the 129 stages)"
-    del graph
     del st
     torch.cuda.empty_cache()
     return res
 
 
 def cpu_baseline(torch, weights, xs, seconds):
-    """The oracle's OpenMP dequant-on-the-fly GEMV (a port of the reference's
-    CPU path) on the Q4 M=1 projections of one layer, repeated for ~`seconds`."""
+    """The oracle's OpenMP dequant-on-the-fly GEMV (oracle/baseline.c, the
+    reference's CPU arithmetic: per-group scale * (x . q) + bias * sum(x)) on
+    bounded samples of the measured workloads, ~`seconds` in total:
+      config 2: one layer's 7 projections per (Q4 / Q8, M), the sweep's weights
+      config 3: 32 of the 2048 rows, Q4 g64 gate/up and down shapes
+      config 5: one decoder layer at batch 1 (norms, 7 projections, SwiGLU, residuals)
+      config 4: Q4_K block dequant of the full 14336 x 4096 tensor, one thread
+    """
     import numpy as np
 
     sys.path.insert(0, str(ROOT / "oracle"))
     import oracle as orc
 
     threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
-    layer = weights[4][0]
-    host = {}
-    for name, k, n in PROJ:
-        wq, s, b = layer[name]
-        host[name] = (wq.cpu().numpy().view(np.uint32), s.cpu().view(torch.int16).numpy().view(np.uint16),
-                      b.cpu().view(torch.int16).numpy().view(np.uint16))
-    xh = {k: xs[(1, k)].cpu().view(torch.int16).numpy().view(np.uint16) for k in {p[1] for p in PROJ}}
-    nbytes, reps = 0, 0
-    t0 = time.perf_counter()
-    while time.perf_counter() - t0 < seconds or reps == 0:
-        for name, k, n in PROJ:
-            wq, s, b = host[name]
-            orc.qmatmul_f32(xh[k], wq, s, b, 64, 4, threads=threads)
-            nbytes += qbytes(1, n, k, 4)
-        reps += 1
-    dt = time.perf_counter() - t0
-    out = {"value": round(nbytes / dt / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
-           "sample": f"Q4 g64 M=1, the 7 projections of one layer, {reps} passes in {dt:.1f} s "
-                     f"(oracle/baseline.c orc_qmatmul_f32, {threads} OpenMP threads)",
-           "host_cpus": os.cpu_count()}
-    # the same GEMV on one core, and the reference's scalar GGUF dequant
-    # (src/gguf/dequant.rs, restated in oracle/oracle.c) on one core, a few
-    # seconds each
-    nbytes, reps, t0 = 0, 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds / 4 or reps == 0:
-        for name, k, n in PROJ:
-            wq, s, b = host[name]
-            orc.qmatmul_f32(xh[k], wq, s, b, 64, 4, threads=1)
-            nbytes += qbytes(1, n, k, 4)
-        reps += 1
-    dt = time.perf_counter() - t0
-    out["single_core"] = {"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s", "cores": 1,
-                          "sample": f"the same GEMV, {reps} passes in {dt:.1f} s"}
+    threads = min(threads, 16)
+    u16 = lambda t: t.cpu().view(torch.int16).numpy().view(np.uint16)  # noqa: E731
+    host = {bits: {name: (weights[bits][0][name][0].cpu().numpy().view(np.uint32), u16(weights[bits][0][name][1]),
+                          u16(weights[bits][0][name][2])) for name, _, _ in PROJ} for bits in BITS}
+    xh = {(m, k): u16(xs[(m, k)]) for m in MS for k in {p[1] for p in PROJ}}
+
+    def run(fn, budget):
+        reps, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < budget or reps == 0:
+            fn()
+            reps += 1
+        return reps, time.perf_counter() - t0
+
+    t_all = time.perf_counter()
+    out = {"unit": "GB/s", "cores": threads, "kind": "port", "host_cpus": os.cpu_count()}
+    sweep = {}
+    for bits in BITS:
+        for m in MS:
+            def layer():
+                for name, k, n in PROJ:
+                    orc.qmatmul_f32(xh[(m, k)], *host[bits][name], GS, bits, threads=threads)
+            reps, dt = run(layer, seconds * 0.04)
+            nb = sum(qbytes(m, n, k, bits) for _, k, n in PROJ)
+            sweep[f"q{bits}_m{m}"] = {"GB/s": round(reps * nb / dt / 1e9, 2), "passes": reps, "s": round(dt, 2)}
+    out["config2"] = sweep
+    # the headline figure: config 2 as the bench's `value` weighs it (every
+    # (bits, M) pass moves its own bytes), from the per-entry rates
+    tot_b = sum(qbytes(m, n, k, bits) for bits in BITS for m in MS for _, k, n in PROJ)
+    tot_s = sum(sum(qbytes(m, n, k, bits) for _, k, n in PROJ) / (sweep[f"q{bits}_m{m}"]["GB/s"] * 1e9)
+                for bits in BITS for m in MS)
+    out["value"] = round(tot_b / tot_s / 1e9, 2)
+    out["sample"] = (f"config 2: one layer's 7 projections per (Q4/Q8 g64, M in {{1,4,16,32}}), "
+                     f"oracle/baseline.c orc_qmatmul_f32 on {threads} OpenMP threads")
+    c3 = {}
+    for name, pj in (("gate_up", "gate"), ("down", "down")):
+        k, n = {p[0]: (p[1], p[2]) for p in PROJ}[pj]
+        xr = u16(seeded.normal(0x5EED0400 + k, 32 * k).view(32, k).to(torch.bfloat16))
+        reps, dt = run(lambda: orc.qmatmul_f32(xr, *host[4][pj], GS, 4, threads=threads), seconds * 0.05)
+        c3[name] = {"TFLOP/s": round(reps * 2 * 32 * n * k / dt / 1e12, 4), "rows": 32, "passes": reps}
+    out["config3_sampled_rows"] = c3
+    d = 4096
+    rng = np.random.default_rng(5)
+    ln = orc.f32_to_bf16(1 + 0.1 * rng.standard_normal(d).astype(np.float32))
+    x1 = xh[(1, 4096)]
+
+    def dec_layer():
+        h1 = orc.rms_norm(x1, ln, 1e-5)
+        q = orc.qmatmul_f32(h1, *host[4]["q"], GS, 4, threads=threads)
+        kk = orc.qmatmul_f32(h1, *host[4]["k"], GS, 4, threads=threads)
+        v = orc.f32_to_bf16(orc.qmatmul_f32(h1, *host[4]["v"], GS, 4, threads=threads))
+        attn = orc.repeat_kv(v, 8, 128, 4)  # attention replaced by v (identity), as the chain does
+        h = orc.add(x1, orc.f32_to_bf16(orc.qmatmul_f32(attn, *host[4]["o"], GS, 4, threads=threads)))
+        h2 = orc.rms_norm(h, ln, 1e-5)
+        g = orc.f32_to_bf16(orc.qmatmul_f32(h2, *host[4]["gate"], GS, 4, threads=threads))
+        u = orc.f32_to_bf16(orc.qmatmul_f32(h2, *host[4]["up"], GS, 4, threads=threads))
+        a = orc.silu_mul(g, u)
+        del q, kk
+        return orc.add(h, orc.f32_to_bf16(orc.qmatmul_f32(a, *host[4]["down"], GS, 4, threads=threads)))
+    reps, dt = run(dec_layer, seconds * 0.1)
+    ms = dt / reps * 1e3
+    out["config5_layer"] = {"ms_per_layer": round(ms, 3), "tokens_per_s_32_layers_no_head": round(1e3 / (32 * ms), 2),
+                            "sample": "one Llama-3-8B decoder layer at batch 1, Q4 g64, attention = identity on v"}
+    # the same config-2 GEMV on one core
+    reps, dt = run(lambda: [orc.qmatmul_f32(xh[(1, k)], *host[4][name], GS, 4, threads=1) for name, k, n in PROJ],
+                   seconds * 0.1)
+    out["single_core_q4_m1"] = {"GB/s": round(reps * sum(qbytes(1, n, k, 4) for _, k, n in PROJ) / dt / 1e9, 3),
+                                "cores": 1, "passes": reps}
+    # config 4: the reference's scalar block loop (src/gguf/dequant.rs,
+    # restated in oracle/oracle.c) on one thread, blocks quantized from
+    # seeded N(0, 0.02) as the GPU leg's
     n = 14336 * 4096
-    be, bb = orc.gguf_block(12)  # Q4_K
-    rng = np.random.default_rng(0x5EED0400)
-    raw = rng.integers(0, 256, (n // be, bb), dtype=np.uint8)
-    for o in (0, 2):  # f16 d / dmin ~ 2^-7 .. 2^-5, positive
-        raw[:, o + 1] = 0x20 + rng.integers(0, 8, n // be, dtype=np.uint8)
-    raw = raw.reshape(-1)
-    reps, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds / 4 or reps == 0:
-        orc.gguf_dequantize(12, raw, n, threads=1)
-        reps += 1
-    dt = time.perf_counter() - t0
-    gb = reps * (raw.size + 4 * n) / 1e9
-    out["gguf_dequant_single_core"] = {"value": round(gb / dt, 3), "unit": "GB/s", "cores": 1,
-                                       "sample": f"Q4_K 14336x4096 to f32, {reps} passes in {dt:.1f} s "
-                                                 "(oracle/oracle.c, the reference's block loop, one thread)"}
+    raw = orc.gguf_quantize(12, orc.normal(0x5EED0400 + 12, n, 0.0, 0.02))
+    reps, dt = run(lambda: orc.gguf_dequantize(12, raw, n, threads=1), seconds * 0.1)
+    out["config4_gguf_q4k_single_core"] = {"GB/s": round(reps * (raw.size + 4 * n) / dt / 1e9, 3), "cores": 1,
+                                           "passes": reps, "sample": "Q4_K 14336x4096 -> f32"}
+    out["total_s"] = round(time.perf_counter() - t_all, 1)
     return out
 
 

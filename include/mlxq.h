@@ -139,10 +139,14 @@ int mlxq_qmatmul_algo(const void* x, int64_t M, const uint32_t* wq,
 /* mlxq_qmatmul for callers that cannot allocate or pass a workspace (code
  * under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc).  No counterpart in the reference.  Same kernels and results as
- * mlxq_qmatmul with a workspace, except that M > 32 always takes the fused
- * prefill kernel (MLXQ_ALGO_QMM; the library GEMM path needs a workspace of
- * the whole dequantized weight and a hipBLASLt handle, which allocates), and
- * the split-K partial sums live in a fixed library scratch array in device
+ * mlxq_qmatmul with a workspace, except where mlxq_qmatmul would take the
+ * library GEMM (some shapes above 512 rows; it needs a workspace of the
+ * whole dequantized weight and a hipBLASLt handle, which allocates): there
+ * the qmm kernel runs instead (or 32-row decode calls when K does not suit
+ * it).  So for M > 32: 33..64 rows run as 32-row decode calls, gate/up-like
+ * shapes at 65..128 rows on the 64-row streaming form, the others on qmm
+ * (mlxq_qmatmul_route with noalloc = 1 names the route).  The split-K
+ * partial sums live in a fixed library scratch array in device
  * memory (mlxq_qmatmul_noalloc_max_scratch() bytes, 64 MiB, held by every
  * device the library runs on until the process ends); nothing is allocated.
  * A shape whose workspace size exceeds the scratch returns
@@ -155,6 +159,21 @@ int mlxq_qmatmul_noalloc(const void* x, int64_t M, const uint32_t* wq,
                          const void* scales, const void* biases,
                          const void* bias_vec, int64_t N, int64_t K,
                          int group_size, int bits, void* y, void* stream);
+
+/* The kernels a call of mlxq_qmatmul_algo (noalloc = 0, with a workspace
+ * of workspace_bytes) or of mlxq_qmatmul_noalloc (noalloc = 1) with these
+ * sizes would launch, as a NUL-terminated " + "-separated list of kernel
+ * names with their template arguments (e.g. "qmm_kernel<4, 64, 8, 2>",
+ * "tile::qmv_stream_kernel<8, 64, 2, 8, 4, 2, false> + ...", a library GEMM
+ * as "hipBLASLt GEMM"), into buf.  The library's own dispatch runs with
+ * every launch suppressed, so the answer is the route the call takes, for
+ * labels, measurement bookkeeping and tests.  Launches nothing and touches
+ * no device memory, but needs the device (the dispatch queries occupancy and
+ * the kernel names come from the runtime).  No counterpart in the
+ * reference. */
+int mlxq_qmatmul_route(int64_t M, int64_t N, int64_t K, int group_size,
+                       int bits, size_t workspace_bytes, int algo,
+                       int noalloc, char* buf, size_t buf_len);
 
 /* Size in bytes of mlxq_qmatmul_noalloc's scratch array. */
 size_t mlxq_qmatmul_noalloc_max_scratch(void);
@@ -219,84 +238,6 @@ int mlxq_qmatmul_add_rms_norm(const void* x, int64_t M, const uint32_t* wq,
                               size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------ */
-/* Whole batch-1 decode step in one persistent launch                  */
-/* ------------------------------------------------------------------ */
-
-/* A quantized projection's packed weights (MLX affine layout). */
-typedef struct {
-  const uint32_t* wq;   /* [N, K*bits/32] */
-  const void* scales;   /* [N, K/group_size] bf16 */
-  const void* biases;   /* [N, K/group_size] bf16 */
-} mlxq_qweight;
-
-/* One Llama layer of the decode chain (src/models/llama.rs:689-735). */
-typedef struct {
-  mlxq_qweight q, k, v, o, gate, up, down;
-  const void* ln1;      /* [hidden] bf16, input_layernorm (llama.rs:698)          */
-  const void* ln2;      /* [hidden] bf16, post_attention_layernorm (llama.rs:728) */
-} mlxq_decode_layer;
-
-typedef struct {
-  int32_t layers, hidden, intermediate, heads, kv_heads, head_dim, vocab;
-  int32_t group_size, bits;
-  float eps;
-} mlxq_decode_config;
-
-/* Launch parameters filled by mlxq_decode_plan (host memory, caller-owned). */
-typedef struct {
-  void* workspace;
-  int32_t stages, grid, lds_bytes, max_k, hidden, vocab;
-  int32_t trace;  /* nonzero: the launch records per-stage wall-clock stamps
-                     in the workspace (set from MLXQ_DECODE_TRACE at plan time) */
-  int64_t timeout_ticks;  /* longest grid-barrier wait, in 100 MHz wall-clock
-                             ticks (default 0.5 s; MLXQ_DECODE_TIMEOUT_TICKS
-                             at plan time overrides it, e.g. to force the
-                             time-out path in a test) */
-} mlxq_decode_plan_t;
-
-/* Device workspace bytes for a plan: header, stage table and the per-layer
- * activations (q, k, v, h, SwiGLU output, layer output). */
-int mlxq_decode_plan_size(const mlxq_decode_config* cfg, size_t* bytes);
-
-/* Replaces, for batch 1, the per-layer chain of CausalLm's decode forward
- * (src/models/llama.rs:689-735: rms_norm -> q/k/v (:806-812) -> attention
- * -> o (:829-835) + residual -> rms_norm -> gate/up -> silu*mul -> down
- * (:1040-1045) + residual; final norm + lm_head :595-603) with attention
- * taken as the identity on v repeated to the query heads (one cached
- * position), every projection Q4 g64.  Uploads the stage table into the
- * workspace (synchronous on `stream`; not for use under graph capture) and
- * resets its barrier state.  The workspace must stay allocated and the weight
- * pointers valid while the plan is used.  MLXQ_ERR_UNSUPPORTED: widths not a
- * multiple of 512 (hidden, intermediate, heads*head_dim), bits != 4 or
- * group_size != 64; callers then run the per-projection calls. */
-int mlxq_decode_plan(const mlxq_decode_config* cfg,
-                     const mlxq_decode_layer* layers, const void* final_norm,
-                     const mlxq_qweight* lm_head, void* workspace,
-                     size_t workspace_bytes, mlxq_decode_plan_t* plan,
-                     void* stream);
-
-/* One decode step: x [hidden] bf16 (16-byte aligned, read only) ->
- * logits [vocab] bf16, as the chain of mlxq_rms_norm / mlxq_qmatmul /
- * mlxq_repeat_kv / mlxq_add / mlxq_silu_mul up to f32 summation order.
- * One launch with one workgroup per CU, all resident, synchronising through
- * a grid barrier in the workspace; capturable in a HIP graph.  Calls on one
- * plan must not overlap (they share its barrier and activations).
- * Precondition: the launch's workgroups (one per CU) must all be resident at
- * once, so no other kernel may hold CUs while a step runs (work on another
- * stream or in another process on the same GPU breaks this).  A barrier that
- * waits longer than 0.5 s (workgroups not co-resident) ends the launch
- * without finishing the logits; mlxq_decode_status then reports it, every
- * later step on the plan also ends at its first barrier, and the plan must
- * be made again.  Callers that cannot guarantee co-residency check
- * mlxq_decode_status after a step (a synchronous read). */
-int mlxq_decode_step(const mlxq_decode_plan_t* plan, const void* x,
-                     void* logits, void* stream);
-
-/* *timed_out = 1 if a launch on this plan gave up at a grid barrier
- * (synchronous read of the workspace header). */
-int mlxq_decode_status(const mlxq_decode_plan_t* plan, int* timed_out);
-
-/* ------------------------------------------------------------------ */
 /* Decode layer chain around the projections (bf16, MLX rounding points) */
 /* ------------------------------------------------------------------ */
 
@@ -323,7 +264,8 @@ int mlxq_add(const void* a, const void* b, int64_t n, void* y, void* stream);
  * the next one (src/models/llama.rs:729-733 then :698, or the final norm
  * at :596), in one launch: sum = bf16(a + b) as mlxq_add, y =
  * rms_norm(sum, weight, eps) as mlxq_rms_norm.  a, b, sum, y: [rows, dim]
- * bf16, dim % 8 == 0. */
+ * bf16, dim % 8 == 0.  sum may be a or b (in-place residual update); y may
+ * not alias a, b or sum. */
 int mlxq_add_rms_norm(const void* a, const void* b, const void* weight,
                       int64_t rows, int64_t dim, float eps, void* sum,
                       void* y, void* stream);

@@ -24,6 +24,7 @@ OBJ = PKG / "_build"
 LIB = PKG / "libmlxq.so"
 BIN = PKG / "bin"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+sys.path.insert(0, str(PKG))
 ARCH = "gfx950"
 
 COMMON = [
@@ -46,9 +47,11 @@ def sources() -> list[Path]:
     return srcs
 
 
-def compile_one(src: Path, verbose: bool) -> Path:
+def compile_one(src: Path, verbose: bool, src_hash: str = "unknown") -> Path:
     obj = OBJ / (src.parent.name + "_" + src.name + ".o")
     cmd = [HIPCC, *COMMON]
+    if src.name == "capi.cpp":  # mlxq_version() reports the sources the library was built from
+        cmd.append(f'-DMLXQ_SOURCE_HASH="{src_hash}"')
     if src.name in NO_CONTRACT:
         cmd.append("-ffp-contract=off")
     if src.name in MFMA_VGPR:
@@ -71,8 +74,11 @@ def compile_one(src: Path, verbose: bool) -> Path:
 def build(jobs: int = 8, verbose: bool = False) -> Path:
     OBJ.mkdir(exist_ok=True)
     srcs = sources()
+    from provenance import source_hash
+
+    h = source_hash()
     with cf.ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
-        objs = list(ex.map(lambda s: compile_one(s, verbose), srcs))
+        objs = list(ex.map(lambda s: compile_one(s, verbose, h), srcs))
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", str(tmp), *map(str, objs),
            "-L/opt/rocm/lib", "-lhipblaslt", "-Wl,-rpath,/opt/rocm/lib"]

@@ -144,9 +144,9 @@ template <int DT, int BITS>
 void launch_quant(const void* w, int64_t n_lanes, int group_size, uint32_t* wq, void* s, void* b, hipStream_t st) {
   dim3 grid(ceil_div(n_lanes, kThreads));
   switch (group_size) {
-    case 32: hipLaunchKernelGGL((affine_quantize_kernel<DT, BITS, 4>), grid, dim3(kThreads), 0, st, w, n_lanes, wq, s, b); break;
-    case 64: hipLaunchKernelGGL((affine_quantize_kernel<DT, BITS, 8>), grid, dim3(kThreads), 0, st, w, n_lanes, wq, s, b); break;
-    default: hipLaunchKernelGGL((affine_quantize_kernel<DT, BITS, 16>), grid, dim3(kThreads), 0, st, w, n_lanes, wq, s, b); break;
+    case 32: MLXQ_LAUNCH((affine_quantize_kernel<DT, BITS, 4>), grid, dim3(kThreads), 0, st, w, n_lanes, wq, s, b); break;
+    case 64: MLXQ_LAUNCH((affine_quantize_kernel<DT, BITS, 8>), grid, dim3(kThreads), 0, st, w, n_lanes, wq, s, b); break;
+    default: MLXQ_LAUNCH((affine_quantize_kernel<DT, BITS, 16>), grid, dim3(kThreads), 0, st, w, n_lanes, wq, s, b); break;
   }
 }
 
@@ -186,11 +186,11 @@ extern "C" int mlxq_dequantize(const uint32_t* wq, const void* scales, const voi
   dim3 grid(ceil_div(n_lanes, kThreads));
   const int lpg = group_size / 8;
   if (dtype == MLXQ_F32) {
-    if (bits == 4) hipLaunchKernelGGL((affine_dequantize_kernel<MLXQ_F32, 4>), grid, dim3(kThreads), 0, st, wq, scales, biases, n_lanes, lpg, out);
-    else hipLaunchKernelGGL((affine_dequantize_kernel<MLXQ_F32, 8>), grid, dim3(kThreads), 0, st, wq, scales, biases, n_lanes, lpg, out);
+    if (bits == 4) MLXQ_LAUNCH((affine_dequantize_kernel<MLXQ_F32, 4>), grid, dim3(kThreads), 0, st, wq, scales, biases, n_lanes, lpg, out);
+    else MLXQ_LAUNCH((affine_dequantize_kernel<MLXQ_F32, 8>), grid, dim3(kThreads), 0, st, wq, scales, biases, n_lanes, lpg, out);
   } else {
-    if (bits == 4) hipLaunchKernelGGL((affine_dequantize_kernel<MLXQ_BF16, 4>), grid, dim3(kThreads), 0, st, wq, scales, biases, n_lanes, lpg, out);
-    else hipLaunchKernelGGL((affine_dequantize_kernel<MLXQ_BF16, 8>), grid, dim3(kThreads), 0, st, wq, scales, biases, n_lanes, lpg, out);
+    if (bits == 4) MLXQ_LAUNCH((affine_dequantize_kernel<MLXQ_BF16, 4>), grid, dim3(kThreads), 0, st, wq, scales, biases, n_lanes, lpg, out);
+    else MLXQ_LAUNCH((affine_dequantize_kernel<MLXQ_BF16, 8>), grid, dim3(kThreads), 0, st, wq, scales, biases, n_lanes, lpg, out);
   }
   return check_launch("dequantize");
 }

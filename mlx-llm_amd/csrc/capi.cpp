@@ -4,7 +4,12 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <cxxabi.h>
+#include <string.h>
+
+#include <algorithm>
 #include <atomic>
+#include <functional>
 #include <mutex>
 #include <string>
 
@@ -20,7 +25,45 @@ int fail(int status, const std::string& msg) {
   g_last_error = msg;
   return status;
 }
+namespace {
+thread_local std::string* g_route_log = nullptr;  // non-null while a route query runs on this thread
+}
+bool route_query_active() { return g_route_log != nullptr; }
+void route_query_note(const char* what) {
+  if (!g_route_log) return;
+  if (!g_route_log->empty()) *g_route_log += " + ";
+  *g_route_log += what;
+}
+void route_query_kernel(const void* kern) {
+  if (!g_route_log) return;
+  // the device function's name, demangled, without its argument list,
+  // return type and the library's namespaces: e.g. "qmm_kernel<4, 64, 8, 2>"
+  std::string name = "?";
+  hipFunction_t f = nullptr;
+  if (hipGetFuncBySymbol(&f, kern) == hipSuccess && f) {
+    if (const char* raw = hipKernelNameRef(f)) {
+      int st = 0;
+      char* dm = abi::__cxa_demangle(raw, nullptr, nullptr, &st);
+      name = st == 0 && dm ? dm : raw;
+      free(dm);
+    }
+  }
+  if (name.rfind("void ", 0) == 0) name = name.substr(5);
+  int depth = 0;  // cut the argument list: the last top-level '(' ... ')'
+  for (size_t i = name.size(); i-- > 0;) {
+    if (name[i] == ')') depth++;
+    if (name[i] == '(' && --depth == 0) {
+      name = name.substr(0, i);
+      break;
+    }
+  }
+  for (const std::string pre : {std::string("(anonymous namespace)::"), std::string("mlxq::")}) {
+    for (size_t at; (at = name.find(pre)) != std::string::npos;) name.erase(at, pre.size());
+  }
+  route_query_note(name.c_str());
+}
 int check_launch(const char* what) {
+  if (g_route_log) return MLXQ_OK;  // nothing was launched (MLXQ_LAUNCH recorded it)
   hipError_t e = hipGetLastError();
   if (e != hipSuccess)
     return fail(MLXQ_ERR_DEVICE, std::string(what) + ": " + hipGetErrorString(e));
@@ -101,7 +144,29 @@ extern "C" int mlxq_reload_overrides(void) {
 
 extern "C" const char* mlxq_last_error(void) { return g_last_error.c_str(); }
 
-extern "C" const char* mlxq_version(void) { return "mlxq 0.1.0 (gfx950)"; }
+#ifndef MLXQ_SOURCE_HASH
+#define MLXQ_SOURCE_HASH "unknown"
+#endif
+// The source hash is that of the kernel, host and header sources the
+// library was built from (mlx-llm_amd/build.py), so that a caller can refuse
+// a library built from other sources.
+extern "C" const char* mlxq_version(void) { return "mlxq 0.2.0 (gfx950) src=" MLXQ_SOURCE_HASH; }
+
+namespace mlxq {
+// Run `call` as a route query: launches suppressed, families recorded.
+int run_route_query(const std::function<int()>& call, char* buf, size_t len) {
+  std::string log;
+  g_route_log = &log;
+  const int rc = call();
+  g_route_log = nullptr;
+  if (rc) return rc;
+  if (!buf || len == 0) return fail(MLXQ_ERR_INVALID, "qmatmul_route: null buffer");
+  const size_t n = std::min(log.size(), len - 1);
+  memcpy(buf, log.data(), n);
+  buf[n] = 0;
+  return MLXQ_OK;
+}
+}  // namespace mlxq
 
 // GgmlType::from_tag + block() (src/gguf/dequant.rs:85-141).  The table is
 // the GGUF/ggml on-disk format, so it is necessarily identical.

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <functional>
 #include <string>
 
 #include "../../include/mlxq.h"
@@ -14,8 +15,21 @@ namespace mlxq {
 void set_error(const std::string& msg);
 void clear_error();
 int fail(int status, const std::string& msg);
-// Check the launch that was just enqueued.
+// Check the launch that was just enqueued.  During a route query (below)
+// nothing was enqueued: it records `what` instead.
 int check_launch(const char* what);
+
+// ---- route queries (mlxq_qmatmul_route): the real dispatch runs on dummy
+// pointers with every launch suppressed and recorded by kernel name, so the
+// answer is by construction the route a call takes ----
+bool route_query_active();
+// record a kernel the dispatch would launch (its name from the runtime)
+void route_query_kernel(const void* kern);
+// record a launch that is not one of this library's kernels (library calls)
+void route_query_note(const char* what);
+// run `call` as a route query, the recorded families into buf
+int run_route_query(const std::function<int()>& call, char* buf, size_t len);
+
 
 // Kernel-choice overrides for tuning and tests, from MLXQ_* environment
 // variables.  Read once, on first use (not on every call: the dispatch path
@@ -40,6 +54,16 @@ struct Overrides {
 const Overrides& overrides();
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Every kernel launch of the library goes through this: recorded instead
+// of launched while a route query is active on this thread.
+#define MLXQ_LAUNCH(kern, ...)                                                  \
+  do {                                                                          \
+    if (::mlxq::route_query_active())                                           \
+      ::mlxq::route_query_kernel(reinterpret_cast<const void*>(kern));          \
+    else                                                                        \
+      hipLaunchKernelGGL(kern, __VA_ARGS__);                                    \
+  } while (0)
 
 // ---- device scalar conversions (bit-level, independent of FP modes) ----
 __device__ __forceinline__ float bits_to_f32(uint32_t u) { return __uint_as_float(u); }

@@ -138,10 +138,10 @@ void launch_blocks(const uint8_t* data, int64_t nblocks, void* out, hipStream_t 
   if (chunks == 0) return;
   bool aligned = (reinterpret_cast<uintptr_t>(data) & 15u) == 0;
   if (aligned)
-    hipLaunchKernelGGL((gguf_dequant_kernel<TAG, BF16OUT, true>), dim3(chunks), dim3(kThreads), 0, st, data,
+    MLXQ_LAUNCH((gguf_dequant_kernel<TAG, BF16OUT, true>), dim3(chunks), dim3(kThreads), 0, st, data,
                        nblocks, out);
   else
-    hipLaunchKernelGGL((gguf_dequant_kernel<TAG, BF16OUT, false>), dim3(chunks), dim3(kThreads), 0, st, data,
+    MLXQ_LAUNCH((gguf_dequant_kernel<TAG, BF16OUT, false>), dim3(chunks), dim3(kThreads), 0, st, data,
                        nblocks, out);
 }
 
@@ -149,7 +149,7 @@ template <int TAG, bool BF16OUT>
 void launch_float(const uint8_t* data, int64_t n, void* out, hipStream_t st) {
   int64_t grid = ceil_div(n, static_cast<int64_t>(kThreads));
   if (grid == 0) return;
-  hipLaunchKernelGGL((gguf_float_kernel<TAG, BF16OUT>), dim3(grid), dim3(kThreads), 0, st, data, n, out);
+  MLXQ_LAUNCH((gguf_float_kernel<TAG, BF16OUT>), dim3(grid), dim3(kThreads), 0, st, data, n, out);
 }
 
 template <bool BF16OUT>

@@ -127,7 +127,7 @@ int launch_lpg(int rows, int K, int row_bytes, int perm_hd, const uint8_t* d, ui
                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
     if (e != hipSuccess) return fail(MLXQ_ERR_DEVICE, std::string("gguf_requantize: LDS size: ") + hipGetErrorString(e));
   }
-  hipLaunchKernelGGL(kern, grid, dim3(kThreads), lds, st, d, rows, K, row_bytes, perm_hd, wq, s, b);
+  MLXQ_LAUNCH(kern, grid, dim3(kThreads), lds, st, d, rows, K, row_bytes, perm_hd, wq, s, b);
   return check_launch("gguf_requantize");
 }
 

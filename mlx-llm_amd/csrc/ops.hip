@@ -144,12 +144,13 @@ __global__ void silu_mul_kernel(const uint4* __restrict__ g, const uint4* __rest
 // The residual add of a layer's end and the RMSNorm that starts the next
 // layer (or the final norm) in one pass: one workgroup per row writes
 // s = bf16(a + b) and y = rms_norm(s), each rounded as add_kernel /
-// rms_norm_kernel round it.
-__global__ __launch_bounds__(kNormThreads) void add_rms_norm_kernel(const uint16_t* __restrict__ a,
-                                                                    const uint16_t* __restrict__ b,
+// rms_norm_kernel round it.  s may be a or b (the in-place residual update
+// h = h + x): each element of a and b is read once, by the thread that then
+// writes that element of s, and the second pass reads s back (the same
+// thread's own writes), never a or b.
+__global__ __launch_bounds__(kNormThreads) void add_rms_norm_kernel(const uint16_t* a, const uint16_t* b,
                                                                     const uint16_t* __restrict__ w, int D, float eps,
-                                                                    uint16_t* __restrict__ s,
-                                                                    uint16_t* __restrict__ y) {
+                                                                    uint16_t* s, uint16_t* __restrict__ y) {
   __shared__ float part[kNormThreads / 64];
   const int64_t off = static_cast<int64_t>(blockIdx.x) * D;
   const uint4* ar = reinterpret_cast<const uint4*>(a + off);
@@ -180,12 +181,12 @@ __global__ __launch_bounds__(kNormThreads) void add_rms_norm_kernel(const uint16
   for (int i = 0; i < kNormThreads / 64; i++) tot += part[i];
   const float inv = 1.0f / sqrtf(tot / static_cast<float>(D) + eps);
   for (int i = threadIdx.x; i < pieces; i += kNormThreads) {
-    const uint4 p = ar[i], q = br[i], g = wv[i];
-    const uint32_t pa[4] = {p.x, p.y, p.z, p.w}, qb[4] = {q.x, q.y, q.z, q.w}, gw[4] = {g.x, g.y, g.z, g.w};
+    const uint4 p = sr[i], g = wv[i];  // the sums this thread wrote above
+    const uint32_t sa[4] = {p.x, p.y, p.z, p.w}, gw[4] = {g.x, g.y, g.z, g.w};
     uint32_t o[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-      const uint32_t sv = pack2(lo_f(pa[j]) + lo_f(qb[j]), hi_f(pa[j]) + hi_f(qb[j]));
+      const uint32_t sv = sa[j];
       const float n0 = bf16_bits_to_f32(f32_to_bf16_bits(lo_f(sv) * inv));
       const float n1 = bf16_bits_to_f32(f32_to_bf16_bits(hi_f(sv) * inv));
       o[j] = pack2(lo_f(gw[j]) * n0, hi_f(gw[j]) * n1);
@@ -244,7 +245,7 @@ extern "C" int mlxq_rms_norm(const void* x, const void* weight, int64_t rows, in
               : pt <= 4 ? rms_norm_reg_kernel<4>
               : pt <= 8 ? rms_norm_reg_kernel<8>
                         : rms_norm_kernel;
-  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(rows)), dim3(kNormThreads), 0, as_stream(stream),
+  MLXQ_LAUNCH(kern, dim3(static_cast<unsigned>(rows)), dim3(kNormThreads), 0, as_stream(stream),
                      static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(weight), static_cast<int>(dim),
                      eps, static_cast<uint16_t*>(y));
   return check_launch("rms_norm");
@@ -261,7 +262,7 @@ extern "C" int mlxq_add_rms_norm(const void* a, const void* b, const void* weigh
   if (misaligned(a) || misaligned(b) || misaligned(weight) || misaligned(sum) || misaligned(y))
     return fail(MLXQ_ERR_INVALID, "add_rms_norm: pointers must be 16-byte aligned");
   if (rows > INT32_MAX || dim > INT32_MAX) return fail(MLXQ_ERR_INVALID, "add_rms_norm: too large");
-  hipLaunchKernelGGL(add_rms_norm_kernel, dim3(static_cast<unsigned>(rows)), dim3(kNormThreads), 0,
+  MLXQ_LAUNCH(add_rms_norm_kernel, dim3(static_cast<unsigned>(rows)), dim3(kNormThreads), 0,
                      as_stream(stream), static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b),
                      static_cast<const uint16_t*>(weight), static_cast<int>(dim), eps, static_cast<uint16_t*>(sum),
                      static_cast<uint16_t*>(y));
@@ -277,7 +278,7 @@ extern "C" int mlxq_silu_mul(const void* gate, const void* up, int64_t n, void* 
   if (misaligned(gate) || misaligned(up) || misaligned(y))
     return fail(MLXQ_ERR_INVALID, "silu_mul: pointers must be 16-byte aligned");
   const int64_t n8 = n / 8;
-  hipLaunchKernelGGL(silu_mul_kernel, dim3(grid_for(n8)), dim3(256), 0, as_stream(stream),
+  MLXQ_LAUNCH(silu_mul_kernel, dim3(grid_for(n8)), dim3(256), 0, as_stream(stream),
                      static_cast<const uint4*>(gate), static_cast<const uint4*>(up), n8, static_cast<uint4*>(y));
   return check_launch("silu_mul");
 }
@@ -291,7 +292,7 @@ extern "C" int mlxq_add(const void* a, const void* b, int64_t n, void* y, void* 
   if (misaligned(a) || misaligned(b) || misaligned(y))
     return fail(MLXQ_ERR_INVALID, "add: pointers must be 16-byte aligned");
   const int64_t n8 = n / 8;
-  hipLaunchKernelGGL(add_kernel, dim3(grid_for(n8)), dim3(256), 0, as_stream(stream), static_cast<const uint4*>(a),
+  MLXQ_LAUNCH(add_kernel, dim3(grid_for(n8)), dim3(256), 0, as_stream(stream), static_cast<const uint4*>(a),
                      static_cast<const uint4*>(b), n8, static_cast<uint4*>(y));
   return check_launch("add");
 }
@@ -305,7 +306,7 @@ extern "C" int mlxq_repeat_kv(const void* x, int64_t rows, int kv_heads, int hea
   if (!x || !y) return fail(MLXQ_ERR_INVALID, "repeat_kv: null pointer");
   if (misaligned(x) || misaligned(y)) return fail(MLXQ_ERR_INVALID, "repeat_kv: pointers must be 16-byte aligned");
   const int64_t total = rows * kv_heads * groups * (head_dim / 8);
-  hipLaunchKernelGGL(repeat_kv_kernel, dim3(grid_for(total)), dim3(256), 0, as_stream(stream),
+  MLXQ_LAUNCH(repeat_kv_kernel, dim3(grid_for(total)), dim3(256), 0, as_stream(stream),
                      static_cast<const uint4*>(x), rows, kv_heads, groups, head_dim / 8, static_cast<uint4*>(y));
   return check_launch("repeat_kv");
 }

@@ -353,6 +353,26 @@ extern "C" int mlxq_qmatmul_add_rms_norm(const void* x, int64_t M, const uint32_
   return mlxq_rms_norm(so, norm_weight, M, N, eps, y, stream);
 }
 
+// ---------------------------------------------------------------- route query
+
+extern "C" int mlxq_qmatmul_route(int64_t M, int64_t N, int64_t K, int group_size, int bits, size_t workspace_bytes,
+                                  int algo, int noalloc, char* buf, size_t buf_len) {
+  clear_error();
+  // dummy 256-byte-aligned pointers: nothing is launched or dereferenced
+  void* const p = reinterpret_cast<void*>(uintptr_t(1) << 20);
+  const uint32_t* const wq = static_cast<const uint32_t*>(p);
+  if (noalloc) {
+    const size_t need = fused_workspace_bytes(M, N, K, group_size, bits);
+    return run_route_query([&] { return qmatmul_dispatch(p, M, wq, p, p, nullptr, N, K, group_size, bits, p,
+                                                         need ? p : nullptr, need, MLXQ_ALGO_AUTO, false, nullptr); },
+                           buf, buf_len);
+  }
+  return run_route_query([&] { return qmatmul_dispatch(p, M, wq, p, p, nullptr, N, K, group_size, bits, p,
+                                                       workspace_bytes ? p : nullptr, workspace_bytes, algo, true,
+                                                       nullptr); },
+                         buf, buf_len);
+}
+
 // ---------------------------------------------------------------- no-alloc
 
 namespace {

@@ -495,7 +495,7 @@ int launch(const uint16_t* x, int M, const uint32_t* wq, const uint16_t* s, cons
   }
   const int64_t tiles = ceil_div(N, Gm::BN) * ceil_div(M, Gm::BM);
   dim3 grid(static_cast<unsigned>(8 * ceil_div(tiles, 8)), splits);
-  hipLaunchKernelGGL(kern, grid, dim3(Gm::THREADS), Gm::LDS_BYTES, st, x, M, wq, s, b, bias, N, K, y,
+  MLXQ_LAUNCH(kern, grid, dim3(Gm::THREADS), Gm::LDS_BYTES, st, x, M, wq, s, b, bias, N, K, y,
                      splits > 1 ? part : nullptr, K / splits);
   if (int rc = check_launch("qmm")) return rc;
   if (splits == 1) return MLXQ_OK;

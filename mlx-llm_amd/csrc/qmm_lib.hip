@@ -176,7 +176,8 @@ int launch_qmm_lib(const uint16_t* x, int64_t M, const uint32_t* wq, const uint1
   if (he != hipSuccess || dev < 0 || dev >= kMaxDev)
     return fail(MLXQ_ERR_DEVICE, "qmatmul (library GEMM): no current device");
   const LtPlan* p = nullptr;
-  if (int rc = get_plan(dev, M, N, K, bias != nullptr, &p)) return rc;
+  if (!route_query_active())
+    if (int rc = get_plan(dev, M, N, K, bias != nullptr, &p)) return rc;
 
   uint16_t* wd = static_cast<uint16_t*>(workspace);
   void* ltws = static_cast<char*>(workspace) + weight_bytes(N, K);
@@ -184,12 +185,16 @@ int launch_qmm_lib(const uint16_t* x, int64_t M, const uint32_t* wq, const uint1
   const int gshift = group_size == 32 ? 5 : group_size == 64 ? 6 : 7;
   const dim3 grid(static_cast<unsigned>(ceil_div(units, 1024)));
   if (bits == 4)
-    hipLaunchKernelGGL(dequant_bf16_kernel<4>, grid, dim3(256), 0, st, wq, s, b, reinterpret_cast<u32x4*>(wd), units,
+    MLXQ_LAUNCH(dequant_bf16_kernel<4>, grid, dim3(256), 0, st, wq, s, b, reinterpret_cast<u32x4*>(wd), units,
                        gshift);
   else
-    hipLaunchKernelGGL(dequant_bf16_kernel<8>, grid, dim3(256), 0, st, wq, s, b, reinterpret_cast<u32x4*>(wd), units,
+    MLXQ_LAUNCH(dequant_bf16_kernel<8>, grid, dim3(256), 0, st, wq, s, b, reinterpret_cast<u32x4*>(wd), units,
                        gshift);
   if (int rc = check_launch("qmm_lib dequant")) return rc;
+  if (route_query_active()) {  // no handle, no plan: the GEMM's place in the route only
+    route_query_note("hipBLASLt GEMM");
+    return MLXQ_OK;
+  }
 
   const float alpha = 1.f, beta = 0.f;
   hipblasStatus_t ls;

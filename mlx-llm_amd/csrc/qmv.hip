@@ -456,9 +456,9 @@ void launch_narrow(const QmvPlan& p, const uint16_t* x, int M, const uint32_t* w
                    const uint16_t* b, const uint16_t* bias, int N, int K, uint16_t* y, hipStream_t st) {
   dim3 grid(p.row_tiles);
   switch (p.unroll) {
-    case 1: hipLaunchKernelGGL((qmv_kernel<QmvWaveNarrow, BITS, GS, MT, SUB, 4, 1>), grid, dim3(kThreads), 0, st, x, M, wq, s, b, bias, N, K, y); break;
-    case 2: hipLaunchKernelGGL((qmv_kernel<QmvWaveNarrow, BITS, GS, MT, SUB, 4, 2>), grid, dim3(kThreads), 0, st, x, M, wq, s, b, bias, N, K, y); break;
-    default: hipLaunchKernelGGL((qmv_kernel<QmvWaveNarrow, BITS, GS, MT, SUB, 4, 4>), grid, dim3(kThreads), 0, st, x, M, wq, s, b, bias, N, K, y); break;
+    case 1: MLXQ_LAUNCH((qmv_kernel<QmvWaveNarrow, BITS, GS, MT, SUB, 4, 1>), grid, dim3(kThreads), 0, st, x, M, wq, s, b, bias, N, K, y); break;
+    case 2: MLXQ_LAUNCH((qmv_kernel<QmvWaveNarrow, BITS, GS, MT, SUB, 4, 2>), grid, dim3(kThreads), 0, st, x, M, wq, s, b, bias, N, K, y); break;
+    default: MLXQ_LAUNCH((qmv_kernel<QmvWaveNarrow, BITS, GS, MT, SUB, 4, 4>), grid, dim3(kThreads), 0, st, x, M, wq, s, b, bias, N, K, y); break;
   }
 }
 
@@ -470,7 +470,7 @@ void launch_wide(const QmvPlan& p, const uint16_t* x, int M, const uint32_t* wq,
   constexpr int U = (QmvWaveWide<BITS, GS, MT, SUB, MV>::CPG == 2 ||
                      (BITS == 4 && (MT == 2 || SUB >= 2 || GS == 32))) ? 2 : 4;
   static_assert(SUB <= 2, "wide qmv: at most 2 sub-tiles");
-  hipLaunchKernelGGL((qmv_kernel<QmvWaveWide, BITS, GS, MT, SUB, MV, U>), dim3(p.row_tiles), dim3(kThreads), 0, st, x,
+  MLXQ_LAUNCH((qmv_kernel<QmvWaveWide, BITS, GS, MT, SUB, MV, U>), dim3(p.row_tiles), dim3(kThreads), 0, st, x,
                      M, wq, s, b, bias, N, K, y);
 }
 

@@ -538,7 +538,7 @@ int run(const Cfg& c, const Params& a, hipStream_t st, int* query) {
     *query = cached;
     return MLXQ_OK;
   }
-  hipLaunchKernelGGL(kern, dim3(c.tiles), dim3(64 * WV), c.lds, st, a);
+  MLXQ_LAUNCH(kern, dim3(c.tiles), dim3(64 * WV), c.lds, st, a);
   return check_launch("qmv_dot");
 }
 

@@ -350,7 +350,7 @@ __global__ __launch_bounds__(64 * W) void qmv_row_kernel(const RowParams p) {
 
 template <int BITS, int NI, int R, int W, int MM, int F>
 int launch_rw(const RowParams& a, int64_t tiles, hipStream_t st) {
-  hipLaunchKernelGGL((qmv_row_kernel<BITS, NI, R, W, MM, F>), dim3(static_cast<unsigned>(tiles)), dim3(64 * W), 0, st,
+  MLXQ_LAUNCH((qmv_row_kernel<BITS, NI, R, W, MM, F>), dim3(static_cast<unsigned>(tiles)), dim3(64 * W), 0, st,
                      a);
   return check_launch("qmv_row");
 }

@@ -835,7 +835,7 @@ int launch_split_add_norm(const float* part, const uint16_t* bias, int64_t M, in
               : pt <= 4 ? tile::split_add_norm_kernel<4>
                         : tile::split_add_norm_kernel<8>;
   if (pt > 8) return fail(MLXQ_ERR_UNSUPPORTED, "split_add_norm: rows longer than 16384");
-  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(M)), dim3(256), 0, st, part, bias, ep.res, ep.norm_w, M * N,
+  MLXQ_LAUNCH(kern, dim3(static_cast<unsigned>(M)), dim3(256), 0, st, part, bias, ep.res, ep.norm_w, M * N,
                      static_cast<int>(N), splits, ep.eps, ep.sum_out, ep.y_norm);
   return check_launch("split_add_norm");
 }
@@ -849,11 +849,11 @@ int launch_split_reduce(const float* part, const uint16_t* bias, uint16_t* y, in
                 : splits == 4 ? tile::split_reduce4_kernel<4>
                 : splits == 8 ? tile::split_reduce4_kernel<8>
                               : tile::split_reduce4_kernel<0>;
-    hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(ceil_div(mn4, 256))), dim3(256), 0, st,
+    MLXQ_LAUNCH(kern, dim3(static_cast<unsigned>(ceil_div(mn4, 256))), dim3(256), 0, st,
                        reinterpret_cast<const float4*>(part), bias, reinterpret_cast<uint2*>(y), mn4,
                        static_cast<int>(N), splits);
   } else {
-    hipLaunchKernelGGL(tile::qmv_tile_reduce_kernel, dim3(static_cast<unsigned>(ceil_div(mn, 256))), dim3(256), 0,
+    MLXQ_LAUNCH(tile::qmv_tile_reduce_kernel, dim3(static_cast<unsigned>(ceil_div(mn, 256))), dim3(256), 0,
                        st, part, bias, y, mn, static_cast<int>(N), splits);
   }
   return check_launch("split_reduce");
@@ -883,13 +883,13 @@ int run(const TileParams& a, int tiles, int mblocks, hipStream_t st, int* query)
     *query = cached;
     return MLXQ_OK;
   }
-  hipLaunchKernelGGL(kern, dim3(tiles, a.splits, mblocks), dim3(64 * WV), 0, st, a);
+  MLXQ_LAUNCH(kern, dim3(tiles, a.splits, mblocks), dim3(64 * WV), 0, st, a);
   return check_launch("qmv_tile");
 }
 
 template <int BITS, int MT, int WV, int NCH, int KH, bool SW = false>
 int run_stream(const TileParams& a, int tiles, int mblocks, hipStream_t st) {
-  hipLaunchKernelGGL((qmv_stream_kernel<BITS, 64, MT, WV, NCH, KH, SW>), dim3(tiles, a.splits, mblocks),
+  MLXQ_LAUNCH((qmv_stream_kernel<BITS, 64, MT, WV, NCH, KH, SW>), dim3(tiles, a.splits, mblocks),
                      dim3(64 * WV), 0, st, a);
   return check_launch("qmv_stream");
 }
@@ -1250,13 +1250,13 @@ namespace tile {
 template <int BITS, bool RES>
 int run_fused_r(const Cfg& c, const TileFused& f, int tiles, int mb, hipStream_t st) {
   if (c.kh == 4) {  // two row groups x four K parts (32 rows per workgroup)
-    hipLaunchKernelGGL((qmv_tile_fused_kernel<BITS, 64, 1, 8, BITS == 4 ? 8 : 16, 4, RES>), dim3(tiles, 1, mb),
+    MLXQ_LAUNCH((qmv_tile_fused_kernel<BITS, 64, 1, 8, BITS == 4 ? 8 : 16, 4, RES>), dim3(tiles, 1, mb),
                        dim3(512), 0, st, f);
   } else if (c.nch == 4) {
-    hipLaunchKernelGGL((qmv_tile_fused_kernel<BITS, 64, 1, 8, 4, 8, RES>), dim3(tiles, 1, mb), dim3(512), 0, st, f);
+    MLXQ_LAUNCH((qmv_tile_fused_kernel<BITS, 64, 1, 8, 4, 8, RES>), dim3(tiles, 1, mb), dim3(512), 0, st, f);
   } else {
     if constexpr (BITS == 8)
-      hipLaunchKernelGGL((qmv_tile_fused_kernel<BITS, 64, 1, 8, 8, 8, RES>), dim3(tiles, 1, mb), dim3(512), 0, st, f);
+      MLXQ_LAUNCH((qmv_tile_fused_kernel<BITS, 64, 1, 8, 8, 8, RES>), dim3(tiles, 1, mb), dim3(512), 0, st, f);
   }
   return check_launch("qmv_tile_fused");
 }

@@ -14,6 +14,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <cstdint>
 #include <set>
 #include <sstream>
 
@@ -220,8 +221,12 @@ std::optional<bool> MetaValue::as_bool() const {
 const std::vector<MetaValue>* MetaValue::as_array() const { return type == Type::Array ? &arr : nullptr; }
 
 int64_t TensorInfo::num_elements() const {
+  // checked: the count sizes the tensor's data range and the dequantize call
   int64_t n = 1;
-  for (int64_t d : shape) n *= d;
+  for (int64_t d : shape) {
+    if (d < 0 || (d > 0 && n > INT64_MAX / d)) msg("gguf: tensor too large: " + name);
+    n *= d;
+  }
   return n;
 }
 
@@ -473,6 +478,17 @@ ConvertReport convert(const GgufFile& g, const std::string& out_dir, const Conve
   }
 
   snapshot::Tensors out;
+  // a repeated tensor name replaces the earlier one (the reference collects
+  // the converted tensors in a HashMap, convert.rs:121-137), so the
+  // snapshot never holds a key twice
+  auto put = [&out](const std::string& name, Array a) {
+    for (auto& kv : out)
+      if (kv.first == name) {
+        kv.second = std::move(a);
+        return;
+      }
+    out.emplace_back(name, std::move(a));
+  };
   std::set<std::string> seen;
   int64_t vocab = -1;
   for (const TensorInfo& t : g.tensors) {
@@ -494,9 +510,9 @@ ConvertReport convert(const GgufFile& g, const std::string& out_dir, const Conve
       const QuantizedLinear q =
           requantize_projection(t.ggml_type, blocks, t.shape[0], t.shape[1], perm, *opts.quantize);
       const std::string base = key->substr(0, key->size() - std::strlen(".weight"));
-      out.emplace_back(base + ".weight", q.weight);
-      out.emplace_back(base + ".scales", q.scales);
-      out.emplace_back(base + ".biases", q.biases);
+      put(base + ".weight", q.weight);
+      put(base + ".scales", q.scales);
+      put(base + ".biases", q.biases);
     } else {
       Array dense = dequantize(t.ggml_type, blocks, static_cast<size_t>(n), DType::BF16);
       if (perm) {
@@ -504,7 +520,7 @@ ConvertReport convert(const GgufFile& g, const std::string& out_dir, const Conve
         const std::vector<uint8_t> host = permute_inverse_qk_rows(dense.to_bytes(), rows, cols, perm, 2);
         dense = Array::from_bytes(host.data(), host.size(), t.shape, DType::BF16);
       }
-      out.emplace_back(*key, dense.reshape(t.shape));  // the snapshot stores the torch shape
+      put(*key, dense.reshape(t.shape));  // the snapshot stores the torch shape
     }
   }
   if (vocab < 0) msg("gguf: no token embedding tensor");

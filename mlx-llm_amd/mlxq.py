@@ -46,6 +46,8 @@ SIGNATURES = {
     "mlxq_qmatmul_noalloc": (ctypes.c_int, [_vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, ctypes.c_int, ctypes.c_int,
                                             _vp, _vp]),
     "mlxq_qmatmul_noalloc_max_scratch": (_sz, []),
+    "mlxq_qmatmul_route": (ctypes.c_int, [_i64, _i64, _i64, ctypes.c_int, ctypes.c_int, _sz, ctypes.c_int, ctypes.c_int,
+                                          ctypes.c_char_p, _sz]),
     "mlxq_qmatmul_fused": (ctypes.c_int, [_vp, _i64, _i64, _vp, ctypes.c_float, ctypes.c_int, ctypes.c_int,
                                           ctypes.c_int, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                           ctypes.c_int, _vp]),
@@ -61,10 +63,6 @@ SIGNATURES = {
     "mlxq_gguf_block": (ctypes.c_int, [_u32, ctypes.POINTER(_i64), ctypes.POINTER(_i64)]),
     "mlxq_gguf_tensor_byte_len": (ctypes.c_int, [_u32, _i64, ctypes.POINTER(_i64)]),
     "mlxq_gguf_dequantize": (ctypes.c_int, [_u32, _vp, _i64, _i64, ctypes.c_int, _vp, _vp]),
-    "mlxq_decode_plan_size": (ctypes.c_int, [_vp, ctypes.POINTER(_sz)]),
-    "mlxq_decode_plan": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _sz, _vp, _vp]),
-    "mlxq_decode_step": (ctypes.c_int, [_vp, _vp, _vp, _vp]),
-    "mlxq_decode_status": (ctypes.c_int, [_vp, ctypes.POINTER(ctypes.c_int)]),
 }
 
 
@@ -72,29 +70,6 @@ class Projection(ctypes.Structure):
     """mlxq_projection (include/mlxq.h)."""
     _fields_ = [("wq", _vp), ("scales", _vp), ("biases", _vp), ("bias", _vp), ("residual", _vp), ("y", _vp),
                 ("N", _i64)]
-
-
-class QWeight(ctypes.Structure):
-    """mlxq_qweight (include/mlxq.h)."""
-    _fields_ = [("wq", _vp), ("scales", _vp), ("biases", _vp)]
-
-
-class DecodeLayer(ctypes.Structure):
-    """mlxq_decode_layer (include/mlxq.h)."""
-    _fields_ = [(n, QWeight) for n in ("q", "k", "v", "o", "gate", "up", "down")] + [("ln1", _vp), ("ln2", _vp)]
-
-
-class DecodeConfig(ctypes.Structure):
-    """mlxq_decode_config (include/mlxq.h)."""
-    _fields_ = [(n, ctypes.c_int32) for n in ("layers", "hidden", "intermediate", "heads", "kv_heads", "head_dim",
-                                              "vocab", "group_size", "bits")] + [("eps", ctypes.c_float)]
-
-
-class DecodePlanT(ctypes.Structure):
-    """mlxq_decode_plan_t (include/mlxq.h)."""
-    _fields_ = [("workspace", _vp)] + [(n, ctypes.c_int32) for n in ("stages", "grid", "lds_bytes", "max_k",
-                                                                      "hidden", "vocab", "trace")] + \
-        [("timeout_ticks", ctypes.c_int64)]
 
 
 class MlxqError(RuntimeError):
@@ -137,6 +112,17 @@ def check(rc: int) -> None:
 
 def version() -> str:
     return lib().mlxq_version().decode()
+
+
+def check_build() -> None:
+    """Refuse a libmlxq.so built from sources other than this tree's (a
+    stale build pushed with newer sources): RuntimeError naming both hashes."""
+    from provenance import library_hash, source_hash
+
+    have, want = library_hash(version()), source_hash()
+    if have != want:
+        raise RuntimeError(f"{LIB_PATH} was built from other sources (library src={have}, tree src={want}); "
+                           "rebuild with `python mlx-llm_amd/build.py`")
 
 
 def reload_overrides() -> None:
@@ -234,6 +220,19 @@ def qmatmul(x, wq, scales, biases, group_size: int = 64, bits: int = 4, bias=Non
                                   group_size, bits, _ptr(y), _ptr(ws), 0 if ws is None else ws.numel(),
                                   algo, _stream()))
     return y.reshape(*x.shape[:-1], n)
+
+
+def qmatmul_route(m: int, n: int, k: int, group_size: int = 64, bits: int = 4, algo: int = ALGO_AUTO,
+                  workspace_bytes=None, noalloc: bool = False) -> str:
+    """The kernel families a qmatmul call of this shape launches (the
+    library's own dispatch, run with launches suppressed), e.g.
+    "qmv_stream + split_reduce"; workspace_bytes defaults to what
+    workspace_size() asks for."""
+    if workspace_bytes is None:
+        workspace_bytes = workspace_size(m, n, k, group_size, bits)
+    buf = ctypes.create_string_buffer(256)
+    check(lib().mlxq_qmatmul_route(m, n, k, group_size, bits, workspace_bytes, algo, int(noalloc), buf, len(buf)))
+    return buf.value.decode()
 
 
 def bind_qmatmul(x, wq, scales, biases, group_size: int = 64, bits: int = 4, out=None, bias=None,
@@ -383,40 +382,3 @@ def gguf_requantize(tag: int, data, rows: int, cols: int, permute_heads: int = 0
     check(lib().mlxq_gguf_requantize(tag, _ptr(data), data.numel(), rows, cols, permute_heads, group_size, bits,
                                      _ptr(wq), _ptr(s), _ptr(b), _stream()))
     return wq, s, b
-
-
-class DecodePlan:
-    """A persistent batch-1 decode step over a stack's quantized weights
-    (mlxq_decode_plan / mlxq_decode_step).  cfg: dict with layers, hidden,
-    intermediate, heads, kv_heads, head_dim, vocab, group_size, bits, eps;
-    layers: list of dicts {q,k,v,o,gate,up,down: (wq, scales, biases),
-    ln1, ln2}; lm_head: (wq, scales, biases).  Raises Unsupported for widths
-    the persistent kernel does not cover.  The plan keeps its workspace and
-    the tensors it points at alive."""
-
-    def __init__(self, cfg: dict, layers, final_norm, lm_head, device):
-        torch = _torch()
-        self.cfg = DecodeConfig(**{k: cfg[k] for k, _ in DecodeConfig._fields_})
-        size = ctypes.c_size_t(0)
-        check(lib().mlxq_decode_plan_size(ctypes.byref(self.cfg), ctypes.byref(size)))
-        self.workspace = torch.zeros(size.value, dtype=torch.uint8, device=device)
-        qw = lambda t: QWeight(_ptr(t[0]), _ptr(t[1]), _ptr(t[2]))  # noqa: E731
-        arr = (DecodeLayer * len(layers))()
-        for i, L in enumerate(layers):
-            arr[i] = DecodeLayer(*(qw(L[p]) for p in ("q", "k", "v", "o", "gate", "up", "down")), _ptr(L["ln1"]),
-                                 _ptr(L["ln2"]))
-        self._keep = (layers, final_norm, lm_head)
-        self._lm = qw(lm_head)
-        self.plan = DecodePlanT()
-        check(lib().mlxq_decode_plan(ctypes.byref(self.cfg), arr, _ptr(final_norm), ctypes.byref(self._lm),
-                                     _ptr(self.workspace), size.value, ctypes.byref(self.plan), _stream()))
-
-    def step(self, x, logits):
-        """One decode step on the current stream: x [hidden] bf16 -> logits [vocab] bf16."""
-        check(lib().mlxq_decode_step(ctypes.byref(self.plan), _ptr(x), _ptr(logits), _stream()))
-        return logits
-
-    def timed_out(self) -> bool:
-        r = ctypes.c_int(0)
-        check(lib().mlxq_decode_status(ctypes.byref(self.plan), ctypes.byref(r)))
-        return bool(r.value)

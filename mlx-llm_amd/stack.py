@@ -147,18 +147,7 @@ class DecodeStack:
     def _lin(self, x, p: QLinear, out):
         return mlxq.qmatmul(x, p.wq, p.scales, p.biases, self.cfg.group_size, self.cfg.bits, out=out)
 
-    def persistent_plan(self):
-        """The single-launch batch-1 decode step over this stack's weights
-        (mlxq.DecodePlan), made once.  Raises mlxq.Unsupported for widths the
-        persistent kernel does not cover."""
-        if getattr(self, "_plan", None) is None:
-            t = lambda p: (p.wq, p.scales, p.biases)  # noqa: E731
-            layers = [dict({k: t(v) for k, v in L.proj.items()}, ln1=L.ln1, ln2=L.ln2) for L in self.layers]
-            self._plan = mlxq.DecodePlan(self.cfg.as_dict(), layers, self.norm, t(self.lm_head), self.device)
-        return self._plan
-
-    def forward(self, b: int | None = None, fused: bool = True, persistent: bool = False, layers=None,
-                head: bool = True):
+    def forward(self, b: int | None = None, fused: bool = True, layers=None, head: bool = True):
         """One decode step of b rows on the current stream: self.x[:b] -> self.logits[:b].
         fused: per layer, four launches of the fused decode kernel (norm + q/k/v,
         head repeat + o + residual, norm + gate/up + SwiGLU, down + residual)
@@ -167,10 +156,6 @@ class DecodeStack:
         layers (an iterable of layer indices, default all) and head=False run
         part of the chain, for checking it layer by layer: without the head
         the hidden state after the last layer run is returned."""
-        if persistent:
-            assert (self.batch if b is None else b) == 1, "the persistent step is batch 1"
-            assert layers is None and head, "the persistent step runs the whole chain"
-            return self.persistent_plan().step(self.x[0], self.logits[0])
         if not fused:
             return self._forward_ops(b, layers, head)
         c = self.cfg
@@ -301,18 +286,18 @@ class DecodeStack:
         self._lin(n, self.lm_head, self.logits[:b])
         return self.logits[:b]
 
-    def capture(self, b: int | None = None, fused: bool = True, persistent: bool = False):
+    def capture(self, b: int | None = None, fused: bool = True):
         """Capture forward(b) in a HIP graph; returns the graph (replay() runs one step)."""
         import torch
         s = torch.cuda.Stream(device=self.device)
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
-            self.forward(b, fused, persistent)  # warm-up outside the capture (plan, kernel attributes)
+            self.forward(b, fused)  # warm-up outside the capture (kernel attributes)
         torch.cuda.current_stream().wait_stream(s)
         torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, stream=s):
-            self.forward(b, fused, persistent)
+            self.forward(b, fused)
         torch.cuda.synchronize()
         return graph
 

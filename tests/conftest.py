@@ -18,10 +18,25 @@ def pytest_configure(config):
 
 
 def _ensure_built():
+    """Build what is missing; a libmlxq.so built from other sources than this
+    tree's is rebuilt where there is no GPU (the build host) and refused where
+    there is one (GPU runs use the library built beforehand, never a stale one)."""
     if not (ORACLE / "liboracle.so").exists():
         subprocess.run(["make", "-s", "-C", str(ORACLE)], check=True)
     if not (PKG / "libmlxq.so").exists():
         subprocess.run([sys.executable, str(PKG / "build.py")], check=True)
+    from provenance import library_hash, source_hash
+
+    out = subprocess.run([sys.executable, "-c", "import mlxq; print(mlxq.version())"], cwd=str(PKG),
+                         capture_output=True, text=True)
+    if library_hash(out.stdout.strip()) == source_hash():
+        return
+    import torch
+
+    if torch.cuda.device_count() > 0:
+        pytest.exit(f"libmlxq.so is stale ({out.stdout.strip()}, tree src={source_hash()}): "
+                    "rebuild with mlx-llm_amd/build.py before running the GPU tests", returncode=3)
+    subprocess.run([sys.executable, str(PKG / "build.py")], check=True)
 
 
 _ensure_built()

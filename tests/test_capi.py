@@ -118,35 +118,6 @@ def test_workspace_sizes_cover_every_decode_shape():
                 mlxq.workspace_size(m, n, k, 64, bits)
 
 
-def _decode_cfg(**kw):
-    base = dict(layers=32, hidden=4096, intermediate=14336, heads=32, kv_heads=8, head_dim=128, vocab=128256,
-                group_size=64, bits=4, eps=1e-5)
-    base.update(kw)
-    return mlxq.DecodeConfig(**base)
-
-
-def test_decode_plan_size_and_unsupported_widths():
-    """Workspace = 256 B header + stage table (4 per layer + lm_head) + per-layer
-    activations padded to 1 KB; Q8, other group sizes and widths that are not
-    multiples of 512 are rejected before anything touches a device."""
-    L = mlxq.lib()
-    size = ctypes.c_size_t(0)
-    cfg = _decode_cfg()
-    assert L.mlxq_decode_plan_size(ctypes.byref(cfg), ctypes.byref(size)) == mlxq.OK
-    per_layer = (4096 + 1024 + 1024 + 4096 + 14336 + 4096) * 2
-    assert size.value > 32 * per_layer and size.value < 32 * per_layer + (8 << 20)
-    size2 = ctypes.c_size_t(0)
-    assert L.mlxq_decode_plan_size(ctypes.byref(_decode_cfg(layers=2)), ctypes.byref(size2)) == mlxq.OK
-    assert size.value - size2.value >= 30 * per_layer
-    for bad in (dict(bits=8), dict(group_size=32), dict(hidden=4000), dict(intermediate=14000)):
-        assert L.mlxq_decode_plan_size(ctypes.byref(_decode_cfg(**bad)), ctypes.byref(size)) == \
-            mlxq.ERR_UNSUPPORTED, bad
-    assert L.mlxq_decode_plan_size(ctypes.byref(_decode_cfg(heads=30)), ctypes.byref(size)) == mlxq.ERR_SHAPE
-    assert L.mlxq_decode_plan_size(ctypes.byref(_decode_cfg(layers=0)), ctypes.byref(size)) == mlxq.ERR_INVALID
-    assert L.mlxq_decode_plan_size(None, ctypes.byref(size)) == mlxq.ERR_INVALID
-    assert L.mlxq_decode_step(None, None, None, None) == mlxq.ERR_INVALID
-
-
 def test_header_compiles_as_c99(tmp_path):
     """include/mlxq.h is a plain C header (the boundary binds from C / cgo /
     bindgen): it compiles alone under -std=c99 -pedantic with warnings as errors."""

@@ -28,7 +28,7 @@ HF = {"attn_q": "self_attn.q_proj", "attn_k": "self_attn.k_proj", "attn_v": "sel
       "ffn_down": "mlp.down_proj"}
 
 
-def make_model(path, seed=0x6600):
+def make_model(path, seed=0x6600, extra=()):
     tensors, src = [], {}
     w = orc.normal(seed, VOCAB * H, 0.0, 0.02)
     tensors.append(("token_embd.weight", [VOCAB, H], 1, w.astype(np.float16).view(np.uint8)))
@@ -43,6 +43,7 @@ def make_model(path, seed=0x6600):
             tensors.append((f"blk.{i}.{nm}.weight", list(shape), tag, data))
     for name, shape, tag, data in tensors:
         src[name] = (shape, tag, np.asarray(data, np.uint8))
+    tensors += list(extra)
     meta = [("general.architecture", gi.STRING, "llama"), ("llama.embedding_length", gi.U32, H),
             ("llama.block_count", gi.U32, LAYERS), ("llama.attention.head_count", gi.U32, HEADS),
             ("llama.attention.head_count_kv", gi.U32, KV), ("llama.feed_forward_length", gi.U32, FFN),
@@ -126,3 +127,39 @@ def test_convert_file_matches_reference_chain(tmp_path, quant):
             want_keys.add(base + ".weight")
             assert np.array_equal(st[base + ".weight"], dense_bf16(shape, tag, data, heads)), base
     assert set(st) == want_keys
+
+
+def test_convert_repeated_tensor_name_last_wins(tmp_path):
+    """A GGUF naming one tensor twice: the snapshot holds the key once, with
+    the later tensor's data (the reference collects the converted tensors
+    by name, convert.rs:121-137)."""
+    gg = tmp_path / "dup.gguf"
+    tag, shape = PROJ["attn_q"]
+    again = orc.gguf_quantize(tag, orc.normal(0x6677, shape[0] * shape[1], 0.0, 0.02))
+    make_model(gg, extra=[("blk.0.attn_q.weight", list(shape), tag, again)])
+    out = tmp_path / "snap"
+    r = subprocess.run([str(CLI), str(gg), str(out), "--quant", "q4"], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
+    header_len = int.from_bytes((out / "model.safetensors").read_bytes()[:8], "little")
+    header = json.loads((out / "model.safetensors").read_bytes()[8:8 + header_len])
+    keys = [k for k in header if k != "__metadata__"]
+    assert len(keys) == len(set(keys))
+    st = load(out)
+    wq, s, b = orc.gguf_requantize(tag, again, shape[0], shape[1], HEADS, 64, 4)
+    base = "model.layers.0.self_attn.q_proj"
+    for suf, w in ((".weight", wq), (".scales", s), (".biases", b)):
+        assert np.array_equal(st[base + suf].reshape(w.shape), w), base + suf
+
+
+def test_convert_rejects_oversized_tensor(tmp_path):
+    """Dimensions whose product overflows 64 bits are refused by name, before
+    anything is sized from the count."""
+    gg = tmp_path / "big.gguf"
+    meta = [("general.architecture", gi.STRING, "llama"), ("llama.embedding_length", gi.U32, 32),
+            ("llama.block_count", gi.U32, 1), ("llama.attention.head_count", gi.U32, 1),
+            ("llama.attention.head_count_kv", gi.U32, 1), ("llama.feed_forward_length", gi.U32, 32)]
+    tensors = [("token_embd.weight", [1 << 40, 1 << 40], 0, np.zeros(64, np.uint8))]
+    gi.write(gg, meta, tensors)
+    r = subprocess.run([str(CLI), str(gg), str(tmp_path / "o")], capture_output=True, text=True, timeout=120)
+    assert r.returncode != 0
+    assert "tensor too large: token_embd.weight" in r.stderr, r.stderr

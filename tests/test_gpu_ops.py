@@ -47,6 +47,24 @@ def test_add_rms_norm(torch_gpu, rows, dim):
     assert np.array_equal(host(y), host(mlxq.rms_norm(s2, dev(w, True), 1e-5)))
 
 
+@pytest.mark.parametrize("alias", ["a", "b"])
+@pytest.mark.parametrize("rows,dim", [(16, 4096), (3, 14336), (2, 8)])
+def test_add_rms_norm_in_place(torch_gpu, alias, rows, dim):
+    """sum written over one of its inputs (the residual update h = h + x):
+    the same sum and norm as with a separate output."""
+    a = orc.f32_to_bf16(orc.normal(510 + rows, rows * dim, 0.0, 2.0)).reshape(rows, dim)
+    b = orc.f32_to_bf16(orc.normal(511 + rows, rows * dim, 0.0, 1.0)).reshape(rows, dim)
+    w = orc.f32_to_bf16(orc.normal(512 + dim, dim, 1.0, 0.2))
+    ad, bd = dev(a, True), dev(b, True)
+    s, y = mlxq.add_rms_norm(ad, bd, dev(w, True), 1e-5, sum_out=ad if alias == "a" else bd)
+    want_s = orc.add(a, b)
+    assert np.array_equal(host(s), want_s)
+    assert np.array_equal(host(ad if alias == "a" else bd), want_s)
+    _ulp_close(host(y), orc.rms_norm(want_s, w, 1e-5))
+    s2, y2 = mlxq.add_rms_norm(dev(a, True), dev(b, True), dev(w, True), 1e-5)
+    assert np.array_equal(host(y), host(y2))
+
+
 def test_silu_mul(torch_gpu):
     n = 16 * 14336
     g = orc.f32_to_bf16(orc.normal(300, n, 0.0, 3.0))

@@ -370,3 +370,19 @@ def test_qmm_small_grids_split_on_narrow_tiles(torch_gpu, bits, name, m):
     y = run(x, wq, s, b, 64, bits, mlxq.ALGO_QMM)
     cols = np.sort(np.random.default_rng(m).choice(n, 128, replace=False))
     assert rel_err(y[:, cols], orc.qmatmul_f64(x, wq[cols], s[cols], b[cols], 64, bits)) <= TIGHT
+
+
+def test_route_query_names_the_kernels(torch_gpu):
+    """mlxq_qmatmul_route runs the library's own dispatch with launches
+    suppressed: the families it names are the route each call takes."""
+    r = mlxq.qmatmul_route
+    assert r(1, 4096, 4096, 64, 4).startswith("row::qmv_row_kernel<4,")           # decode GEMV
+    assert r(2048, 4096, 14336, 64, 4) == "qmm_kernel<4, 64, 4, 2>"              # down-like prefill
+    gate = r(2048, 14336, 4096, 64, 4)                                           # gate/up-like, M >= 1024
+    assert gate.startswith("dequant_bf16_kernel<4>") and gate.endswith(" + hipBLASLt GEMM"), gate
+    assert r(2048, 14336, 4096, 64, 4, algo=mlxq.ALGO_QMM) == "qmm_kernel<4, 64, 8, 2>"
+    assert r(2048, 14336, 4096, 64, 4, noalloc=True) == "qmm_kernel<4, 64, 8, 2>"  # never the library
+    assert r(48, 14336, 4096, 64, 4, noalloc=True) == r(48, 14336, 4096, 64, 4)  # 32-row decode chunks
+    assert r(96, 14336, 4096, 64, 4, noalloc=True) == r(96, 14336, 4096, 64, 4)  # 64-row streaming form
+    assert "split_reduce" in r(512, 4096, 4096, 64, 4)                           # qmm with K split
+    assert r(512, 4096, 4096, 64, 4, workspace_bytes=0) == "qmm_kernel<4, 64, 4, 2>"  # no workspace: unsplit

@@ -58,87 +58,6 @@ def test_llama3_8b_width_two_layers(torch_gpu, batch):
     assert rel_err(orc.bf16_to_f32(got), orc.bf16_to_f32(want).astype(np.float64)) <= TOL
 
 
-# ---- persistent single-launch decode step (mlxq_decode_plan / mlxq_decode_step)
-
-def _persistent(cfg: StackConfig, seeds, graph: bool):
-    """Logits of the persistent step and of the oracle chain for each input
-    seed, on one plan (and one graph when graph=True): later calls must see
-    the new input, not activations left by an earlier call."""
-    st = DecodeStack(cfg, batch=1, seed=11, norm_noise=0.1)
-    layers, norm, lm = st.host_weights()
-    g = None
-    out = []
-    for sd in seeds:
-        x = orc.f32_to_bf16(orc.normal(sd, cfg.hidden, 0.0, 1.0)).reshape(1, cfg.hidden)
-        st.x.copy_(dev(x, True))
-        if graph:
-            if g is None:
-                g = st.capture(1, persistent=True)
-            g.replay()
-        else:
-            st.forward(1, persistent=True)
-        got = host(st.logits).copy()
-        want = orc.decode_stack(x, layers, norm, lm, cfg.as_dict())
-        out.append((got, want))
-    assert not st.persistent_plan().timed_out()
-    return st, out
-
-
-@pytest.mark.parametrize("graph", [False, True])
-def test_persistent_small(torch_gpu, graph):
-    _, res = _persistent(StackConfig(**SMALL), [501, 502, 503], graph)
-    for got, want in res:
-        assert rel_err(orc.bf16_to_f32(got), orc.bf16_to_f32(want).astype(np.float64)) <= TOL
-
-
-def test_persistent_llama3_8b_width_two_layers(torch_gpu):
-    """Config-5 widths, two layers, three inputs through one captured graph;
-    also against the fused multi-launch chain on the same weights."""
-    st, res = _persistent(StackConfig(layers=2), [601, 602, 603], graph=True)
-    for got, want in res:
-        e = rel_err(orc.bf16_to_f32(got), orc.bf16_to_f32(want).astype(np.float64))
-        print("rel_err", e)
-        assert e <= TOL
-    pers = orc.bf16_to_f32(res[-1][0]).astype(np.float64)
-    st.forward(1, fused=True)
-    fused = orc.bf16_to_f32(host(st.logits))
-    assert rel_err(pers, fused.astype(np.float64)) <= TOL
-
-
-def test_persistent_unsupported(torch_gpu):
-    import mlxq
-    st = DecodeStack(StackConfig(bits=8, **SMALL), batch=1, seed=3)
-    with pytest.raises(mlxq.Unsupported):
-        st.persistent_plan()
-
-
-def test_persistent_barrier_timeout_path(torch_gpu, monkeypatch):
-    """Failure handling forced from the host: a 1-tick barrier wait limit
-    makes the grid barriers give up.  Every wave leaves the launch (the
-    bounded waits end it; nothing hangs), the plan reports the time-out, the
-    logits hold NaN, and a fresh plan on the same weights computes the step
-    correctly again."""
-    import torch
-    cfg = StackConfig(**SMALL)
-    st = DecodeStack(cfg, batch=1, seed=13, norm_noise=0.1)
-    x = orc.f32_to_bf16(orc.normal(777, cfg.hidden, 0.0, 1.0)).reshape(1, cfg.hidden)
-    st.x.copy_(dev(x, True))
-    monkeypatch.setenv("MLXQ_DECODE_TIMEOUT_TICKS", "1")
-    st.logits.zero_()
-    st.forward(1, persistent=True)
-    torch.cuda.synchronize()
-    assert st.persistent_plan().timed_out()
-    assert torch.isnan(st.logits.float()).any()  # a timed-out step leaves NaN logits, not stale ones
-    monkeypatch.delenv("MLXQ_DECODE_TIMEOUT_TICKS")
-    st._plan = None  # a new plan: the barrier state starts over
-    st.forward(1, persistent=True)
-    torch.cuda.synchronize()
-    assert not st.persistent_plan().timed_out()
-    layers, norm, lm = st.host_weights()
-    want = orc.decode_stack(x, layers, norm, lm, cfg.as_dict())
-    assert rel_err(orc.bf16_to_f32(host(st.logits)), orc.bf16_to_f32(want).astype(np.float64)) <= TOL
-
-
 # ---- config 5 at its real depth: 32 Llama-3-8B layers + the 128256-row lm_head
 
 @pytest.fixture(scope="module")
@@ -168,8 +87,8 @@ CHAIN_TOL_32 = 6e-2
 @pytest.mark.parametrize("batch", [1, 16])
 def test_llama3_8b_full_depth(torch_gpu, llama3_8b_stack, batch):
     """The whole config-5 decode step (32 layers, Q4 g64 projections and
-    lm_head) as the bench times it -- fused launches captured in a HIP graph,
-    and at batch 1 also the persistent single launch -- against the oracle's
+    lm_head) as the bench times it -- fused launches captured in a HIP graph --
+    against the oracle's
     f64 chain of the same ops on the same packed weights.  Then layer by
     layer: each of the 32 layers (and the head) run on the GPU from the GPU's
     own input state and compared with the oracle's layer on that state."""
@@ -188,15 +107,6 @@ def test_llama3_8b_full_depth(torch_gpu, llama3_8b_stack, batch):
     e_max, e_elem = _errs(fused, want)
     print(f"batch {batch} fused graph, 32 layers: rel_err {e_max:.3e} (elementwise {e_elem:.3e})")
     assert e_max <= CHAIN_TOL_32
-    if batch == 1:
-        p = st.capture(1, persistent=True)
-        p.replay()
-        p.replay()
-        pers = host(st.logits[:1]).copy()
-        assert not st.persistent_plan().timed_out()
-        e_max, e_elem = _errs(pers, want)
-        print(f"batch 1 persistent graph, 32 layers: rel_err {e_max:.3e} (elementwise {e_elem:.3e})")
-        assert e_max <= CHAIN_TOL_32
     # layer by layer (eager fused launches), each from the GPU's own state
     state = x
     worst = 0.0

@@ -34,7 +34,7 @@ def layer(seed, n, k, bits):
 
 @pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("n,k,m1,m2", [(14336, 4096, 32, 16), (4096, 14336, 16, 5), (1024, 4096, 32, 1),
-                                       (4096, 14336, 2048, 512)])
+                                       (4096, 14336, 2048, 512), (14336, 4096, 96, 48), (14336, 4096, 2048, 96)])
 def test_noalloc_matches_workspace_path(torch_gpu, bits, n, k, m1, m2):
     torch = torch_gpu
     print(f"noalloc bits={bits} n={n} k={k} m={m1},{m2}", flush=True)
@@ -42,9 +42,11 @@ def test_noalloc_matches_workspace_path(torch_gpu, bits, n, k, m1, m2):
     bias = dev(orc.f32_to_bf16(np.random.default_rng(n).normal(0, 1, n).astype(np.float32)), bf16=True)
     for m in (m1, m2):
         x = dev(bf16_acts(0x7100 + m, m, k), bf16=True)
-        # M > 32: the fused prefill kernel, which the no-alloc entry point
-        # always takes (mlxq_qmatmul may take the library GEMM there)
-        want = mlxq.qmatmul(x, wq, s, b, 64, bits, bias=bias, algo=mlxq.ALGO_QMM if m > 32 else mlxq.ALGO_AUTO)
+        # the no-alloc route is mlxq_qmatmul's except where that takes the
+        # library GEMM (the qmm kernel runs there): 33..64 rows in 32-row
+        # decode calls, gate/up-like 65..128 rows on the 64-row streaming form
+        lib = "hipBLASLt" in mlxq.qmatmul_route(m, n, k, 64, bits)
+        want = mlxq.qmatmul(x, wq, s, b, 64, bits, bias=bias, algo=mlxq.ALGO_QMM if lib else mlxq.ALGO_AUTO)
         got = noalloc(x, wq, s, b, n, k, bits, bias)
         torch.cuda.synchronize()
         assert torch.equal(got.view(torch.int16), want.view(torch.int16)), m
