@@ -379,6 +379,9 @@ def bench_prefill(torch, mlxq, facts, iters=10):
                    mlxq.qmatmul_route(m, n, k, 64, 4, mlxq.ALGO_QMM))
         busy, src = measured(facts, mlxq, "mfma_busy", 4, m, k, n, "qmm")
         hw["mfma_busy_counter"], hw["mfma_busy_source"] = busy, src
+        # L2-miss bytes (FETCH_SIZE + WRITE_SIZE, copy-calibrated) per launch
+        hw["roofline"]["traffic"], hw["roofline"]["traffic_source"] = measured(facts, mlxq, "traffic_bytes", 4, m, k, n,
+                                                                              "qmm")
         r["hand_written_qmm"] = hw
         wd = w.to(torch.bfloat16)
         lib_us = timed(lambda: torch.matmul(x, wd.t(), out=y))
