@@ -45,58 +45,80 @@ constexpr bool is_float_tag() {
   return TAG == 0 || TAG == 1 || TAG == 30;
 }
 
-// One workgroup per output row at a time (rows blockIdx.x, + gridDim.x, ...):
-// the source row's GGUF bytes (row sr = the un-permuted source of output row
-// r) are staged in LDS with 16-byte loads when aligned, then every lane
-// decodes 8 consecutive elements from LDS, rounds them to bf16 and
-// quantizes its share of the group.  perm_hd > 0: within head h = r /
-// perm_hd, output row rr = r % perm_hd reads source row h * perm_hd +
-// 2 * (rr % half) + rr / half (half = perm_hd / 2), the inverse of
-// llama.cpp's interleave.
+// 16 bytes per lane from global memory straight into LDS: a wave's active
+// lanes fill lane * 16 bytes from `l` (no registers held while in flight)
+__device__ __forceinline__ void lds_dma16(const uint8_t* g, uint8_t* l) {
+  __builtin_amdgcn_global_load_lds(g, l, 16, 0, 0);
+}
+
+// Source row of output row r: perm_hd > 0 un-permutes llama.cpp's q/k head
+// interleave -- within head h = r / perm_hd, output row rr = r % perm_hd
+// reads source row h * perm_hd + 2 * (rr % half) + rr / half (half =
+// perm_hd / 2).
+__device__ __forceinline__ int source_row(int r, int perm_hd) {
+  if (perm_hd <= 0) return r;
+  const int h = r / perm_hd, rr = r - h * perm_hd, half = perm_hd / 2;
+  return h * perm_hd + 2 * (rr % half) + rr / half;
+}
+
+// A workgroup converts `rpw` consecutive output rows.  All of their source
+// rows' GGUF bytes are requested up front (direct global -> LDS loads when
+// 16-byte aligned, so the bytes in flight per CU are those of every resident
+// workgroup's rows), then every lane decodes 8 consecutive elements of a row
+// from LDS, rounds them to bf16 and quantizes its share of the group.
 template <int TAG, int BITS, int LPG, bool ALIGNED16>
 __global__ __launch_bounds__(kThreads) void gguf_requant_kernel(const uint8_t* __restrict__ data, int rows, int K,
-                                                                 int row_bytes, int perm_hd,
+                                                                 int row_bytes, int perm_hd, int rpw,
                                                                  uint32_t* __restrict__ wq,
                                                                  uint16_t* __restrict__ scales,
                                                                  uint16_t* __restrict__ biases) {
   extern __shared__ __align__(16) uint8_t lds[];
   const int lpr = K / 8;  // lanes (8 elements each) per row
-  for (int r = blockIdx.x; r < rows; r += gridDim.x) {
-    int sr = r;
-    if (perm_hd > 0) {
-      const int h = r / perm_hd, rr = r - h * perm_hd, half = perm_hd / 2;
-      sr = h * perm_hd + 2 * (rr % half) + rr / half;
+  const int r0 = blockIdx.x * rpw;
+  const int nr = min(rpw, rows - r0);
+  const int tid = threadIdx.x;
+  if constexpr (ALIGNED16) {
+    const int n16 = row_bytes >> 4;
+    const int pieces = (n16 + 63) >> 6;  // 1 KB wave loads per row
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    for (int t = wave; t < nr * pieces; t += kThreads / 64) {
+      const int i = t / pieces, p = t - i * pieces, q = p * 64 + lane;
+      const uint8_t* src = data + static_cast<int64_t>(source_row(r0 + i, perm_hd)) * row_bytes;
+      if (q < n16) lds_dma16(src + q * 16, lds + i * row_bytes + p * 1024);
     }
-    const uint8_t* src = data + static_cast<int64_t>(sr) * row_bytes;
-    if constexpr (ALIGNED16) {
-      for (int i = threadIdx.x; i < row_bytes / 16; i += kThreads)
-        reinterpret_cast<uint4*>(lds)[i] = reinterpret_cast<const uint4*>(src)[i];
-    } else {
-      for (int i = threadIdx.x; i < row_bytes; i += kThreads) lds[i] = src[i];
+    __builtin_amdgcn_s_waitcnt(0);
+  } else {
+    for (int i = 0; i < nr; i++) {
+      const uint8_t* src = data + static_cast<int64_t>(source_row(r0 + i, perm_hd)) * row_bytes;
+      for (int j = tid; j < row_bytes; j += kThreads) lds[i * row_bytes + j] = src[j];
     }
-    __syncthreads();
+  }
+  __syncthreads();
+  for (int i = 0; i < nr; i++) {
+    const int r = r0 + i;
+    const uint8_t* row = lds + i * row_bytes;
     // lanes of the row in whole groups per pass (kThreads is a multiple of LPG
     // and lpr of LPG, so a group's lanes are active together)
     for (int l0 = 0; l0 < lpr; l0 += kThreads) {
-      const int l = l0 + threadIdx.x;
+      const int l = l0 + tid;
       const bool active = l < lpr;
       float v[8];
 #pragma unroll
-      for (int i = 0; i < 8; i++) v[i] = 0.f;
+      for (int j = 0; j < 8; j++) v[j] = 0.f;
       if (active) {
         const int e = l * 8;
         if constexpr (is_float_tag<TAG>()) {
 #pragma unroll
-          for (int i = 0; i < 8; i++) v[i] = float_elem<TAG>(lds, e + i);
+          for (int j = 0; j < 8; j++) v[j] = float_elem<TAG>(row, e + j);
         } else {
           constexpr int E = Geo<TAG>::E, B = Geo<TAG>::B;
           const int blk = e / E;
-          const uint8_t* b = lds + blk * B;
+          const uint8_t* b = row + blk * B;
 #pragma unroll
-          for (int i = 0; i < 8; i++) v[i] = decode<TAG>(b, e - blk * E + i);  // 8 never straddle a block
+          for (int j = 0; j < 8; j++) v[j] = decode<TAG>(b, e - blk * E + j);  // 8 never straddle a block
         }
 #pragma unroll
-        for (int i = 0; i < 8; i++) v[i] = static_cast<float>(static_cast<__bf16>(v[i]));  // as_dtype(bf16): v_cvt_pk_bf16_f32, round to nearest even (a NaN payload cannot reach a code: max/min skip NaN and a NaN quotient clamps to 0)
+        for (int j = 0; j < 8; j++) v[j] = static_cast<float>(static_cast<__bf16>(v[j]));  // as_dtype(bf16): v_cvt_pk_bf16_f32, round to nearest even (a NaN payload cannot reach a code: max/min skip NaN and a NaN quotient clamps to 0)
       }
       uint32_t codes[8];
       float scale, bias;
@@ -111,23 +133,29 @@ __global__ __launch_bounds__(kThreads) void gguf_requant_kernel(const uint8_t* _
         }
       }
     }
-    __syncthreads();  // the row's bytes are read before the next row is staged
   }
+}
+
+// Rows per workgroup: as many as fit 32 KB of LDS (at most 8), so that a
+// CU's resident workgroups keep ~100 KB of GGUF bytes in flight.
+inline int rows_per_workgroup(int row_bytes) {
+  return std::max(1, std::min(8, (32 * 1024) / std::max(row_bytes, 1)));
 }
 
 template <int TAG, int BITS, int LPG>
 int launch_lpg(int rows, int K, int row_bytes, int perm_hd, const uint8_t* d, uint32_t* wq, uint16_t* s,
                uint16_t* b, hipStream_t st) {
   const bool al = (reinterpret_cast<uintptr_t>(d) & 15u) == 0 && row_bytes % 16 == 0;
-  const size_t lds = (static_cast<size_t>(row_bytes) + 15) / 16 * 16;
-  const dim3 grid(static_cast<unsigned>(rows));  // one row per workgroup: whole rounds of resident workgroups
+  const int rpw = rows_per_workgroup(row_bytes);
+  const size_t lds = static_cast<size_t>(rpw) * row_bytes;
+  const dim3 grid(static_cast<unsigned>((rows + rpw - 1) / rpw));
   auto kern = al ? gguf_requant_kernel<TAG, BITS, LPG, true> : gguf_requant_kernel<TAG, BITS, LPG, false>;
   if (lds > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
     if (e != hipSuccess) return fail(MLXQ_ERR_DEVICE, std::string("gguf_requantize: LDS size: ") + hipGetErrorString(e));
   }
-  MLXQ_LAUNCH(kern, grid, dim3(kThreads), lds, st, d, rows, K, row_bytes, perm_hd, wq, s, b);
+  MLXQ_LAUNCH(kern, grid, dim3(kThreads), lds, st, d, rows, K, row_bytes, perm_hd, rpw, wq, s, b);
   return check_launch("gguf_requantize");
 }
 
