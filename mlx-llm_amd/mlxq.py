@@ -224,13 +224,13 @@ def qmatmul(x, wq, scales, biases, group_size: int = 64, bits: int = 4, bias=Non
 
 def qmatmul_route(m: int, n: int, k: int, group_size: int = 64, bits: int = 4, algo: int = ALGO_AUTO,
                   workspace_bytes=None, noalloc: bool = False) -> str:
-    """The kernel families a qmatmul call of this shape launches (the
-    library's own dispatch, run with launches suppressed), e.g.
-    "qmv_stream + split_reduce"; workspace_bytes defaults to what
+    """The kernels a qmatmul call of this shape launches (the library's own
+    dispatch, run with launches suppressed), e.g. "qmm_kernel<4, 64, 4, 2> +
+    tile::split_reduce4_kernel<4>"; workspace_bytes defaults to what
     workspace_size() asks for."""
     if workspace_bytes is None:
         workspace_bytes = workspace_size(m, n, k, group_size, bits)
-    buf = ctypes.create_string_buffer(256)
+    buf = ctypes.create_string_buffer(1024)
     check(lib().mlxq_qmatmul_route(m, n, k, group_size, bits, workspace_bytes, algo, int(noalloc), buf, len(buf)))
     return buf.value.decode()
 
