@@ -88,7 +88,6 @@ const Overrides* read_overrides() {
   o->qmv_dot_all = flag("MLXQ_QMV_DOT_ALL");
   o->qmv_tile_all = flag("MLXQ_QMV_TILE_ALL");
   o->qmv_legacy = flag("MLXQ_QMV_LEGACY");
-  o->qmv_stream = flag("MLXQ_QMV_STREAM");
   o->qmv_narrow = flag("MLXQ_QMV_NARROW");
   o->tile_mb = flag("MLXQ_QMV_TILE_MB");
   o->qmv_no_tile_fused = flag("MLXQ_QMV_NO_TILE_FUSED");

@@ -35,7 +35,7 @@ int run_route_query(const std::function<int()>& call, char* buf, size_t len);
 // variables.  Read once, on first use (not on every call: the dispatch path
 // does no environment lookups); mlxq_reload_overrides() reads them again.
 struct Overrides {
-  bool qmv_row_all, qmv_no_row, qmv_mfma, qmv_dot_all, qmv_tile_all, qmv_legacy, qmv_stream, qmv_narrow;
+  bool qmv_row_all, qmv_no_row, qmv_mfma, qmv_dot_all, qmv_tile_all, qmv_legacy, qmv_narrow;
   int tile_wv, tile_nch, tile_kh;  // MLXQ_QMV_TILE=waves,chunks[,K parts]
   int tile_fused_rg;               // MLXQ_QMV_TILE_FUSED_RG=1: 16-row whole-K tiles only
   int stream64;                    // MLXQ_QMV_STREAM64=1 / 0: force / forbid the 64-row streaming form

@@ -197,25 +197,9 @@ int qmatmul_dispatch(const void* x, int64_t M, const uint32_t* wq, const void* s
   // below.  MLXQ_QMV_TILE_ALL=1 takes it for every eligible shape,
   // MLXQ_QMV_LEGACY=1 never.
   if (M <= kQmvMaxM && qmv_tile_eligible(M, N, K, group_size, bits) &&
-      (qmv_tile_preferred(M, N, K, bits) || ov.qmv_tile_all) && !ov.qmv_legacy && !ov.qmv_stream) {
+      (qmv_tile_preferred(M, N, K, bits) || ov.qmv_tile_all) && !ov.qmv_legacy) {
     rc = launch_qmv_tile(xp, M, wq, sp, bp, bias, N, K, group_size, bits, yp, workspace, workspace_bytes, st);
     if (rc != MLXQ_ERR_UNSUPPORTED) return rc;  // else: no split fits the workspace, use the block kernel
-  }
-
-  // MLXQ_QMV_STREAM=1: the streaming matrix-core kernel (the fused entry
-  // point's M > 4 form) for plain calls too; measured at parity or slower
-  // than the block kernel below for most plain shapes, so not the default
-  if (M <= kQmvMaxM && qmv_mfma_eligible(M, K, group_size, bits) && ov.qmv_stream) {
-    QmvFused f{};
-    f.x = xp;
-    f.M = M;
-    f.K = K;
-    f.x_stride = K;
-    f.nproj = 1;
-    f.proj[0] = QmvProj{wq, sp, bp, bias, nullptr, yp, N};
-    f.group_size = group_size;
-    f.bits = bits;
-    return launch_qmv_mfma(f, st);
   }
 
   // qmv in chunks of at most 32 activation rows (one launch for decode shapes)
@@ -332,7 +316,7 @@ extern "C" int mlxq_qmatmul_add_rms_norm(const void* x, int64_t M, const uint32_
   const uint16_t* res = static_cast<const uint16_t*>(residual);
   uint16_t* so = static_cast<uint16_t*>(sum_out);
   if (M > kQmvDotMaxM && M <= kQmvMaxM && qmv_tile_eligible(M, N, K, group_size, bits) &&
-      (qmv_tile_preferred(M, N, K, bits) || ov.qmv_tile_all) && !ov.qmv_legacy && !ov.qmv_stream &&
+      (qmv_tile_preferred(M, N, K, bits) || ov.qmv_tile_all) && !ov.qmv_legacy &&
       !ov.qmv_no_tile_fused && x && wq && scales && biases) {
     AddNormEpilogue ep{res, static_cast<const uint16_t*>(norm_weight), eps, so, static_cast<uint16_t*>(y), false};
     rc = launch_qmv_tile(static_cast<const uint16_t*>(x), M, wq, static_cast<const uint16_t*>(scales),
