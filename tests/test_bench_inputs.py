@@ -36,3 +36,40 @@ def test_gguf_blocks_match_oracle_quantizer(tname):
     # and the blocks decode to the values they came from
     y = orc.gguf_dequantize(tag, got, n)
     assert np.abs(y - x).max() <= 0.2 * np.abs(x).max()
+
+
+def test_profile_facts_follow_the_route(tmp_path, monkeypatch):
+    """bench.measured() reports a committed counter figure only while the call
+    runs the kernels it was measured on, and says why otherwise."""
+    bench = _bench()
+    (tmp_path / "a.md").write_text(
+        "text\n```json\n"
+        '[{"kind": "traffic_bytes", "bits": 4, "m": 1, "k": 4096, "n": 4096, "algo": "auto", '
+        '"route": "row::qmv_row_kernel<4, 2, 2, 4, 1, 0>", "value": 123}]\n```\n')
+    monkeypatch.setattr(bench, "PROFILES", tmp_path)
+    facts = bench.profile_facts()
+    assert facts[0]["file"] == "profiles/a.md"
+
+    class Lib:
+        ALGO_AUTO, ALGO_QMM, ALGO_QMM_LIB = 0, 2, 3
+        route = "row::qmv_row_kernel<4, 2, 2, 4, 1, 0>"
+
+        def qmatmul_route(self, m, n, k, gs, bits, algo=0):
+            return self.route
+
+    lib = Lib()
+    assert bench.measured(facts, lib, "traffic_bytes", 4, 1, 4096, 4096) == (123, "profiles/a.md")
+    lib.route = "row::qmv_row_kernel<4, 1, 2, 4, 1, 0>"
+    v, why = bench.measured(facts, lib, "traffic_bytes", 4, 1, 4096, 4096)
+    assert v is None and "now runs" in why
+    assert bench.measured(facts, lib, "mfma_busy", 4, 1, 4096, 4096) == (None, "not measured")
+
+
+def test_committed_profile_facts_parse():
+    """Every machine-readable block under profiles/ parses and names a route."""
+    bench = _bench()
+    facts = bench.profile_facts()
+    assert facts, "no facts committed"
+    for f in facts:
+        assert {"kind", "bits", "m", "k", "n", "route", "value"} <= set(f)
+        assert f["value"] > 0 and f["route"]
