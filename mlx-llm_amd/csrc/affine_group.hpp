@@ -17,15 +17,15 @@
 namespace mlxq {
 namespace {  // internal linkage: each including file has its own copy
 
-// Lane owns 8 consecutive elements v of a group of 8 * LPG; the LPG lanes of
-// the group (aligned, within one wavefront) reduce min/max with butterfly
-// shuffles.  Every lane of the group must call it.
-template <int BITS, int LPG>
-__device__ __forceinline__ void quantize_group8(const float (&v)[8], uint32_t (&codes)[8], float& scale,
+// Lane owns EPL consecutive elements v of a group of EPL * LPG; the LPG
+// lanes of the group (aligned, within one wavefront) reduce min/max with
+// butterfly shuffles.  Every lane of the group must call it.
+template <int BITS, int LPG, int EPL = 8>
+__device__ __forceinline__ void quantize_group8(const float (&v)[EPL], uint32_t (&codes)[EPL], float& scale,
                                                 float& bias) {
   float w_max = v[0], w_min = v[0];
 #pragma unroll
-  for (int i = 1; i < 8; i++) {
+  for (int i = 1; i < EPL; i++) {
     w_max = fmaxf(w_max, v[i]);
     w_min = fminf(w_min, v[i]);
   }
@@ -33,11 +33,13 @@ __device__ __forceinline__ void quantize_group8(const float (&v)[8], uint32_t (&
   // 16-lane row: LPG is 4, 8 or 16 and the lane index is group-aligned) with
   // DPP moves: quad swaps, then the other quad of 8 (lane i <-> 7 - i), then
   // the other 8 of 16 (i <-> 15 - i).  Exact for max/min in any order.
-  static_assert(LPG == 4 || LPG == 8 || LPG == 16, "lanes per group");
+  static_assert(LPG == 2 || LPG == 4 || LPG == 8 || LPG == 16, "lanes per group");
   w_max = fmaxf(w_max, dpp_f32<kDppQuadXor1>(w_max));
   w_min = fminf(w_min, dpp_f32<kDppQuadXor1>(w_min));
-  w_max = fmaxf(w_max, dpp_f32<kDppQuadXor2>(w_max));
-  w_min = fminf(w_min, dpp_f32<kDppQuadXor2>(w_min));
+  if constexpr (LPG >= 4) {
+    w_max = fmaxf(w_max, dpp_f32<kDppQuadXor2>(w_max));
+    w_min = fminf(w_min, dpp_f32<kDppQuadXor2>(w_min));
+  }
   if constexpr (LPG >= 8) {
     w_max = fmaxf(w_max, dpp_f32<kDppRowHalfMirror>(w_max));
     w_min = fminf(w_min, dpp_f32<kDppRowHalfMirror>(w_min));
@@ -68,7 +70,7 @@ __device__ __forceinline__ void quantize_group8(const float (&v)[8], uint32_t (&
   // the comparison is false) the exact division decides.
   const float rcp = __builtin_amdgcn_rcpf(scale);
 #pragma unroll
-  for (int i = 0; i < 8; i++) {
+  for (int i = 0; i < EPL; i++) {
     const float d = v[i] - bias;
     const float t = d * rcp;
     float q = __builtin_rintf(t);
@@ -76,6 +78,21 @@ __device__ __forceinline__ void quantize_group8(const float (&v)[8], uint32_t (&
     q = fminf(fmaxf(q, 0.f), n_bins);
     codes[i] = static_cast<uint32_t>(q);
   }
+}
+
+// Pack 16 codes LSB-first: two words (Q4) or four (Q8) at 16-code index
+// `lane` (8-byte stores).
+template <int BITS>
+__device__ __forceinline__ void store_codes16(uint32_t* wq, int64_t lane, const uint32_t (&codes)[16]) {
+  uint32_t w[BITS / 2];
+#pragma unroll
+  for (int j = 0; j < BITS / 2; j++) {
+    w[j] = 0;
+#pragma unroll
+    for (int i = 0; i < 32 / BITS; i++) w[j] |= codes[j * (32 / BITS) + i] << (BITS * i);
+  }
+#pragma unroll
+  for (int j = 0; j < BITS / 4; j++) reinterpret_cast<uint2*>(wq)[lane * (BITS / 4) + j] = uint2{w[2 * j], w[2 * j + 1]};
 }
 
 // Pack 8 codes LSB-first: one word (Q4) or two (Q8) at lane index `lane`.

@@ -64,8 +64,13 @@ __device__ __forceinline__ int source_row(int r, int perm_hd) {
 // A workgroup converts `rpw` consecutive output rows.  All of their source
 // rows' GGUF bytes are requested up front (direct global -> LDS loads when
 // 16-byte aligned, so the bytes in flight per CU are those of every resident
-// workgroup's rows), then every lane decodes 8 consecutive elements of a row
+// workgroup's rows), then every lane decodes 16 consecutive elements of a row
 // from LDS, rounds them to bf16 and quantizes its share of the group.
+// Each lane takes 16 elements (LPG lanes per group), so the per-block
+// header decode and the per-group scale arithmetic, which every lane of a
+// group repeats, are shared by twice as many elements as with 8.
+constexpr int kEpl = 16;
+
 template <int TAG, int BITS, int LPG, bool ALIGNED16>
 __global__ __launch_bounds__(kThreads) void gguf_requant_kernel(const uint8_t* __restrict__ data, int rows, int K,
                                                                  int row_bytes, int perm_hd, int rpw,
@@ -73,7 +78,7 @@ __global__ __launch_bounds__(kThreads) void gguf_requant_kernel(const uint8_t* _
                                                                  uint16_t* __restrict__ scales,
                                                                  uint16_t* __restrict__ biases) {
   extern __shared__ __align__(16) uint8_t lds[];
-  const int lpr = K / 8;  // lanes (8 elements each) per row
+  const int lpr = K / kEpl;  // lanes (kEpl elements each) per row
   const int r0 = blockIdx.x * rpw;
   const int nr = min(rpw, rows - r0);
   const int tid = threadIdx.x;
@@ -102,30 +107,31 @@ __global__ __launch_bounds__(kThreads) void gguf_requant_kernel(const uint8_t* _
     for (int l0 = 0; l0 < lpr; l0 += kThreads) {
       const int l = l0 + tid;
       const bool active = l < lpr;
-      float v[8];
+      float v[kEpl];
 #pragma unroll
-      for (int j = 0; j < 8; j++) v[j] = 0.f;
+      for (int j = 0; j < kEpl; j++) v[j] = 0.f;
       if (active) {
-        const int e = l * 8;
+        const int e = l * kEpl;
         if constexpr (is_float_tag<TAG>()) {
 #pragma unroll
-          for (int j = 0; j < 8; j++) v[j] = float_elem<TAG>(row, e + j);
+          for (int j = 0; j < kEpl; j++) v[j] = float_elem<TAG>(row, e + j);
         } else {
           constexpr int E = Geo<TAG>::E, B = Geo<TAG>::B;
+          static_assert(E % kEpl == 0, "a lane's elements never straddle a block");
           const int blk = e / E;
           const uint8_t* b = row + blk * B;
 #pragma unroll
-          for (int j = 0; j < 8; j++) v[j] = decode<TAG>(b, e - blk * E + j);  // 8 never straddle a block
+          for (int j = 0; j < kEpl; j++) v[j] = decode<TAG>(b, e - blk * E + j);
         }
 #pragma unroll
-        for (int j = 0; j < 8; j++) v[j] = static_cast<float>(static_cast<__bf16>(v[j]));  // as_dtype(bf16): v_cvt_pk_bf16_f32, round to nearest even (a NaN payload cannot reach a code: max/min skip NaN and a NaN quotient clamps to 0)
+        for (int j = 0; j < kEpl; j++) v[j] = static_cast<float>(static_cast<__bf16>(v[j]));  // as_dtype(bf16): v_cvt_pk_bf16_f32, round to nearest even (a NaN payload cannot reach a code: max/min skip NaN and a NaN quotient clamps to 0)
       }
-      uint32_t codes[8];
+      uint32_t codes[kEpl];
       float scale, bias;
-      quantize_group8<BITS, LPG>(v, codes, scale, bias);  // every lane of the group takes part
+      quantize_group8<BITS, LPG, kEpl>(v, codes, scale, bias);  // every lane of the group takes part
       if (active) {
         const int64_t lane = static_cast<int64_t>(r) * lpr + l;
-        store_codes8<BITS>(wq, lane, codes);
+        store_codes16<BITS>(wq, lane, codes);
         if ((l & (LPG - 1)) == 0) {
           const int64_t g = lane / LPG;
           scales[g] = static_cast<uint16_t>(f32_to_bf16_bits(scale));
@@ -162,9 +168,9 @@ int launch_lpg(int rows, int K, int row_bytes, int perm_hd, const uint8_t* d, ui
 template <int TAG, int BITS>
 int launch_bits(int group_size, int rows, int K, int row_bytes, int perm_hd, const uint8_t* d, uint32_t* wq,
                 uint16_t* s, uint16_t* b, hipStream_t st) {
-  if (group_size == 32) return launch_lpg<TAG, BITS, 4>(rows, K, row_bytes, perm_hd, d, wq, s, b, st);
-  if (group_size == 64) return launch_lpg<TAG, BITS, 8>(rows, K, row_bytes, perm_hd, d, wq, s, b, st);
-  return launch_lpg<TAG, BITS, 16>(rows, K, row_bytes, perm_hd, d, wq, s, b, st);
+  if (group_size == 32) return launch_lpg<TAG, BITS, 32 / kEpl>(rows, K, row_bytes, perm_hd, d, wq, s, b, st);
+  if (group_size == 64) return launch_lpg<TAG, BITS, 64 / kEpl>(rows, K, row_bytes, perm_hd, d, wq, s, b, st);
+  return launch_lpg<TAG, BITS, 128 / kEpl>(rows, K, row_bytes, perm_hd, d, wq, s, b, st);
 }
 
 template <int TAG>
