@@ -346,7 +346,11 @@ extern "C" int mlxq_qmatmul_route(int64_t M, int64_t N, int64_t K, int group_siz
   void* const p = reinterpret_cast<void*>(uintptr_t(1) << 20);
   const uint32_t* const wq = static_cast<const uint32_t*>(p);
   if (noalloc) {
+    if (int rc = check_shape(M, N, K, group_size, bits)) return rc;
     const size_t need = fused_workspace_bytes(M, N, K, group_size, bits);
+    if (need > mlxq_qmatmul_noalloc_max_scratch())  // the call itself refuses such shapes before any launch
+      return fail(MLXQ_ERR_WORKSPACE, "qmatmul_route: the no-alloc call refuses this shape (" + std::to_string(need) +
+                                          " bytes of scratch needed)");
     return run_route_query([&] { return qmatmul_dispatch(p, M, wq, p, p, nullptr, N, K, group_size, bits, p,
                                                          need ? p : nullptr, need, MLXQ_ALGO_AUTO, false, nullptr); },
                            buf, buf_len);

@@ -61,3 +61,12 @@ def test_noalloc_rejects_oversize_before_launch(torch_gpu):
     rc = mlxq.lib().mlxq_qmatmul_noalloc(None, 32, None, None, None, None, 128256, 4096, 64, 4, None, None)
     assert rc == mlxq.ERR_WORKSPACE
     assert b"scratch" in mlxq.lib().mlxq_last_error()
+
+
+def test_noalloc_route_query_refuses_what_the_call_refuses(torch_gpu):
+    """The route query of the no-alloc call refuses the shapes the call itself
+    refuses (scratch beyond the fixed array), and names the kernels otherwise."""
+    with pytest.raises(mlxq.MlxqError) as e:
+        mlxq.qmatmul_route(32, 128256, 4096, 64, 4, noalloc=True)
+    assert e.value.status == mlxq.ERR_WORKSPACE
+    assert mlxq.qmatmul_route(2048, 4096, 14336, 64, 4, noalloc=True).startswith("qmm_kernel<4, 64")
