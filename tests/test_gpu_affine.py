@@ -88,7 +88,7 @@ def test_llama_shapes_bit_exact(torch_gpu, shape, bits):
 
 
 @pytest.mark.parametrize("bits", [4, 8])
-@pytest.mark.parametrize("factor", [1.0, 0.02, 3.0e-5, 7.0])
+@pytest.mark.parametrize("factor", [1.0, 0.02, 3.0e-5, 7.0, 0.0123457, 3.3e-3, 1.7e-6, 0.7071068, 511.3, 9.9e-2])
 def test_codes_at_rounding_ties(torch_gpu, bits, factor):
     """Groups whose quotients (w - bias) / scale sit on or within a few ulps
     of half-integers: min 0 and max n_bins (times `factor`) make scale
