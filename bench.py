@@ -12,7 +12,8 @@ Extra fields (same JSON line):
   roofline      dominant kernel of the step, HIP-event timed per launch
   kernels       per (bits, M) decode GEMV GB/s and % of 8 TB/s
   prefill       config 3: qmatmul at M=2048, Q4, 4096->14336 and 14336->4096, TFLOP/s (default
-                route and the fused qmm kernel)
+                route, the hand-written qmm kernel, the library GEMM on bf16 weights)
+  prefill_roofline  the hand-written qmm kernel over both config-3 shapes, flat
   gguf          config 4: block dequant of a 14336x4096 tensor, GB/s per type
   decode_stack  config 5: quantized Llama-3-8B decode step, tokens/s at batch 1 and 16
   cpu_baseline  the CPU restatement (oracle, OpenMP) on a bounded sample
@@ -326,6 +327,18 @@ def main(argv=None) -> int:
 
     if not a.quick:
         out["prefill"] = bench_prefill(torch, mlxq, facts)
+        # the hand-written prefill kernel's roofline over config 3's two
+        # shapes (FLOPs of both / time of both), flat, beside the nested detail
+        hw = {k: v["hand_written_qmm"] for k, v in out["prefill"].items()}
+        fl = sum(h["roofline"]["flops_per_launch"] for h in hw.values())
+        us = sum(h["us"] for h in hw.values())
+        out["prefill_roofline"] = {
+            "kernel": " / ".join(f"{k}: {h['route']}" for k, h in hw.items()), "bound": "mfma",
+            "achieved": round(fl / (us * 1e-6) / 1e12, 1), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(fl / (us * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+            "us": {k: h["us"] for k, h in hw.items()}, "TFLOP/s": {k: h["TFLOP/s"] for k, h in hw.items()},
+            "mfma_busy_counter": {k: h["mfma_busy_counter"] for k, h in hw.items()},
+            "default_route_TFLOP/s": {k: v["TFLOP/s"] for k, v in out["prefill"].items()}}
         out["gguf"] = bench_gguf(torch, mlxq)
         out["decode_stack"] = bench_stack(torch)
     if not a.quick and not a.no_cpu_baseline:
