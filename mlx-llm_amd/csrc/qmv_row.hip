@@ -388,6 +388,10 @@ int launch_ni(RowParams& a, int64_t M, int R, int W, hipStream_t st) {
     if (R >= 2) return launch_rw<BITS, NI, 2, 4, 1, 0>(a, set_tiles(a, 2, 4, false), st);
     return launch_rw<BITS, NI, 1, 4, 1, 0>(a, set_tiles(a, 1, 4, false), st);
   } else {
+    if (R >= 2) {
+      if (W >= 8) return launch_rw<BITS, NI, 2, 8, 1, 0>(a, set_tiles(a, 2, 8, false), st);
+      return launch_rw<BITS, NI, 2, 4, 1, 0>(a, set_tiles(a, 2, 4, false), st);
+    }
     if (W >= 16) return launch_rw<BITS, NI, 1, 16, 1, 0>(a, set_tiles(a, 1, 16, false), st);
     if (W >= 8) return launch_rw<BITS, NI, 1, 8, 1, 0>(a, set_tiles(a, 1, 8, false), st);
     return launch_rw<BITS, NI, 1, 4, 1, 0>(a, set_tiles(a, 1, 4, false), st);
@@ -415,7 +419,8 @@ int launch_fused_r(RowParams& a, int R, hipStream_t st) {
 }
 template <int BITS, int F>
 int launch_fused_f(RowParams& a, int64_t ni, int R, hipStream_t st) {
-  if constexpr (BITS == 4 && F == 0) {  // the down projection (+ residual): 7 KB rows, 8 waves
+  if constexpr (BITS == 4 && F == 0) {  // the down projection (+ residual): 7 KB rows, 8 waves (in
+    // the batch-1 chain 2 rows x 4 waves, faster for the plain call, measured 0.4% slower per step)
     if (ni == 7) return launch_rw<4, 7, 1, 8, 1, 0>(a, set_tiles(a, 1, 8, false), st);
   }
   if (ni == 1) return launch_fused_r<BITS, 1, F>(a, R, st);
@@ -439,9 +444,9 @@ bool qmv_row_eligible(int64_t M, int64_t N, int64_t K, int group_size, int bits)
   if (M > 1 && K > 4096) return false;  // the activation rows share the workgroup's LDS
   if ((K * bits / 8) % 1024) return false;
   const int64_t ni = K * bits / 8 / 1024;
-  // Q4 with 7 KB rows (the down projection, K = 14336): 8 waves per
-  // workgroup share the 28 KB activation staging (9.92 -> 9.50 us against
-  // qmv_dot); 14 KB and longer Q4 rows stay on qmv_dot
+  // Q4 with 7 KB rows (the down projection, K = 14336) run here, faster
+  // than qmv_dot (9.92 -> 9.50 us at one row x 8 waves, less at two rows x
+  // 4 waves); 14 KB and longer Q4 rows stay on qmv_dot
   if (bits == 4 && ni >= 14 && !overrides().qmv_row_all) return false;
   return ni == 1 || ni == 2 || ni == 4 || ni == 7 || ni == 8 || ni == 14 || ni == 16;
 }
@@ -450,8 +455,11 @@ bool qmv_row_eligible(int64_t M, int64_t N, int64_t K, int group_size, int bits)
 // shapes (MLXQ_QMV_ROW_R / MLXQ_QMV_ROW_W override them).
 void qmv_row_geometry(int64_t N, int64_t K, int bits, int& R, int& W) {
   const int64_t ni = K * bits / 8 / 1024;
-  R = bits == 4 && ni <= 2 && N >= 4096 ? 2 : 1;  // Q4 q/o 4.96 vs 5.18 us, gate 9.72 vs 10.48; Q8 best at 1
-  W = bits == 4 && ni >= 7 ? 8 : 4;               // Q8 down: 14.2 us at 4 waves, 16.9 at 8; Q4 down 9.7 at 4, 9.5 at 8
+  // Q4 q/o 4.96 vs 5.18 us at 2 rows, gate 9.72 vs 10.48; Q4 down (7 KB rows)
+  // 10.06 us at 2 rows x 4 waves against 10.66 at 1 x 8 and 11.16 at 2 x 8
+  // (the two rows share each lane's activation reads from LDS); Q8 best at 1
+  R = bits == 4 && ((ni <= 2 && N >= 4096) || ni == 7) ? 2 : 1;
+  W = bits == 4 && ni >= 8 ? 8 : 4;  // Q8 down: 14.2 us at 4 waves, 16.9 at 8
   if (overrides().row_r) R = overrides().row_r;
   if (overrides().row_w) W = overrides().row_w;
 }
