@@ -419,8 +419,9 @@ int launch_fused_r(RowParams& a, int R, hipStream_t st) {
 }
 template <int BITS, int F>
 int launch_fused_f(RowParams& a, int64_t ni, int R, hipStream_t st) {
-  if constexpr (BITS == 4 && F == 0) {  // the down projection (+ residual): 7 KB rows, 8 waves (in
-    // the batch-1 chain 2 rows x 4 waves, faster for the plain call, measured 0.4% slower per step)
+  // the down projection (+ residual): 7 KB rows, one row x 8 waves (the plain
+  // call's 2 rows x 4 waves measured 0.4% slower per batch-1 decode step here)
+  if constexpr (BITS == 4 && F == 0) {
     if (ni == 7) return launch_rw<4, 7, 1, 8, 1, 0>(a, set_tiles(a, 1, 8, false), st);
   }
   if (ni == 1) return launch_fused_r<BITS, 1, F>(a, R, st);

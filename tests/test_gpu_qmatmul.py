@@ -311,7 +311,7 @@ ROW_K = {4: [2048, 4096, 8192, 14336], 8: [1024, 2048, 4096, 7168, 8192, 14336, 
 
 @pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("gs", [32, 64, 128])
-@pytest.mark.parametrize("geom", ["auto", "1,4", "2,4", "4,4", "1,8", "1,16"])
+@pytest.mark.parametrize("geom", ["auto", "1,4", "2,4", "4,4", "1,8", "2,8", "1,16"])
 def test_qmv_row_batch1(torch_gpu, monkeypatch, bits, gs, geom):
     """Batch-1 whole-row kernel (qmv_row.hip) at every row length it is
     built for (1..16 KB of codes), every forced (rows per wave, waves per
