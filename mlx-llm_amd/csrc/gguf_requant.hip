@@ -27,6 +27,7 @@ namespace mlxq {
 namespace {
 
 constexpr int kThreads = 256;
+constexpr int kEpl = 16;  // elements per lane
 
 // Element e of a float-typed GGUF tensor (F32 = 0, F16 = 1, BF16 = 30).
 template <int TAG>
@@ -61,15 +62,109 @@ __device__ __forceinline__ int source_row(int r, int perm_hd) {
   return h * perm_hd + 2 * (rr % half) + rr / half;
 }
 
+// The 16 consecutive elements j0 .. j0 + 15 (j0 a multiple of 16) of the
+// block at b (LDS), with the per-element arithmetic of decode<TAG> in the
+// same order (bit-identical), for the formats where one lane's 16 elements
+// share their bytes' layout: one nibble half of 16 consecutive bytes and one
+// scale.  decode<TAG> takes j at run time, so per element it re-derives the
+// half, the byte and (k-quants) the sub-block scale; here they are derived
+// once per lane and the bytes are read as whole 2- or 16-byte words.
+__device__ __forceinline__ uint32_t lds_u16(const uint8_t* p) { return *reinterpret_cast<const uint16_t*>(p); }
+
+template <int TAG>
+__device__ __forceinline__ void decode16(const uint8_t* b, int j0, float (&v)[kEpl]) {
+  if constexpr (TAG == 2 || TAG == 20) {
+    // Q4_0 / IQ4_NL: element j0 + k is nibble (j0 / 16) of byte 2 + k
+    const float d = rd_f16(b, 0);
+    const int sh = (j0 >> 2) & 4;
+#pragma unroll
+    for (int k = 0; k < 16; k += 2) {
+      const uint32_t w = lds_u16(b + 2 + k);
+      const uint32_t q0 = (w >> sh) & 0xFu, q1 = (w >> (sh + 8)) & 0xFu;
+      if constexpr (TAG == 2) {
+        v[k] = static_cast<float>(static_cast<int>(q0) - 8) * d;
+        v[k + 1] = static_cast<float>(static_cast<int>(q1) - 8) * d;
+      } else {
+        v[k] = d * static_cast<float>(iq4nl_value(q0));
+        v[k + 1] = d * static_cast<float>(iq4nl_value(q1));
+      }
+    }
+  } else if constexpr (TAG == 8) {
+    // Q8_0: element j0 + k is the signed byte 2 + j0 + k
+    const float d = rd_f16(b, 0);
+#pragma unroll
+    for (int k = 0; k < 16; k += 2) {
+      const uint32_t w = lds_u16(b + 2 + j0 + k);
+      v[k] = static_cast<float>(static_cast<int8_t>(w & 0xFFu)) * d;
+      v[k + 1] = static_cast<float>(static_cast<int8_t>(w >> 8)) * d;
+    }
+  } else if constexpr (TAG == 12) {
+    // Q4_K: sub-block 2c + hi; bytes 16 + 32c + (j0 & 31) .. +15 (16-byte aligned)
+    const int c = j0 >> 6, hi = (j0 >> 5) & 1;
+    uint32_t sc, m;
+    scale_min_k4(2 * c + hi, b + 4, sc, m);
+    const float d = rd_f16(b, 0), dmin = rd_f16(b, 2);
+    const float d1 = d * static_cast<float>(sc);
+    const float m1 = dmin * static_cast<float>(m);
+    const uint4 q = *reinterpret_cast<const uint4*>(b + 16 + 32 * c + (j0 & 31));
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+    const int sh = 4 * hi;
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+      const uint32_t nib = (w[k >> 2] >> (8 * (k & 3) + sh)) & 0xFu;
+      v[k] = d1 * static_cast<float>(nib) - m1;
+    }
+  } else if constexpr (TAG == 14) {
+    // Q6_K: 128-half idx, quarter t, bytes l = (j0 & 31) + k of ql (at 32 (t & 1),
+    // nibble t / 2) and qh (2-bit field t); one scale per 16 elements
+    const int idx = j0 >> 7, t = (j0 >> 5) & 3, l0 = j0 & 31;
+    const uint8_t* qlp = b + 64 * idx + 32 * (t & 1) + l0;
+    const uint8_t* qhp = b + 128 + 32 * idx + l0;
+    const int sc = static_cast<int8_t>(b[192 + 8 * idx + (l0 >> 4) + 2 * t]);
+    const float ds = rd_f16(b, 208) * static_cast<float>(sc);
+    const int shl = 4 * (t >> 1), shh = 2 * t;
+#pragma unroll
+    for (int k = 0; k < 16; k += 2) {
+      const uint32_t wl = lds_u16(qlp + k), wh = lds_u16(qhp + k);
+#pragma unroll
+      for (int e = 0; e < 2; e++) {
+        const uint32_t lo = (wl >> (8 * e + shl)) & 0xFu, hb = (wh >> (8 * e + shh)) & 3u;
+        const int q = static_cast<int>(static_cast<int8_t>(lo | (hb << 4))) - 32;
+        v[k + e] = ds * static_cast<float>(q);
+      }
+    }
+  } else if constexpr (TAG == 23) {
+    // IQ4_XS: sub-block ib, nibble (j0 / 16) & 1 of bytes 8 + 16 ib .. +15 (8-byte aligned)
+    const int ib = j0 >> 5;
+    const float d = rd_f16(b, 0);
+    const uint32_t shw = static_cast<uint32_t>(b[2]) | (static_cast<uint32_t>(b[3]) << 8);
+    const int ls = static_cast<int>((b[4 + (ib >> 1)] >> (4 * (ib & 1))) & 0xFu) |
+                   static_cast<int>(((shw >> (2 * ib)) & 3u) << 4);
+    const float dl = d * static_cast<float>(ls - 32);
+    const uint2 q0 = *reinterpret_cast<const uint2*>(b + 8 + 16 * ib);
+    const uint2 q1 = *reinterpret_cast<const uint2*>(b + 16 + 16 * ib);
+    const uint32_t w[4] = {q0.x, q0.y, q1.x, q1.y};
+    const int sh = (j0 >> 2) & 4;
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+      const uint32_t nib = (w[k >> 2] >> (8 * (k & 3) + sh)) & 0xFu;
+      v[k] = dl * static_cast<float>(iq4nl_value(nib));
+    }
+  }
+}
+template <int TAG>
+constexpr bool has_decode16() {
+  return TAG == 2 || TAG == 8 || TAG == 12 || TAG == 14 || TAG == 20 || TAG == 23;
+}
+
 // A workgroup converts `rpw` consecutive output rows.  All of their source
 // rows' GGUF bytes are requested up front (direct global -> LDS loads when
 // 16-byte aligned, so the bytes in flight per CU are those of every resident
 // workgroup's rows), then every lane decodes 16 consecutive elements of a row
 // from LDS, rounds them to bf16 and quantizes its share of the group.
-// Each lane takes 16 elements (LPG lanes per group), so the per-block
-// header decode and the per-group scale arithmetic, which every lane of a
-// group repeats, are shared by twice as many elements as with 8.
-constexpr int kEpl = 16;
+// Each lane takes kEpl = 16 elements (LPG lanes per group), so the
+// per-block header decode and the per-group scale arithmetic, which every
+// lane of a group repeats, are shared by twice as many elements as with 8.
 
 template <int TAG, int BITS, int LPG, bool ALIGNED16>
 __global__ __launch_bounds__(kThreads) void gguf_requant_kernel(const uint8_t* __restrict__ data, int rows, int K,
@@ -120,8 +215,12 @@ __global__ __launch_bounds__(kThreads) void gguf_requant_kernel(const uint8_t* _
           static_assert(E % kEpl == 0, "a lane's elements never straddle a block");
           const int blk = e / E;
           const uint8_t* b = row + blk * B;
+          if constexpr (has_decode16<TAG>()) {
+            decode16<TAG>(b, e - blk * E, v);
+          } else {
 #pragma unroll
-          for (int j = 0; j < kEpl; j++) v[j] = decode<TAG>(b, e - blk * E + j);
+            for (int j = 0; j < kEpl; j++) v[j] = decode<TAG>(b, e - blk * E + j);
+          }
         }
 #pragma unroll
         for (int j = 0; j < kEpl; j++) v[j] = static_cast<float>(static_cast<__bf16>(v[j]));  // as_dtype(bf16): v_cvt_pk_bf16_f32, round to nearest even (a NaN payload cannot reach a code: max/min skip NaN and a NaN quotient clamps to 0)
