@@ -62,19 +62,30 @@ __device__ __forceinline__ void quantize_group8(const float (&v)[EPL], uint32_t 
     bias = edge;
   }
 
-  // code = rint(fl((w - bias) / scale)).  Fast form: t = (w - bias) *
-  // rcp(scale) is within 3 ulps of the correctly rounded quotient (v_rcp_f32
-  // 1 ulp, the product 0.5, the quotient 0.5; below 2e-4 for |t| < 1024), so
-  // wherever t is 5e-4 or more away from a half-integer, rint(t) equals rint
-  // of the correctly rounded quotient.  Near a tie (and for NaN/inf, where
-  // the comparison is false) the exact division decides.
-  const float rcp = __builtin_amdgcn_rcpf(scale);
+  // code = rint(fl((w - bias) / scale)), fl the correctly rounded f32
+  // division.  The compiler's division of d by scale is v_div_scale (of
+  // both operands), v_rcp_f32, one Newton step of the reciprocal, the
+  // quotient and two residual corrections (the last through v_div_fmas),
+  // then v_div_fixup.  Where the operands need no scaling and the quotient
+  // no fixing (finite, |scale| in [2^-60, 2^60], |quotient| < 1024) the
+  // scalings are identities and v_div_fmas is a plain fma, so the same
+  // sequence without them gives the same bits; its reciprocal step depends
+  // on the scale only and is done once for the lane's elements.  Elsewhere
+  // (never for weights of ordinary magnitude) the division itself runs.
+  // A quotient below 1024 in magnitude but far smaller than the scale
+  // (|d| << |scale|) could still meet a scaled division; its code is 0
+  // either way (rint of a value far below 0.5).
+  const float r0 = __builtin_amdgcn_rcpf(scale);
+  const float r1 = fmaf(fmaf(-scale, r0, 1.0f), r0, r0);
+  const bool ordinary = fabsf(scale) >= 0x1p-60f && fabsf(scale) <= 0x1p60f;
 #pragma unroll
   for (int i = 0; i < EPL; i++) {
     const float d = v[i] - bias;
-    const float t = d * rcp;
-    float q = __builtin_rintf(t);
-    if (!(fabsf(t - q) < 0.4995f && fabsf(t) < 1024.f)) q = __builtin_rintf(d / scale);
+    const float q0 = d * r1;
+    const float q1 = fmaf(fmaf(-scale, q0, d), r1, q0);
+    const float q2 = fmaf(fmaf(-scale, q1, d), r1, q1);
+    float q = __builtin_rintf(q2);
+    if (!(ordinary && fabsf(q0) < 1024.f)) q = __builtin_rintf(d / scale);
     q = fminf(fmaxf(q, 0.f), n_bins);
     codes[i] = static_cast<uint32_t>(q);
   }

@@ -88,13 +88,16 @@ def test_llama_shapes_bit_exact(torch_gpu, shape, bits):
 
 
 @pytest.mark.parametrize("bits", [4, 8])
-@pytest.mark.parametrize("factor", [1.0, 0.02, 3.0e-5, 7.0, 0.0123457, 3.3e-3, 1.7e-6, 0.7071068, 511.3, 9.9e-2])
+@pytest.mark.parametrize("factor", [1.0, 0.02, 3.0e-5, 7.0, 0.0123457, 3.3e-3, 1.7e-6, 0.7071068, 511.3, 9.9e-2,
+                                    3.1e20, 2.0e30])
 def test_codes_at_rounding_ties(torch_gpu, bits, factor):
     """Groups whose quotients (w - bias) / scale sit on or within a few ulps
     of half-integers: min 0 and max n_bins (times `factor`) make scale
     -factor and bias max, so every element j + 1/2 (times `factor`) lands on a
     tie of the code rounding; with factor not a power of two the f32 products
-    put the quotients a few ulps to either side of it."""
+    put the quotients a few ulps to either side of it.  The two largest
+    factors give scales above 2^60, where the quantizer takes the division
+    instead of its unscaled form of it."""
     rng = np.random.default_rng(77 + bits)
     n_bins = (1 << bits) - 1
     gs, rows, cols = 64, 64, 512
