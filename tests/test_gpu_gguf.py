@@ -61,6 +61,19 @@ def test_random_blocks_bit_exact(torch_gpu, tag):
     assert np.array_equal(got_bf16, orc.f32_to_bf16(ref))
 
 
+@pytest.mark.parametrize("tag", DEVICE_TAGS)
+def test_ragged_chunk_past_its_first_half(torch_gpu, tag):
+    """A last chunk of 1280 elements: the f32 kernels that store a chunk as
+    two 1 KB halves (elements tid*4.. and 1024 + tid*4..) write all of the
+    first half and part of the second."""
+    e = orc.gguf_block(tag)[0]
+    data, n = random_blocks(tag, 3 * 2048 // e + 1280 // e)
+    ref = orc.gguf_dequantize(tag, data, n)
+    got = gpu_dequant(tag, data, n)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    assert np.array_equal(gpu_dequant(tag, data, n, torch_gpu.bfloat16), orc.f32_to_bf16(ref))
+
+
 @pytest.mark.parametrize("tag", [2, 12, 14, 23])
 def test_unaligned_input_pointer(torch_gpu, tag):
     data, n = random_blocks(tag, 40)
