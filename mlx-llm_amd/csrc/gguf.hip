@@ -69,14 +69,29 @@ __device__ __forceinline__ void lds_dma16(const uint8_t* g, uint8_t* l) {
   __builtin_amdgcn_global_load_lds(g, l, 16, 0, 0);
 }
 
-// f32 output in two 1 KB halves per store pass, for the formats whose
-// per-element decode does not depend on decoding 8 neighbours together
-// (measured, µs for a 14336 x 4096 tensor: Q4_0 53.3 -> 47.6, Q8_0 61 ->
-// 51.7, Q6_K 56.5 -> 49.6, IQ4_NL 52 -> 47.4, IQ4_XS 52 -> 48; Q4_K 56 ->
-// 71.5, so the k-quants with packed sub-block scales keep 8 consecutive)
+// f32 output in two 1 KB halves per store pass (measured, µs for a 14336 x
+// 4096 tensor: Q4_0 53.3 -> 47.6, Q8_0 61 -> 51.7, Q6_K 56.5 -> 49.6,
+// IQ4_NL 52 -> 47.4, IQ4_XS 52 -> 48; Q4_K with its 4-element run decoder
+// 58 -> 48); the other formats keep 8 consecutive elements per thread
 template <int TAG>
 constexpr bool f32_halves() {
-  return TAG == 2 || TAG == 8 || TAG == 14 || TAG == 20 || TAG == 23;
+  return TAG == 2 || TAG == 8 || TAG == 12 || TAG == 14 || TAG == 20 || TAG == 23;
+}
+
+// Q4_K elements j .. j + 3 (j a multiple of 4: one sub-block, one nibble
+// half) with decode<12>'s arithmetic in its order: the sub-block's scale and
+// min and the block's d, dmin derived once for the four
+__device__ __forceinline__ void q4k_run4(const uint8_t* b, int j, float* v) {
+  const int c = j >> 6, hi = (j >> 5) & 1, l = j & 31;
+  uint32_t sc, m;
+  scale_min_k4(2 * c + hi, b + 4, sc, m);
+  const float d = rd_f16(b, 0), dmin = rd_f16(b, 2);
+  const float d1 = d * static_cast<float>(sc);
+  const float m1 = dmin * static_cast<float>(m);
+  const uint32_t w = *reinterpret_cast<const uint32_t*>(b + 16 + 32 * c + l);  // 4-byte aligned
+  const int sh = 4 * hi;
+#pragma unroll
+  for (int i = 0; i < 4; i++) v[i] = d1 * static_cast<float>((w >> (8 * i + sh)) & 0xFu) - m1;
 }
 
 template <int TAG, bool BF16OUT, bool ALIGNED16>
@@ -126,9 +141,14 @@ __global__ __launch_bounds__(kThreads) void gguf_dequant_kernel(const uint8_t* _
       if (e0 >= nb * E) return;  // the second half lies beyond the first
       float v[kVec];
 #pragma unroll
-      for (int i = 0; i < kVec; i++) {
-        const int e = e0 + (i >> 2) * (kThreads * 4) + (i & 3);
-        v[i] = decode<TAG>(lds + (e / E) * B, e % E);
+      for (int h = 0; h < 2; h++) {
+        const int e = e0 + h * (kThreads * 4);
+        if constexpr (TAG == 12) {
+          q4k_run4(lds + (e / E) * B, e % E, v + 4 * h);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; i++) v[4 * h + i] = decode<TAG>(lds + ((e + i) / E) * B, (e + i) % E);
+        }
       }
       f32x4* o = reinterpret_cast<f32x4*>(static_cast<float*>(out) + static_cast<int64_t>(blockIdx.x) * kCpw * kChunkElems + e0);
       __builtin_nontemporal_store(f32x4{v[0], v[1], v[2], v[3]}, o);
