@@ -78,20 +78,29 @@ constexpr bool f32_halves() {
   return TAG == 2 || TAG == 8 || TAG == 12 || TAG == 14 || TAG == 20 || TAG == 23;
 }
 
-// Q4_K elements j .. j + 3 (j a multiple of 4: one sub-block, one nibble
-// half) with decode<12>'s arithmetic in its order: the sub-block's scale and
-// min and the block's d, dmin derived once for the four
-__device__ __forceinline__ void q4k_run4(const uint8_t* b, int j, float* v) {
+// Q4_K elements j .. j + N - 1 (one sub-block, one nibble half) with
+// decode<12>'s arithmetic in its order: the sub-block's scale and min and
+// the block's d, dmin derived once for the run
+// (N = 4 or 8: j a multiple of N; the run's bytes are N-byte aligned)
+template <int N>
+__device__ __forceinline__ void q4k_run(const uint8_t* b, int j, float* v) {
   const int c = j >> 6, hi = (j >> 5) & 1, l = j & 31;
   uint32_t sc, m;
   scale_min_k4(2 * c + hi, b + 4, sc, m);
   const float d = rd_f16(b, 0), dmin = rd_f16(b, 2);
   const float d1 = d * static_cast<float>(sc);
   const float m1 = dmin * static_cast<float>(m);
-  const uint32_t w = *reinterpret_cast<const uint32_t*>(b + 16 + 32 * c + l);  // 4-byte aligned
+  uint32_t w[N / 4];
+  if constexpr (N == 8) {
+    const uint2 q = *reinterpret_cast<const uint2*>(b + 16 + 32 * c + l);
+    w[0] = q.x;
+    w[1] = q.y;
+  } else {
+    w[0] = *reinterpret_cast<const uint32_t*>(b + 16 + 32 * c + l);
+  }
   const int sh = 4 * hi;
 #pragma unroll
-  for (int i = 0; i < 4; i++) v[i] = d1 * static_cast<float>((w >> (8 * i + sh)) & 0xFu) - m1;
+  for (int i = 0; i < N; i++) v[i] = d1 * static_cast<float>((w[i >> 2] >> (8 * (i & 3) + sh)) & 0xFu) - m1;
 }
 
 template <int TAG, bool BF16OUT, bool ALIGNED16>
@@ -144,7 +153,7 @@ __global__ __launch_bounds__(kThreads) void gguf_dequant_kernel(const uint8_t* _
       for (int h = 0; h < 2; h++) {
         const int e = e0 + h * (kThreads * 4);
         if constexpr (TAG == 12) {
-          q4k_run4(lds + (e / E) * B, e % E, v + 4 * h);
+          q4k_run<4>(lds + (e / E) * B, e % E, v + 4 * h);
         } else {
 #pragma unroll
           for (int i = 0; i < 4; i++) v[4 * h + i] = decode<TAG>(lds + ((e + i) / E) * B, (e + i) % E);
@@ -157,10 +166,14 @@ __global__ __launch_bounds__(kThreads) void gguf_dequant_kernel(const uint8_t* _
       const int e0 = c * kChunkElems + tid * kVec;  // element within the workgroup
       if (e0 >= nb * E) return;
       float v[kVec];
+      if constexpr (TAG == 12) {
+        q4k_run<8>(lds + (e0 / E) * B, e0 % E, v);
+      } else {
 #pragma unroll
-      for (int i = 0; i < kVec; i++) {
-        const int e = e0 + i;
-        v[i] = decode<TAG>(lds + (e / E) * B, e % E);
+        for (int i = 0; i < kVec; i++) {
+          const int e = e0 + i;
+          v[i] = decode<TAG>(lds + (e / E) * B, e % E);
+        }
       }
       store_vec<BF16OUT>(out, static_cast<int64_t>(blockIdx.x) * kCpw * kChunkElems + e0, v);
     }
