@@ -475,10 +475,12 @@ bool qmv_row_eligible(int64_t M, int64_t N, int64_t K, int group_size, int bits)
 // shapes (MLXQ_QMV_ROW_R / MLXQ_QMV_ROW_W override them).
 void qmv_row_geometry(int64_t N, int64_t K, int bits, int& R, int& W) {
   const int64_t ni = K * bits / 8 / 1024;
-  // Q4 q/o 4.96 vs 5.18 us at 2 rows, gate 9.72 vs 10.48; Q4 down (7 KB rows)
-  // 10.06 us at 2 rows x 4 waves against 10.66 at 1 x 8 and 11.16 at 2 x 8
-  // (the two rows share each lane's activation reads from LDS); Q8 best at 1
-  R = bits == 4 && ((ni <= 2 && N >= 4096) || ni == 7) ? 2 : 1;
+  // Q4 gate 9.72 vs 10.48 us at 2 rows (with the non-temporal loads 8.4-8.8
+  // either way); q/o 4.10 at 1 row vs 4.28 at 2 (it was 4.96 vs 5.18 the
+  // other way before the non-temporal loads); Q4 down (7 KB rows) 10.06 us at
+  // 2 rows x 4 waves against 10.66 at 1 x 8 and 11.16 at 2 x 8 (the two rows
+  // share each lane's activation reads from LDS); Q8 best at 1
+  R = bits == 4 && ((ni <= 2 && N > 8192) || ni == 7) ? 2 : 1;
   W = bits == 4 && ni >= 8 ? 8 : 4;  // Q8 down: 14.2 us at 4 waves, 16.9 at 8
   if (overrides().row_r) R = overrides().row_r;
   if (overrides().row_w) W = overrides().row_w;
