@@ -78,16 +78,23 @@ __device__ __forceinline__ void quantize_group8(const float (&v)[EPL], uint32_t 
   const float r0 = __builtin_amdgcn_rcpf(scale);
   const float r1 = fmaf(fmaf(-scale, r0, 1.0f), r0, r0);
   const bool ordinary = fabsf(scale) >= 0x1p-60f && fabsf(scale) <= 0x1p60f;
+  bool any_other = !ordinary;  // one test for the lane's elements, one branch
 #pragma unroll
   for (int i = 0; i < EPL; i++) {
     const float d = v[i] - bias;
     const float q0 = d * r1;
     const float q1 = fmaf(fmaf(-scale, q0, d), r1, q0);
     const float q2 = fmaf(fmaf(-scale, q1, d), r1, q1);
-    float q = __builtin_rintf(q2);
-    if (!(ordinary && fabsf(q0) < 1024.f)) q = __builtin_rintf(d / scale);
-    q = fminf(fmaxf(q, 0.f), n_bins);
-    codes[i] = static_cast<uint32_t>(q);
+    any_other |= !(fabsf(q0) < 1024.f);
+    codes[i] = static_cast<uint32_t>(fminf(fmaxf(__builtin_rintf(q2), 0.f), n_bins));
+  }
+  if (any_other) {
+#pragma unroll
+    for (int i = 0; i < EPL; i++) {
+      const float d = v[i] - bias;
+      if (!(ordinary && fabsf(d * r1) < 1024.f))
+        codes[i] = static_cast<uint32_t>(fminf(fmaxf(__builtin_rintf(d / scale), 0.f), n_bins));
+    }
   }
 }
 
